@@ -1,0 +1,172 @@
+/*
+ * gdn_mi355x.h -- C ABI of the MI355X (gfx950) Gated DeltaNet layer path.
+ *
+ * One extern "C" entry point per kernel of the GDN path of nano-vllm-extend's
+ * Qwen3.5 hybrid model.  Each entry point names the reference function it
+ * replaces (paths relative to the reference repository root).
+ *
+ * Conventions (all entry points):
+ *  - Every pointer is a device pointer.  bf16 tensors are passed as raw 16-bit
+ *    words (`uint16_t`), fp32 as `float`, slot ids as int64 (torch.long).
+ *  - Strides are in elements, not bytes.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Launches are
+ *    asynchronous; nothing synchronises, allocates or keeps global state, so
+ *    every entry point is safe under HIP-graph capture and reentrant.
+ *  - Outputs are caller-allocated.  State pools are mutated in place where
+ *    stated, exactly as the reference kernels mutate them.
+ *  - Return value: 0 on success, GDN_ERR_* (< 0) for rejected arguments,
+ *    or a positive hipError_t from the launch.
+ */
+#ifndef GDN_MI355X_H
+#define GDN_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_ABI_VERSION 1
+
+#define GDN_OK 0
+#define GDN_ERR_INVALID_ARG (-1) /* shape / stride / pointer rejected */
+#define GDN_ERR_UNSUPPORTED (-2) /* valid but not built (e.g. head dim) */
+
+/* ABI version of the loaded library (GDN_ABI_VERSION). */
+int gdn_abi_version(void);
+
+/*
+ * Fused gate/beta.  Replaces fused_g_beta / _gdn_g_beta_kernel
+ * (nanovllm/models/qwen3_5.py:320-360) and its eager chain (:936-937, :982-992).
+ *   g[i]    = -exp(A_log[h]) * softplus(a[i] + dt_bias[h])   (fp32, softplus
+ *             threshold 20: z > 20 ? z : log(1 + exp(z)))
+ *   beta[i] = sigmoid(b[i])                                 (bf16)
+ * with h = i % Hv, i in [0, total).  If mask != NULL, g = 0 on rows
+ * (i / Hv) whose mask byte is 0 (padding rows).
+ * a, b: bf16 [total]; A_log, dt_bias: [Hv] in bf16 (param_is_fp32 = 0) or fp32 (1).
+ */
+int gdn_g_beta(const uint16_t* b, const uint16_t* a, const void* A_log, const void* dt_bias,
+               int param_is_fp32, const uint8_t* mask, float* g, uint16_t* beta, int64_t total,
+               int Hv, void* stream);
+
+/*
+ * Varlen causal depthwise conv1d + SiLU with in-place conv-state roll.
+ * Replaces causal_conv_silu_varlen / _causal_conv_silu_varlen_kernel
+ * (nanovllm/models/qwen3_5.py:402-473).
+ *   x      [N, C] bf16, row stride sx_row, channel stride 1 (packed varlen rows)
+ *   state  conv state of sequence r at state + row(r)*ss_seq + c*ss_ch + j,
+ *          j in [0, K-1), row(r) = ids ? ids[r] : r.  Read as the K-1 left
+ *          padding, then overwritten with the row's last K-1 raw inputs
+ *          (old state entries when the row has fewer than K-1 tokens).
+ *   w      [C, K] bf16 contiguous
+ *   y      q / k / v parts: y[0 : N*key_dim) = [N, key_dim], then
+ *          [N, key_dim], then [N, C - 2*key_dim].  With C == 3*key_dim this is
+ *          the reference's [3, N, C/3] layout.
+ *   lens, cu_start: int32 [n_seqs] (tokens and first packed row per sequence).
+ */
+int gdn_conv_varlen(const uint16_t* x, int64_t sx_row, uint16_t* state, int64_t ss_seq,
+                    int64_t ss_ch, const int64_t* ids, const uint16_t* w, uint16_t* y,
+                    int key_dim, const int32_t* lens, const int32_t* cu_start, int n_seqs,
+                    int64_t N, int C, int K, void* stream);
+
+/*
+ * Single-token conv + SiLU with in-place state roll in the slot pool.
+ * Replaces conv_decode_step / _conv_decode_step_kernel
+ * (nanovllm/models/qwen3_5.py:515-558).
+ *   y[b, c] = silu(x[b,c]*w[c,K-1] + sum_{i<K-1} s[i]*w[c,i]),  s = pool row ids[b]
+ *   then s[i] <- s[i+1], s[K-2] <- x[b,c]   (pure bit copies)
+ * x: [B, C] bf16 row stride sx_row; pool slot stride sp_slot, channel stride sp_ch,
+ * state entries contiguous; y: [B, C] row stride sy_row.  Duplicate ids (the
+ * CUDA-graph dummy slot) are tolerated: they race only on that slot.
+ */
+int gdn_conv_decode(const uint16_t* x, int64_t sx_row, uint16_t* pool, int64_t sp_slot,
+                    int64_t sp_ch, const int64_t* ids, const uint16_t* w, uint16_t* y,
+                    int64_t sy_row, int B, int C, int K, void* stream);
+
+/*
+ * Padded-batch conv + SiLU with per-row state writeback.
+ * Replaces causal_conv_silu / _causal_conv_silu_kernel
+ * (nanovllm/models/qwen3_5.py:249-317).
+ *   x [n, C, T] with arbitrary strides; state [n, C, K-1] (strides ss_n, ss_c,
+ *   entries contiguous); y [n, C, T] contiguous.  endp[r] in [-1, T]: the
+ *   row's new state is its K-1 inputs before position endp[r]; -1 skips it.
+ */
+int gdn_conv_padded(const uint16_t* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
+                    uint16_t* state, int64_t ss_n, int64_t ss_c, const uint16_t* w,
+                    uint16_t* y, const int32_t* endp, int n, int C, int T, int K,
+                    void* stream);
+
+/*
+ * Chunked gated delta rule over packed varlen sequences (chunk size 64).
+ * Replaces the fla chunk_gated_delta_rule call (nanovllm/models/qwen3_5.py:956-960,
+ * semantics of the torch port _torch_chunk_gated_delta_rule :152-227).
+ *   q, k  [N, Hk, D] bf16, token strides sq_tok / sk_tok, head stride D
+ *   v     [N, Hv, D] bf16, token stride sv_tok, head stride D
+ *   g     [N, Hv] fp32 contiguous; beta [N, Hv] bf16 contiguous
+ *   value head h reads key head h / (Hv / Hk)   (grouped-value layout)
+ *   cu_seqlens int64 [n_seqs + 1] (device)
+ *   h0    initial state of sequence r at h0 + row(r)*state_stride, [Hv, D, D]
+ *         fp32 dense; NULL = zero state.  hT likewise receives the final
+ *         state (NULL = not written); row(r) = state_ids ? state_ids[r] : r.
+ *         h0 == hT (in-place update of a slot pool) is allowed.
+ *   o     [N, Hv, D] bf16 contiguous
+ *   l2norm != 0: q, k rows are L2-normalised in fp32 (eps 1e-6) first.
+ * D must be 64 or 128.
+ */
+int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k, int64_t sk_tok,
+                      const uint16_t* v, int64_t sv_tok, const float* g, const uint16_t* beta,
+                      const float* h0, float* hT, const int64_t* state_ids, int64_t state_stride,
+                      const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv, int D,
+                      float scale, int l2norm, uint16_t* o, void* stream);
+
+/*
+ * Recurrent gated delta rule for decode: T >= 1 tokens per sequence, state
+ * read once and written once.  Replaces recurrent_gdn_inplace /
+ * _recurrent_inplace_kernel (nanovllm/models/qwen3_5.py:561-613, T = 1, in
+ * place) and recurrent_gated_delta_rule -> fla fused_recurrent /
+ * _torch_recurrent_gated_delta_rule (:230-238, :616-651, gathered state).
+ * Per token: q,k L2-normalised (eps 1e-6), q *= scale, S *= exp(g),
+ * delta = beta*(v - S^T k), S += k delta^T, o = S^T q.
+ *   q, k  [B, T, Hk, D] bf16 with batch strides sq_b/sk_b and token strides
+ *         sq_t/sk_t (head stride D); v [B, T, Hv, D] likewise
+ *   g [B, T, Hv] fp32, beta [B, T, Hv] bf16, contiguous
+ *   s_in  state of sequence b at s_in + row(b)*s_in_stride ([Hv, D, D] dense)
+ *   s_out final state written at s_out + row(b)*s_out_stride (may equal s_in:
+ *         in-place pool update); NULL = not written
+ *   row(b) = ids ? ids[b] : b
+ *   inter [B, T, Hv, D, D] fp32 per-token states (NULL = not written)
+ *   o     [B, T, Hv, D] bf16 contiguous
+ * Duplicate ids (dummy slot) are tolerated.  D must be 64 or 128.
+ */
+int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k,
+                  int64_t sk_b, int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t,
+                  const float* g, const uint16_t* beta, const float* s_in, int64_t s_in_stride,
+                  float* s_out, int64_t s_out_stride, const int64_t* ids, float* inter,
+                  uint16_t* o, int B, int T, int Hk, int Hv, int D, float scale, int l2norm,
+                  void* stream);
+
+/*
+ * Speculative-verify commit: pool[ids[b]] <- inter[b, accepted[b] - 1]
+ * (accepted[b] in [1, T]; 0 leaves the slot untouched).  No counterpart in
+ * the reference (spec decode is disabled for qwen3_5, nanovllm/config.py:84);
+ * it consumes the per-token state format of gdn_recurrent.
+ */
+int gdn_state_commit(float* pool, int64_t slot_stride, const int64_t* ids, const float* inter,
+                     const int32_t* accepted, int B, int T, int Hv, int D, void* stream);
+
+/*
+ * Gated RMSNorm on the value head dim.  Replaces Qwen3_5RMSNormGated /
+ * _rms_gated_forward (nanovllm/models/qwen3_5.py:121-131, :697-709):
+ *   y = bf16( float(bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))) * silu(float(z)) )
+ * x, z: [n_tok, H, D] bf16 with token strides sx_tok / sz_tok (head stride D);
+ * w [D] bf16; y [n_tok, H, D] contiguous.
+ */
+int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16_t* z, int64_t sz_tok,
+                      const uint16_t* w, uint16_t* y, int64_t n_tok, int H, int D, float eps,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_MI355X_H */

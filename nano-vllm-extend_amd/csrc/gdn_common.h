@@ -1,0 +1,78 @@
+// Shared device helpers for the gfx950 GDN kernels: bf16 bit conversions,
+// MFMA fragment types, wave reductions, XCD-aware block remapping and the
+// launch-status plumbing used by every extern "C" entry point.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gdn_mi355x.h"
+
+namespace gdn {
+
+// ---- bf16 <-> fp32 (bit exact with torch: round-to-nearest-even, quiet NaN) ----
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// hi/lo split of an fp32 value into two bf16 terms: x ~= hi + lo with
+// |x - hi - lo| <= 2^-16 |x|.  Used to run fp32-accurate products on the
+// bf16 matrix cores (two or three MFMA passes).
+__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+  hi = f2bf(x);
+  lo = f2bf(x - bf2f(hi));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// ---- MFMA fragment types (v_mfma_f32_16x16x32_bf16) ----
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma16x16x32(const s16x8_t& a, const s16x8_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// fp32 matrix-core product, 16x16x4: A lane l = A[l&15][l>>4], B lane l = B[l>>4][l&15].
+__device__ __forceinline__ f32x4_t mfma16x16x4f32(float a, float b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---- wave-level reductions (wave64) ----
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// ---- XCD-aware block remap ----
+// Workgroups are dispatched round-robin over the 8 XCDs (block b lands on XCD
+// b % 8).  Remapping gives each XCD a contiguous range of work items, so the
+// blocks that share operands (e.g. the v-blocks of one head) share one L2.
+// Launch with grid = 8 * ceil(total / 8); returns -1 for padding blocks.
+__device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t total) {
+  const int64_t per = (total + 7) / 8;
+  const int64_t w = (b % 8) * per + b / 8;
+  return w < total ? w : -1;
+}
+
+constexpr int kNumXcd = 8;
+
+}  // namespace gdn
+
+// Status of the last launch on this thread, as an entry-point return code.
+static inline int gdn_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GDN_OK : static_cast<int>(e);
+}

@@ -1,0 +1,247 @@
+// Recurrent gated delta rule for decode (T >= 1 tokens per sequence) against
+// a slot-indexed fp32 state pool, plus the speculative-verify state commit.
+//
+// Math per token (nanovllm/models/qwen3_5.py:575-594, :616-651):
+//   q, k L2-normalised in fp32 (eps 1e-6), q *= scale
+//   S <- S * exp(g);  kv = S^T k;  delta = beta * (v - kv);  S <- S + k delta^T
+//   o = S^T q  =  (S*exp(g))^T q + delta * (k . q)
+// The last identity lets one cross-wave reduction pass produce both kv and o.
+//
+// HBM-bound: the D x D fp32 state tile of each (sequence, head) is read once
+// into registers and written once (plus optional per-token states).  One
+// workgroup of 256 threads owns a (sequence, head, v-block) tile of D x VB
+// columns, VB = D / NVB; each thread holds float4 column groups of NP rows so
+// every wave access is a contiguous run of VB*4 bytes per row.
+#include "gdn_common.h"
+
+namespace {
+
+template <int D, int NVB>
+__global__ __launch_bounds__(256) void recurrent_kernel(
+    const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, const uint16_t* __restrict__ k,
+    int64_t sk_b, int64_t sk_t, const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t,
+    const float* __restrict__ g, const uint16_t* __restrict__ beta, const float* s_in,
+    int64_t s_in_stride, float* s_out, int64_t s_out_stride, const int64_t* __restrict__ ids,
+    float* __restrict__ inter, uint16_t* __restrict__ o, int B, int T, int Hk, int Hv,
+    float scale, int l2norm) {
+  constexpr int VB = D / NVB;     // state columns per workgroup
+  constexpr int CPR = VB / 4;     // float4 column groups per row
+  constexpr int RPP = 256 / CPR;  // rows per pass of the workgroup
+  constexpr int NP = D / RPP;     // passes (float4 registers per thread)
+  static_assert(CPR <= 64 && 64 % CPR == 0 && NP >= 1, "tile shape");
+
+  __shared__ float sq[2][D];
+  __shared__ float sk[2][D];
+  __shared__ float skq[2];
+  __shared__ float red[2][4][2][VB];
+
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(B) * Hv * NVB);
+  if (wi < 0) return;
+  const int vb = static_cast<int>(wi % NVB);
+  const int h = static_cast<int>((wi / NVB) % Hv);
+  const int b = static_cast<int>(wi / (static_cast<int64_t>(NVB) * Hv));
+  const int kh = h / (Hv / Hk);
+  const int tid = threadIdx.x;
+  const int c4 = tid % CPR;
+  const int r0 = tid / CPR;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int col = vb * VB + c4 * 4;
+
+  const int64_t row = ids ? ids[b] : b;
+  const float* sin = s_in + row * s_in_stride + static_cast<int64_t>(h) * D * D + col;
+  float4 S[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j)
+    S[j] = *reinterpret_cast<const float4*>(sin + static_cast<int64_t>(r0 + RPP * j) * D);
+
+  for (int t = 0; t < T; ++t) {
+    const int buf = t & 1;
+    // --- q, k of this token: wave 0 normalises and publishes them ---
+    if (wave == 0) {
+      constexpr int E = D / 64;
+      const uint16_t* qp = q + static_cast<int64_t>(b) * sq_b + static_cast<int64_t>(t) * sq_t + static_cast<int64_t>(kh) * D;
+      const uint16_t* kp = k + static_cast<int64_t>(b) * sk_b + static_cast<int64_t>(t) * sk_t + static_cast<int64_t>(kh) * D;
+      float qf[E], kf[E];
+      float qq = 0.f, kk = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        qf[e] = gdn::bf2f(qp[lane * E + e]);
+        kf[e] = gdn::bf2f(kp[lane * E + e]);
+        qq += qf[e] * qf[e];
+        kk += kf[e] * kf[e];
+      }
+      qq = gdn::wave_sum(qq);
+      kk = gdn::wave_sum(kk);
+      const float rq = l2norm ? rsqrtf(qq + 1e-6f) : 1.0f;
+      const float rk = l2norm ? rsqrtf(kk + 1e-6f) : 1.0f;
+      float kq = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float qn = (qf[e] * rq) * scale;
+        const float kn = kf[e] * rk;
+        sq[buf][lane * E + e] = qn;
+        sk[buf][lane * E + e] = kn;
+        kq += qn * kn;
+      }
+      kq = gdn::wave_sum(kq);
+      if (lane == 0) skq[buf] = kq;
+    }
+    const int64_t gi = (static_cast<int64_t>(b) * T + t) * Hv + h;
+    const float eg = expf(g[gi]);
+    const float bt = gdn::bf2f(beta[gi]);
+    float vv[4];
+    {
+      const uint16_t* vp = v + static_cast<int64_t>(b) * sv_b + static_cast<int64_t>(t) * sv_t + static_cast<int64_t>(h) * D + col;
+      const uint2 u = *reinterpret_cast<const uint2*>(vp);
+      const uint16_t* us = reinterpret_cast<const uint16_t*>(&u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vv[i] = gdn::bf2f(us[i]);
+    }
+    __syncthreads();
+
+    // --- decay, then partial S^T k and S^T q over this thread's rows ---
+    float kv[4] = {0.f, 0.f, 0.f, 0.f}, qv[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const float kr = sk[buf][r0 + RPP * j];
+      const float qr = sq[buf][r0 + RPP * j];
+      S[j].x *= eg; S[j].y *= eg; S[j].z *= eg; S[j].w *= eg;
+      kv[0] += S[j].x * kr; kv[1] += S[j].y * kr; kv[2] += S[j].z * kr; kv[3] += S[j].w * kr;
+      qv[0] += S[j].x * qr; qv[1] += S[j].y * qr; qv[2] += S[j].z * qr; qv[3] += S[j].w * qr;
+    }
+#pragma unroll
+    for (int m = CPR; m < 64; m <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kv[i] += __shfl_xor(kv[i], m, 64);
+        qv[i] += __shfl_xor(qv[i], m, 64);
+      }
+    }
+    if (lane < CPR) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        red[buf][wave][0][c4 * 4 + i] = kv[i];
+        red[buf][wave][1][c4 * 4 + i] = qv[i];
+      }
+    }
+    __syncthreads();
+
+    // --- delta, state update, output ---
+    const float kq = skq[buf];
+    float delta[4], out[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float kvt = red[buf][0][0][c4 * 4 + i] + red[buf][1][0][c4 * 4 + i] +
+                        red[buf][2][0][c4 * 4 + i] + red[buf][3][0][c4 * 4 + i];
+      const float qvt = red[buf][0][1][c4 * 4 + i] + red[buf][1][1][c4 * 4 + i] +
+                        red[buf][2][1][c4 * 4 + i] + red[buf][3][1][c4 * 4 + i];
+      delta[i] = (vv[i] - kvt) * bt;
+      out[i] = qvt + delta[i] * kq;
+    }
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const float kr = sk[buf][r0 + RPP * j];
+      S[j].x += kr * delta[0]; S[j].y += kr * delta[1]; S[j].z += kr * delta[2]; S[j].w += kr * delta[3];
+    }
+    if (inter) {
+      float* ip = inter + (static_cast<int64_t>(b) * T + t) * Hv * D * D + static_cast<int64_t>(h) * D * D + col;
+#pragma unroll
+      for (int j = 0; j < NP; ++j) *reinterpret_cast<float4*>(ip + static_cast<int64_t>(r0 + RPP * j) * D) = S[j];
+    }
+    if (r0 == 0) {
+      uint2 u;
+      uint16_t* us = reinterpret_cast<uint16_t*>(&u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) us[i] = gdn::f2bf(out[i]);
+      *reinterpret_cast<uint2*>(o + gi * D + col) = u;
+    }
+  }
+
+  if (s_out) {
+    float* sout = s_out + row * s_out_stride + static_cast<int64_t>(h) * D * D + col;
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+      *reinterpret_cast<float4*>(sout + static_cast<int64_t>(r0 + RPP * j) * D) = S[j];
+  }
+}
+
+// pool[ids[b]] <- inter[b, accepted[b]-1]  (accepted 0: untouched).
+// grid = B * Hv blocks of 256 threads, float4 copies.
+__global__ __launch_bounds__(256) void state_commit_kernel(float* __restrict__ pool, int64_t slot_stride,
+                                                           const int64_t* __restrict__ ids,
+                                                           const float* __restrict__ inter,
+                                                           const int32_t* __restrict__ accepted,
+                                                           int T, int Hv, int D) {
+  const int b = blockIdx.x / Hv;
+  const int h = blockIdx.x % Hv;
+  const int a = accepted[b];
+  if (a <= 0 || a > T) return;
+  const float4* src = reinterpret_cast<const float4*>(
+      inter + ((static_cast<int64_t>(b) * T + (a - 1)) * Hv + h) * D * D);
+  float4* dst = reinterpret_cast<float4*>(pool + ids[b] * slot_stride + static_cast<int64_t>(h) * D * D);
+  for (int i = threadIdx.x; i < D * D / 4; i += 256) dst[i] = src[i];
+}
+
+template <int D, int NVB>
+int launch_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k, int64_t sk_b,
+                     int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t, const float* g,
+                     const uint16_t* beta, const float* s_in, int64_t s_in_stride, float* s_out,
+                     int64_t s_out_stride, const int64_t* ids, float* inter, uint16_t* o, int B,
+                     int T, int Hk, int Hv, float scale, int l2norm, hipStream_t stream) {
+  const int64_t work = static_cast<int64_t>(B) * Hv * NVB;
+  const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
+  recurrent_kernel<D, NVB><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
+      q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
+      ids, inter, o, B, T, Hk, Hv, scale, l2norm);
+  return gdn_launch_status();
+}
+
+}  // namespace
+
+extern "C" int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k,
+                             int64_t sk_b, int64_t sk_t, const uint16_t* v, int64_t sv_b,
+                             int64_t sv_t, const float* g, const uint16_t* beta,
+                             const float* s_in, int64_t s_in_stride, float* s_out,
+                             int64_t s_out_stride, const int64_t* ids, float* inter, uint16_t* o,
+                             int B, int T, int Hk, int Hv, int D, float scale, int l2norm,
+                             void* stream) {
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (B < 0 || T < 1 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
+  if (B == 0) return GDN_OK;
+  if (!q || !k || !v || !g || !beta || !s_in || !o) return GDN_ERR_INVALID_ARG;
+  // float4 state access and 8-byte v access
+  if (s_in_stride % 4 || (s_out && s_out_stride % 4) || sv_b % 4 || sv_t % 4 ||
+      reinterpret_cast<uintptr_t>(s_in) % 16 || (s_out && reinterpret_cast<uintptr_t>(s_out) % 16) ||
+      (inter && reinterpret_cast<uintptr_t>(inter) % 16) || reinterpret_cast<uintptr_t>(v) % 8 ||
+      reinterpret_cast<uintptr_t>(o) % 8)
+    return GDN_ERR_INVALID_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t heads = static_cast<int64_t>(B) * Hv;
+  // Split the v columns over more workgroups when there are few (b, h) tiles,
+  // so the launch still covers the 256 CUs with enough bytes in flight.
+  const int nvb = heads >= 2048 ? 1 : (heads >= 512 ? 2 : 4);
+#define GDN_REC_ARGS q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, \
+                     s_out_stride, ids, inter, o, B, T, Hk, Hv, scale, l2norm, s
+  if (D == 128) {
+    if (nvb == 1) return launch_recurrent<128, 1>(GDN_REC_ARGS);
+    if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);
+    return launch_recurrent<128, 4>(GDN_REC_ARGS);
+  }
+  if (nvb == 1) return launch_recurrent<64, 1>(GDN_REC_ARGS);
+  if (nvb == 2) return launch_recurrent<64, 2>(GDN_REC_ARGS);
+  return launch_recurrent<64, 4>(GDN_REC_ARGS);
+#undef GDN_REC_ARGS
+}
+
+extern "C" int gdn_state_commit(float* pool, int64_t slot_stride, const int64_t* ids,
+                                const float* inter, const int32_t* accepted, int B, int T, int Hv,
+                                int D, void* stream) {
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (B < 0 || T < 1 || Hv <= 0 || slot_stride % 4) return GDN_ERR_INVALID_ARG;
+  if (B == 0) return GDN_OK;
+  if (!pool || !ids || !inter || !accepted) return GDN_ERR_INVALID_ARG;
+  state_commit_kernel<<<dim3(static_cast<unsigned>(B * Hv)), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+      pool, slot_stride, ids, inter, accepted, T, Hv, D);
+  return gdn_launch_status();
+}

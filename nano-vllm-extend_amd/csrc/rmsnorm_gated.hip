@@ -1,0 +1,84 @@
+// Gated RMSNorm over the value head dim (D = 64 or 128), rounding in the
+// eager order of nanovllm/models/qwen3_5.py:121-131:
+//   n  = bf16(x * rsqrt(mean(x^2) + eps))      (fp32 math)
+//   wn = bf16(w * n)                           (bf16 x bf16 product)
+//   y  = bf16(float(wn) * silu(float(z)))
+// HBM-bound: 3 * D * 2 bytes per row.  D/8 lanes per row, 16-byte vectors.
+#include "gdn_common.h"
+
+namespace {
+
+template <int D>
+__global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const uint16_t* __restrict__ x,
+                                                            int64_t sx_tok,
+                                                            const uint16_t* __restrict__ z,
+                                                            int64_t sz_tok,
+                                                            const uint16_t* __restrict__ w,
+                                                            uint16_t* __restrict__ y,
+                                                            int64_t rows, int H, float eps) {
+  constexpr int kLanes = D / 8;                 // lanes per row
+  constexpr int kRowsPerBlock = 256 / kLanes;
+  const int lane = threadIdx.x % kLanes;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
+  const bool active = row < rows;
+  const int64_t tok = active ? row / H : 0;
+  const int h = active ? static_cast<int>(row % H) : 0;
+
+  uint4 xv = make_uint4(0, 0, 0, 0), zv = make_uint4(0, 0, 0, 0);
+  if (active) {
+    xv = *reinterpret_cast<const uint4*>(x + tok * sx_tok + static_cast<int64_t>(h) * D + lane * 8);
+    zv = *reinterpret_cast<const uint4*>(z + tok * sz_tok + static_cast<int64_t>(h) * D + lane * 8);
+  }
+  const uint4 wv = *reinterpret_cast<const uint4*>(w + lane * 8);
+  const uint16_t* xs = reinterpret_cast<const uint16_t*>(&xv);
+  const uint16_t* zs = reinterpret_cast<const uint16_t*>(&zv);
+  const uint16_t* ws = reinterpret_cast<const uint16_t*>(&wv);
+
+  float xf[8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    xf[i] = gdn::bf2f(xs[i]);
+    ss += xf[i] * xf[i];
+  }
+#pragma unroll
+  for (int m = kLanes / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+  const float r = rsqrtf(ss / static_cast<float>(D) + eps);
+
+  uint4 out;
+  uint16_t* os = reinterpret_cast<uint16_t*>(&out);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float n = gdn::bf2f(gdn::f2bf(xf[i] * r));
+    const float wn = gdn::bf2f(gdn::f2bf(gdn::bf2f(ws[i]) * n));
+    const float zf = gdn::bf2f(zs[i]);
+    os[i] = gdn::f2bf(wn * (zf / (1.0f + expf(-zf))));
+  }
+  if (active) *reinterpret_cast<uint4*>(y + row * D + lane * 8) = out;
+}
+
+}  // namespace
+
+extern "C" int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16_t* z,
+                                 int64_t sz_tok, const uint16_t* w, uint16_t* y, int64_t n_tok,
+                                 int H, int D, float eps, void* stream) {
+  if (n_tok < 0 || H <= 0) return GDN_ERR_INVALID_ARG;
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (n_tok == 0) return GDN_OK;
+  if (!x || !z || !w || !y) return GDN_ERR_INVALID_ARG;
+  // 16-byte vector access needs 8-element alignment of every row start.
+  if ((sx_tok % 8) || (sz_tok % 8) || (reinterpret_cast<uintptr_t>(x) % 16) ||
+      (reinterpret_cast<uintptr_t>(z) % 16) || (reinterpret_cast<uintptr_t>(w) % 16) ||
+      (reinterpret_cast<uintptr_t>(y) % 16))
+    return GDN_ERR_INVALID_ARG;
+  const int64_t rows = n_tok * H;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 128) {
+    const int64_t nb = (rows + 15) / 16;
+    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps);
+  } else {
+    const int64_t nb = (rows + 31) / 32;
+    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps);
+  }
+  return gdn_launch_status();
+}

@@ -1,0 +1,259 @@
+"""Host-side mirror of the Qwen3.5 GDN layer between its projections.
+
+GatedDeltaNetCore reproduces the dispatch and data flow of
+Qwen3_5GatedDeltaNet.forward / _gdn_prefill_varlen / _gdn_padded
+(nanovllm/models/qwen3_5.py:864-1087) from the projection outputs
+(mixed qkv, z, b, a) to the gated-norm output that feeds out_proj, on the
+HIP kernels of this package.  The in/out projection GEMMs are the caller's.
+
+A/B switches (read from the environment at construction, as the reference
+reads them at import; "1" = HIP kernel):
+  NANOVLLM_GDN_GBETA    fused g/beta kernel  | "0": eager torch chain (:936-937)
+  NANOVLLM_CONV_TRITON  conv kernels         | "0": F.conv1d chain (:1020-1024, :1057-1065)
+  NANOVLLM_GDN_INPLACE  in-place decode      | "0": gather -> recurrent kernel -> scatter (:1028-1030)
+  NANOVLLM_GDN_VARLEN   varlen prefill       | "0": padded prefill path (:1032-1077)
+  FLA_CHUNK, FLA_RECURRENT                   | "0" selected the reference's pure-torch ports,
+                                               which this build does not ship: raises.
+The varlen prefill reads and writes the state pools at the slot ids
+directly (no gather / scatter copies).
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .state_pool import varlen_meta
+
+
+@dataclass
+class Switches:
+    gbeta: bool = True
+    conv_kernel: bool = True
+    inplace: bool = True
+    varlen: bool = True
+    fla_chunk: bool = True
+    fla_recurrent: bool = True
+
+    @classmethod
+    def from_env(cls) -> "Switches":
+        e = os.environ.get
+        return cls(gbeta=e("NANOVLLM_GDN_GBETA", "1") == "1",
+                   conv_kernel=e("NANOVLLM_CONV_TRITON", "1") == "1",
+                   inplace=e("NANOVLLM_GDN_INPLACE", "1") == "1",
+                   varlen=e("NANOVLLM_GDN_VARLEN", "1") == "1",
+                   fla_chunk=e("FLA_CHUNK", "1") == "1",
+                   fla_recurrent=e("FLA_RECURRENT", "1") == "1")
+
+
+class GatedDeltaNetCore:
+    """GDN layer core for one layer's parameters.
+
+    conv_weight [C, K] (or [C, 1, K]) bf16 with C = 2*Hk*D + Hv*D;
+    A_log, dt_bias [Hv]; norm_weight [D]; eps = rms_norm_eps."""
+
+    # Prefill segment budget (tokens per padded chunk-kernel call), as the
+    # reference uses with its fused chunk kernel (qwen3_5.py:853-862).
+    PREFILL_SEGMENT_TOKENS = 16384
+
+    def __init__(self, num_k_heads: int, num_v_heads: int, head_dim: int, conv_weight: torch.Tensor,
+                 A_log: torch.Tensor, dt_bias: torch.Tensor, norm_weight: torch.Tensor,
+                 eps: float = 1e-6, switches: Switches | None = None):
+        assert num_v_heads % num_k_heads == 0
+        self.Hk, self.Hv, self.D = num_k_heads, num_v_heads, head_dim
+        self.key_dim = num_k_heads * head_dim
+        self.value_dim = num_v_heads * head_dim
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        self.K = conv_weight.shape[-1]
+        self.conv_w = conv_weight.reshape(self.conv_dim, self.K)
+        self.A_log, self.dt_bias, self.norm_w, self.eps = A_log, dt_bias, norm_weight, eps
+        self.sw = switches or Switches.from_env()
+        if not self.sw.fla_chunk:
+            raise NotImplementedError("FLA_CHUNK=0 selects the reference's pure-torch chunk port, "
+                                      "which is not part of this build")
+        if not self.sw.inplace and not self.sw.fla_recurrent:
+            raise NotImplementedError("FLA_RECURRENT=0 selects the reference's pure-torch recurrent "
+                                      "port, which is not part of this build")
+
+    def _to(self, dev):
+        if self.conv_w.device != dev:
+            self.conv_w = self.conv_w.to(dev)
+            self.A_log = self.A_log.to(dev)
+            self.dt_bias = self.dt_bias.to(dev)
+            self.norm_w = self.norm_w.to(dev)
+
+    # ---------------------------------------------------------------- gates --
+    def _g_beta(self, b, a, mask):
+        if self.sw.gbeta:
+            return ops.fused_g_beta(b, a, self.A_log, self.dt_bias, mask)
+        beta = b.sigmoid()
+        g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias.float())
+        if mask is not None:
+            g = g.masked_fill(~mask.unsqueeze(-1), 0.0)
+        return g, beta
+
+    def _norm(self, core, z):
+        return ops.rms_norm_gated(core, z, self.norm_w, self.eps)
+
+    # --------------------------------------------------------------- decode --
+    def decode(self, mixed, z, b, a, ids, conv_cache, s_cache):
+        """One token per row (the T == 1 branch of _gdn_padded, qwen3_5.py:1008-1030).
+        mixed [B, C], z [B, Hv*D], b/a [B, Hv]; pools are per-layer views.
+        Returns core [B, Hv, D] bf16."""
+        self._to(mixed.device)
+        B = mixed.shape[0]
+        Hk, Hv, D = self.Hk, self.Hv, self.D
+        g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
+        if self.sw.conv_kernel:
+            y = ops.conv_decode_step(mixed, conv_cache, ids, self.conv_w)
+        else:
+            window = torch.cat([conv_cache[ids], mixed.unsqueeze(-1)], dim=-1)
+            conv_cache[ids] = window[..., 1:]
+            y = F.silu(F.conv1d(window, self.conv_w.unsqueeze(1), groups=self.conv_dim))[..., 0]
+        kd = self.key_dim
+        q = y[:, :kd].view(B, 1, Hk, D)
+        k = y[:, kd:2 * kd].view(B, 1, Hk, D)
+        v = y[:, 2 * kd:].view(B, 1, Hv, D)
+        g1, b1 = g.view(B, 1, Hv), beta.view(B, 1, Hv)
+        if self.sw.inplace:
+            out = ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_cache, ids)
+        else:
+            out, new_s = ops.recurrent_gated_delta_rule(q, k, v, g1, b1, s_cache[ids])
+            s_cache[ids] = new_s
+        return self._norm(out.view(B, Hv, D), z.view(B, Hv, D))
+
+    # ------------------------------------------------------- varlen prefill --
+    def prefill_varlen(self, mixed, z, b, a, lens_q, ids, conv_cache, s_cache):
+        """Varlen prefill group (_gdn_prefill_varlen, qwen3_5.py:922-965) with the
+        conv and recurrent states read / written in the pools at `ids`.
+        mixed [N, C], z [N, Hv*D], b/a [N, Hv].  Returns core [N, Hv, D] bf16."""
+        self._to(mixed.device)
+        N = mixed.shape[0]
+        Hk, Hv, D = self.Hk, self.Hv, self.D
+        g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
+        cu_gpu, lens_gpu, _, cu64_gpu = varlen_meta(lens_q, mixed.device)
+        if self.sw.conv_kernel:
+            q, k, v = ops.causal_conv_silu_varlen_parts(mixed, conv_cache, self.conv_w, lens_gpu, cu_gpu[:-1],
+                                                        self.key_dim, state_ids=ids)
+        else:
+            q, k, v = self._conv_varlen_eager(mixed, lens_q, ids, conv_cache)
+        o, _ = ops.chunk_gated_delta_rule_varlen(q.view(N, Hk, D), k.view(N, Hk, D), v.view(N, Hv, D),
+                                                 g, beta, cu64_gpu, s_cache, state_ids=ids,
+                                                 final_state=s_cache)
+        return self._norm(o, z.view(N, Hv, D))
+
+    def _conv_varlen_eager(self, mixed, lens_q, ids, conv_cache):
+        """F.conv1d chain per sequence (the reference's NANOVLLM_CONV_TRITON=0 form)."""
+        outs = []
+        off = 0
+        w = self.conv_w.unsqueeze(1)
+        K = self.K
+        for r, T in enumerate(lens_q):
+            slot = ids[r:r + 1]
+            window = torch.cat([conv_cache[slot], mixed[off:off + T].t().unsqueeze(0)], dim=-1)
+            outs.append(F.silu(F.conv1d(window, w, groups=self.conv_dim))[0].t())
+            conv_cache[slot] = window[..., -(K - 1):]
+            off += T
+        y = torch.cat(outs, dim=0)
+        kd = self.key_dim
+        return y[:, :kd].contiguous(), y[:, kd:2 * kd].contiguous(), y[:, 2 * kd:].contiguous()
+
+    # ------------------------------------------------------- padded prefill --
+    def prefill_padded(self, x, z, b, a, lens, ids, conv_cache, s_cache):
+        """Padded prefill over [n, T, .] rows (T > 1 branch of _gdn_padded,
+        qwen3_5.py:1032-1077): T-segments thread the conv and recurrent
+        states; padding rows are exact no-ops (g = 0, masked conv output).
+        x [n, T, C], z [n, T, Hv*D], b/a [n, T, Hv], lens [n] (device).
+        Returns core [n, T, Hv, D] bf16."""
+        self._to(x.device)
+        n, T, C = x.shape
+        Hk, Hv, D, K = self.Hk, self.Hv, self.D, self.K
+        mask = torch.arange(T, device=x.device) < lens.unsqueeze(1)
+        g, beta = self._g_beta(b.contiguous(), a.contiguous(), mask)
+        seg = max(1, self.PREFILL_SEGMENT_TOKENS // n)
+        conv_states = conv_cache[ids]
+        state = s_cache[ids]
+        outs = []
+        kd = self.key_dim
+        for t0 in range(0, T, seg):
+            t1 = min(t0 + seg, T)
+            m = t1 - t0
+            mixed = x[:, t0:t1].transpose(1, 2)                       # [n, C, m] strided view
+            r = lens - t0
+            valid = r > 0
+            if self.sw.conv_kernel:
+                endp = r.clamp(min=-1, max=m).to(torch.int32)
+                mixed = ops.causal_conv_silu(mixed, conv_states, self.conv_w, endp)
+                conv_cache[ids[valid]] = conv_states[valid]
+            else:
+                window = torch.cat([conv_states, mixed], dim=-1)
+                mixed = F.silu(F.conv1d(window, self.conv_w.unsqueeze(1), groups=self.conv_dim))
+                starts = r.clamp(min=0, max=m)
+                cols = starts.view(n, 1, 1) + torch.arange(K - 1, device=x.device, dtype=torch.int64)
+                sel = window.gather(-1, cols.expand(n, window.size(1), K - 1))
+                conv_cache[ids[valid]] = sel[valid]
+                conv_states = window[..., -(K - 1):]
+            mixed = mixed * mask[:, t0:t1].unsqueeze(1).to(mixed.dtype)
+            q = mixed[:, :kd].transpose(1, 2).reshape(n, m, Hk, D)
+            k = mixed[:, kd:2 * kd].transpose(1, 2).reshape(n, m, Hk, D)
+            v = mixed[:, 2 * kd:].transpose(1, 2).reshape(n, m, Hv, D)
+            o, state = ops.chunk_gated_delta_rule(q, k, v, g=g[:, t0:t1].contiguous(),
+                                                  beta=beta[:, t0:t1].contiguous(), initial_state=state,
+                                                  output_final_state=True, use_qk_l2norm_in_kernel=True)
+            outs.append(o)
+        s_cache[ids] = state
+        out = torch.cat(outs, dim=1)                                  # [n, T, Hv, D]
+        return self._norm(out, z.view(n, T, Hv, D))
+
+    # ------------------------------------------------------------- dispatch --
+    def forward(self, mixed, z, b, a, cu_seqlens_q, max_seqlen_q, ids, conv_cache, s_cache,
+                lens_q: list[int] | None = None):
+        """Dispatch of Qwen3_5GatedDeltaNet.forward (qwen3_5.py:864-920) over a
+        varlen step: all-decode -> decode; a contiguous decode prefix goes to
+        the decode path and the rest to the varlen (or padded) prefill.
+        mixed [N, C], z [N, Hv*D], b/a [N, Hv].  Returns [N, Hv*D] bf16."""
+        N = mixed.shape[0]
+        lens = cu_seqlens_q[1:] - cu_seqlens_q[:-1]
+        bs = lens.shape[0]
+        T = int(max_seqlen_q)
+        if T == 1:
+            return self.decode(mixed, z, b, a, ids, conv_cache, s_cache).view(N, self.value_dim)
+        if lens_q is None:
+            lens_q = lens.tolist()
+        n1 = 0
+        while n1 < bs and lens_q[n1] == 1:
+            n1 += 1
+        pre_ok = 0 < n1 < bs and min(lens_q[n1:]) > 1
+        if n1 == 0 or pre_ok:
+            parts = []
+            off = 0
+            if n1:
+                parts.append(self.decode(mixed[:n1], z[:n1], b[:n1], a[:n1], ids[:n1], conv_cache,
+                                         s_cache).view(n1, self.value_dim))
+                off = n1
+            if self.sw.varlen:
+                parts.append(self.prefill_varlen(mixed[off:], z[off:], b[off:], a[off:], lens_q[off:],
+                                                 ids[off:], conv_cache, s_cache).view(-1, self.value_dim))
+                return torch.cat(parts, dim=0)
+            lens_p = lens[off:]
+            Tp = T if off == 0 else max(lens_q[off:])
+            parts.append(self._padded_varlen(mixed[off:], z[off:], b[off:], a[off:], lens_p, Tp, ids[off:],
+                                             conv_cache, s_cache))
+            return torch.cat(parts, dim=0)
+        # len-1 rows that are not a contiguous prefix: one padded pass
+        return self._padded_varlen(mixed, z, b, a, lens, T, ids, conv_cache, s_cache)
+
+    def _padded_varlen(self, mixed, z, b, a, lens, T, ids, conv_cache, s_cache):
+        n = lens.shape[0]
+        mask = torch.arange(T, device=mixed.device) < lens.unsqueeze(1)
+
+        def pad(t):
+            p = t.new_zeros(n, T, t.shape[-1])
+            p[mask] = t
+            return p
+
+        core = self.prefill_padded(pad(mixed), pad(z), pad(b), pad(a), lens, ids, conv_cache, s_cache)
+        return core.reshape(n, T, self.value_dim)[mask]

@@ -1,0 +1,411 @@
+"""GDN operators with the reference's Python signatures, backed by the gfx950
+HIP kernels of libgdn_mi355x.so.
+
+Each function mirrors a module-level function of
+nanovllm/models/qwen3_5.py (cited per function): same argument meaning,
+same output allocation (torch.empty on the input's device), same in-place
+mutation of the state pools, and the reference's shape asserts.  There is no
+CPU or eager fallback: a CPU tensor or a missing library raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _check_cuda(*ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("GDN ops run on the GPU only (got a CPU tensor; there is no CPU path)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _bf16(t: torch.Tensor, name: str) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+
+
+def _stream(dev: torch.device) -> int:
+    return _lib.stream_handle(dev)
+
+
+# ----------------------------------------------------------------- g / beta --
+def fused_g_beta(b: torch.Tensor, a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
+                 mask: torch.Tensor | None):
+    """g = -exp(A_log) * softplus(a + dt_bias) (fp32, 0 on padding rows),
+    beta = sigmoid(b) (bf16).  b/a [.., Vh] bf16 contiguous; a_log/dt_bias
+    [Vh] (bf16 or fp32); mask [n, T] bool or None.
+    Reference: fused_g_beta, nanovllm/models/qwen3_5.py:345-360."""
+    dev = _check_cuda(b, a, a_log, dt_bias, mask)
+    _bf16(a, "a")
+    _bf16(b, "b")
+    assert a.is_contiguous() and b.is_contiguous() and a.shape == b.shape
+    vh = a.shape[-1]
+    if a_log.dtype != dt_bias.dtype or a_log.dtype not in (torch.bfloat16, torch.float32):
+        a_log = a_log.float()
+        dt_bias = dt_bias.float()
+    a_log = a_log.contiguous()
+    dt_bias = dt_bias.contiguous()
+    assert a_log.numel() == vh and dt_bias.numel() == vh
+    g = torch.empty_like(a, dtype=torch.float32)
+    beta = torch.empty_like(a)
+    flat_mask = None
+    if mask is not None:
+        flat_mask = mask.reshape(-1).contiguous()
+        if flat_mask.dtype != torch.bool:
+            flat_mask = flat_mask.to(torch.bool)
+        assert flat_mask.numel() * vh == a.numel()
+    _lib.call("gdn_g_beta", _lib.ptr(b), _lib.ptr(a), _lib.ptr(a_log), _lib.ptr(dt_bias),
+              int(a_log.dtype == torch.float32), _lib.ptr(flat_mask), _lib.ptr(g), _lib.ptr(beta),
+              a.numel(), vh, _stream(dev))
+    return g, beta
+
+
+# --------------------------------------------------------------------- conv --
+def _conv_varlen(x, state, weight, lens, cuseq, key_dim, state_ids):
+    dev = _check_cuda(x, state, weight, lens, cuseq, state_ids)
+    _bf16(x, "x")
+    _bf16(state, "state")
+    N, C = x.shape
+    K = weight.shape[-1]
+    w = weight.reshape(C, K)
+    _bf16(w, "weight")
+    w = w.contiguous()
+    assert x.stride(1) == 1 and state.stride(2) == 1 and tuple(state.shape[1:]) == (C, K - 1)
+    n = lens.shape[0]
+    lens32 = lens.to(torch.int32).contiguous()
+    cu32 = cuseq.to(torch.int32).contiguous()
+    assert cu32.shape[0] >= n
+    ids = None
+    if state_ids is not None:
+        ids = state_ids.to(torch.int64).contiguous()
+        assert ids.shape[0] == n
+    y = torch.empty(N * C, dtype=x.dtype, device=x.device)
+    _lib.call("gdn_conv_varlen", _lib.ptr(x), x.stride(0), _lib.ptr(state), state.stride(0),
+              state.stride(1), _lib.ptr(ids), _lib.ptr(w), _lib.ptr(y), key_dim, _lib.ptr(lens32),
+              _lib.ptr(cu32), n, N, C, K, _stream(dev))
+    return y
+
+
+def causal_conv_silu_varlen_parts(x: torch.Tensor, state: torch.Tensor, weight: torch.Tensor,
+                                  lens: torch.Tensor, cuseq: torch.Tensor, key_dim: int,
+                                  state_ids: torch.Tensor | None = None):
+    """Varlen conv + SiLU returning the (q, k, v) parts [N, key_dim],
+    [N, key_dim], [N, C - 2*key_dim], each contiguous (one allocation), so
+    grouped-value layouts (C != 3*key_dim) are covered.  state: conv states
+    [n, C, K-1], or with state_ids the slot pool [slots, C, K-1] updated in
+    place at those rows."""
+    N, C = x.shape
+    y = _conv_varlen(x, state, weight, lens, cuseq, key_dim, state_ids)
+    q = y[: N * key_dim].view(N, key_dim)
+    k = y[N * key_dim: 2 * N * key_dim].view(N, key_dim)
+    v = y[2 * N * key_dim:].view(N, C - 2 * key_dim)
+    return q, k, v
+
+
+def causal_conv_silu_varlen(x: torch.Tensor, state: torch.Tensor, weight: torch.Tensor,
+                            lens: torch.Tensor, cuseq: torch.Tensor) -> torch.Tensor:
+    """x [N, C] bf16 contiguous varlen; state [n, C, K-1] (updated in place);
+    lens int32 [n]; cuseq int32 [n] (per-row starts).  Returns [3, N, C//3]:
+    the q/k/v thirds, each contiguous.
+    Reference: causal_conv_silu_varlen, nanovllm/models/qwen3_5.py:459-473."""
+    N, C = x.shape
+    d3 = C // 3
+    assert d3 * 3 == C and d3 % 64 == 0
+    return _conv_varlen(x, state, weight, lens, cuseq, d3, None).view(3, N, d3)
+
+
+def conv_decode_step(x: torch.Tensor, state_pool: torch.Tensor, ids: torch.Tensor,
+                     weight: torch.Tensor) -> torch.Tensor:
+    """x [n, C] (decode rows); state_pool [slots, C, K-1] rolled in place at
+    rows `ids`; weight [C, K] (or [C, 1, K]).  Returns y [n, C].
+    Reference: conv_decode_step, nanovllm/models/qwen3_5.py:546-558."""
+    dev = _check_cuda(x, state_pool, ids, weight)
+    _bf16(x, "x")
+    _bf16(state_pool, "state_pool")
+    n, C = x.shape
+    K = weight.shape[-1]
+    w = weight.reshape(C, K).contiguous()
+    assert x.stride(1) == 1 and state_pool.stride(2) == 1
+    ids64 = ids.to(torch.int64).contiguous()
+    y = torch.empty(n, C, dtype=x.dtype, device=x.device)
+    _lib.call("gdn_conv_decode", _lib.ptr(x), x.stride(0), _lib.ptr(state_pool), state_pool.stride(0),
+              state_pool.stride(1), _lib.ptr(ids64), _lib.ptr(w), _lib.ptr(y), y.stride(0), n, C, K,
+              _stream(dev))
+    return y
+
+
+def causal_conv_silu(x: torch.Tensor, state: torch.Tensor, weight: torch.Tensor,
+                     endp: torch.Tensor) -> torch.Tensor:
+    """x [n, C, T] (arbitrary strides), state [n, C, K-1] (updated in place
+    at each row's endp), weight [C, K].  Returns y [n, C, T] contiguous;
+    endp int32 [n] (-1 = skip writeback).
+    Reference: causal_conv_silu, nanovllm/models/qwen3_5.py:300-317."""
+    dev = _check_cuda(x, state, weight, endp)
+    _bf16(x, "x")
+    _bf16(state, "state")
+    n, C, T = x.shape
+    K = weight.shape[-1]
+    w = weight.reshape(C, K).contiguous()
+    assert state.stride(2) == 1
+    e32 = endp.to(torch.int32).contiguous()
+    y = torch.empty(n, C, T, dtype=x.dtype, device=x.device)
+    _lib.call("gdn_conv_padded", _lib.ptr(x), x.stride(0), x.stride(1), x.stride(2), _lib.ptr(state),
+              state.stride(0), state.stride(1), _lib.ptr(w), _lib.ptr(y), _lib.ptr(e32), n, C, T, K,
+              _stream(dev))
+    return y
+
+
+# -------------------------------------------------------------- chunk rule --
+def _state_view_ok(s: torch.Tensor, H: int, D: int) -> bool:
+    return (s.dtype == torch.float32 and s.dim() == 4 and tuple(s.shape[1:]) == (H, D, D)
+            and s.stride(1) == D * D and s.stride(2) == D and s.stride(3) == 1)
+
+
+def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+                                  beta: torch.Tensor, cu_seqlens: torch.Tensor,
+                                  initial_state: torch.Tensor | None = None, *,
+                                  output_final_state: bool = True,
+                                  use_qk_l2norm_in_kernel: bool = True, scale: float | None = None,
+                                  state_ids: torch.Tensor | None = None,
+                                  final_state: torch.Tensor | None = None):
+    """Varlen chunked gated delta rule (chunk 64) on packed rows.
+
+    q, k [N, Hk, D]; v [N, Hv, D] (bf16, head dim contiguous, any token
+    stride); g [N, Hv] fp32; beta [N, Hv] bf16; cu_seqlens [n+1] (device).
+    Value head h uses key head h // (Hv // Hk).
+    initial_state: [n, Hv, D, D] fp32, or with state_ids a slot pool
+    [slots, Hv, D, D] (any slot stride) read at rows state_ids.
+    Final states go to `final_state` (same indexing; may be the pool itself
+    for an in-place update) or to a new [n, Hv, D, D] tensor.
+    Returns (o [N, Hv, D] bf16, final or None)."""
+    dev = _check_cuda(q, k, v, g, beta, cu_seqlens, initial_state, state_ids, final_state)
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
+        _bf16(t, nm)
+    N, Hk, D = k.shape
+    Hv = v.shape[1]
+    assert q.shape == k.shape and v.shape[0] == N and v.shape[2] == D and Hv % Hk == 0
+    assert q.stride(2) == 1 and k.stride(2) == 1 and v.stride(2) == 1
+    assert q.stride(1) == D and k.stride(1) == D and v.stride(1) == D
+    g = g.float().contiguous() if g.dtype != torch.float32 else g.contiguous()
+    beta = beta.contiguous()
+    assert g.shape == (N, Hv) and beta.shape == (N, Hv)
+    cu = cu_seqlens.to(torch.int64).contiguous()
+    n = cu.shape[0] - 1
+    ids = None
+    if state_ids is not None:
+        ids = state_ids.to(torch.int64).contiguous()
+        assert ids.shape[0] == n
+    h0 = initial_state
+    if h0 is not None and not _state_view_ok(h0, Hv, D):
+        assert state_ids is None, "pool-indexed initial state must be an fp32 [slots, H, D, D] view"
+        h0 = h0.float().contiguous()
+    hT = None
+    if output_final_state:
+        if final_state is not None:
+            assert _state_view_ok(final_state, Hv, D)
+            hT = final_state
+        else:
+            assert state_ids is None or h0 is not None
+            hT = torch.empty(n, Hv, D, D, dtype=torch.float32, device=q.device)
+    if ids is not None and hT is not None and final_state is None:
+        raise ValueError("state_ids requires final_state (the pool) for the output state")
+    sstride = 0
+    for st in (h0, hT):
+        if st is not None:
+            sstride = st.stride(0)
+    if h0 is not None and hT is not None:
+        assert h0.stride(0) == hT.stride(0), "initial and final state must share the slot stride"
+    if scale is None:
+        scale = D ** -0.5
+    o = torch.empty(N, Hv, D, dtype=v.dtype, device=v.device)
+    _lib.call("gdn_chunk_prefill", _lib.ptr(q), q.stride(0), _lib.ptr(k), k.stride(0), _lib.ptr(v),
+              v.stride(0), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0), _lib.ptr(hT), _lib.ptr(ids),
+              sstride, _lib.ptr(cu), n, N, Hk, Hv, D, float(scale), int(bool(use_qk_l2norm_in_kernel)),
+              _lib.ptr(o), _stream(dev))
+    return o, hT
+
+
+def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, initial_state=None,
+                           output_final_state=False, use_qk_l2norm_in_kernel=False,
+                           cu_seqlens=None, cu_seqlens_cpu=None, chunk_size=64, **kwargs):
+    """Drop-in for the chunk GDN entry point the reference calls.
+
+    Covers both reference call forms:
+      * chunk_gated_delta_rule(q, k, v, g, beta, chunk_size=64, initial_state=...)
+        (nanovllm/models/qwen3_5.py:140-149): batched [B, T, H, D], always
+        returns the final state, L2-norm in kernel;
+      * the fla varlen call (qwen3_5.py:956-960): q[None] [1, N, H, D],
+        cu_seqlens int64 [n+1], initial_state [n, H, D, D].
+    Returns (o [B, T, Hv, D] bf16, final [B or n, Hv, D, D] fp32 or None)."""
+    if chunk_size != 64:
+        raise ValueError("only chunk_size=64 is built (the reference's value)")
+    if "cu_seqlens" in kwargs:
+        cu_seqlens = kwargs.pop("cu_seqlens")
+    B, T, Hq, D = query.shape
+    Hv = value.shape[2]
+    if cu_seqlens is not None:
+        assert B == 1, "varlen mode takes a single packed batch row"
+        cu = cu_seqlens
+        qf, kf, vf = query[0], key[0], value[0]
+        gf, bf = g[0], beta[0]
+    else:
+        cu = torch.arange(B + 1, device=query.device, dtype=torch.int64) * T
+        qf = query.reshape(B * T, Hq, D)
+        kf = key.reshape(B * T, Hq, D)
+        vf = value.reshape(B * T, Hv, D)
+        gf = g.reshape(B * T, Hv)
+        bf = beta.reshape(B * T, Hv)
+    o, final = chunk_gated_delta_rule_varlen(qf, kf, vf, gf, bf, cu, initial_state,
+                                             output_final_state=output_final_state,
+                                             use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+                                             scale=scale)
+    return o.view(B, T, Hv, D), final
+
+
+def chunk_gated_delta_rule_ref_api(query, key, value, g, beta, chunk_size=64, initial_state=None):
+    """The reference module's own signature (nanovllm/models/qwen3_5.py:140-149):
+    final state always returned, q/k L2-normalised in kernel."""
+    return chunk_gated_delta_rule(query, key, value, g=g, beta=beta, initial_state=initial_state,
+                                  output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                  chunk_size=chunk_size)
+
+
+# ---------------------------------------------------------- recurrent rule --
+def _recurrent(q, k, v, g, beta, s_in, s_out, ids, inter, scale, l2norm):
+    dev = _check_cuda(q, k, v, g, beta, s_in, s_out, ids, inter)
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
+        _bf16(t, nm)
+    Bsz, T, Hk, D = k.shape
+    Hv = v.shape[2]
+    assert q.shape == k.shape and v.shape[:2] == (Bsz, T) and v.shape[3] == D and Hv % Hk == 0
+    assert q.stride(2) == D and k.stride(2) == D and v.stride(2) == D
+    assert q.stride(3) == 1 and k.stride(3) == 1 and v.stride(3) == 1
+    g = g.float() if g.dtype != torch.float32 else g
+    assert g.is_contiguous() and beta.is_contiguous()
+    assert g.numel() == Bsz * T * Hv and beta.numel() == Bsz * T * Hv
+    assert _state_view_ok(s_in, Hv, D)
+    if s_out is not None:
+        assert _state_view_ok(s_out, Hv, D)
+    ids64 = None
+    if ids is not None:
+        ids64 = ids.to(torch.int64).contiguous()
+        assert ids64.shape[0] == Bsz
+    if inter is not None:
+        assert inter.is_contiguous() and inter.dtype == torch.float32
+        assert inter.shape == (Bsz, T, Hv, D, D)
+    out = torch.empty(Bsz, T, Hv, D, dtype=v.dtype, device=v.device)
+    if scale is None:
+        scale = D ** -0.5
+    _lib.call("gdn_recurrent", _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(k), k.stride(0),
+              k.stride(1), _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(g), _lib.ptr(beta),
+              _lib.ptr(s_in), s_in.stride(0), _lib.ptr(s_out), s_out.stride(0) if s_out is not None else 0,
+              _lib.ptr(ids64), _lib.ptr(inter), _lib.ptr(out), Bsz, T, Hk, Hv, D, float(scale),
+              int(bool(l2norm)), _stream(dev))
+    return out
+
+
+def recurrent_gdn_inplace(q, k, v, g, beta, s_pool, ids):
+    """q/k/v [bs, 1, H, D] bf16, g/beta [bs, 1, H]; updates s_pool rows `ids`
+    in place, returns out [bs, 1, H, DV] bf16.  q/k/v may be strided views
+    of the conv output; s_pool a per-layer view of the state pool.
+    Reference: recurrent_gdn_inplace, nanovllm/models/qwen3_5.py:597-613."""
+    bs, _, H, DK = k.shape
+    DV = v.shape[-1]
+    assert q.stride(2) == DK and k.stride(2) == DK and v.stride(2) == DV
+    assert g.is_contiguous() and beta.is_contiguous()
+    assert s_pool.stride(1) == DK * DV and s_pool.stride(2) == DV and s_pool.stride(3) == 1
+    return _recurrent(q, k, v, g, beta, s_pool, s_pool, ids, None, None, True)
+
+
+def recurrent_gated_delta_rule(query, key, value, g=None, beta=None, initial_state=None, scale=None,
+                               output_final_state=True, use_qk_l2norm_in_kernel=True, **kwargs):
+    """Gathered-state recurrent rule (T >= 1 tokens per row).
+    query/key [B, T, Hk, D], value [B, T, Hv, D], g/beta [B, T, Hv];
+    initial_state [B, Hv, D, D] fp32 or None (zeros).  Returns
+    (out [B, T, Hv, D], final [B, Hv, D, D] or None).
+    Reference: recurrent_gated_delta_rule / _torch_recurrent_gated_delta_rule,
+    nanovllm/models/qwen3_5.py:230-238, :616-651."""
+    Bsz, T, Hk, D = key.shape
+    Hv = value.shape[2]
+    if initial_state is None:
+        s_in = torch.zeros(Bsz, Hv, D, D, dtype=torch.float32, device=value.device)
+    else:
+        s_in = initial_state if _state_view_ok(initial_state, Hv, D) else initial_state.float().contiguous()
+    s_out = torch.empty(Bsz, Hv, D, D, dtype=torch.float32, device=value.device) if output_final_state else None
+    out = _recurrent(query, key, value, g.contiguous(), beta.contiguous(), s_in, s_out, None, None, scale,
+                     use_qk_l2norm_in_kernel)
+    return out, s_out
+
+
+def recurrent_gdn_multitoken(q, k, v, g, beta, s_pool, ids, intermediate_states=None):
+    """Speculative-verify decode: T draft tokens per sequence against the
+    slot pool.  q/k [B, T, Hk, D], v [B, T, Hv, D], g/beta [B, T, Hv].
+    With intermediate_states ([B, T, Hv, D, D] fp32) the per-token states
+    are written there and the pool is left untouched (commit_states picks
+    the accepted prefix); without it the pool is advanced by all T tokens.
+    Returns out [B, T, Hv, D].  (No reference counterpart: spec decode is
+    disabled for qwen3_5, nanovllm/config.py:84.)"""
+    s_out = None if intermediate_states is not None else s_pool
+    return _recurrent(q, k, v, g, beta, s_pool, s_out, ids, intermediate_states, None, True)
+
+
+def commit_states(s_pool, ids, intermediate_states, accepted):
+    """s_pool[ids[b]] <- intermediate_states[b, accepted[b] - 1]
+    (accepted in [1, T]; 0 leaves the slot unchanged)."""
+    dev = _check_cuda(s_pool, ids, intermediate_states, accepted)
+    Bsz, T, Hv, D, _ = intermediate_states.shape
+    assert _state_view_ok(s_pool, Hv, D) and intermediate_states.is_contiguous()
+    ids64 = ids.to(torch.int64).contiguous()
+    acc = accepted.to(torch.int32).contiguous()
+    _lib.call("gdn_state_commit", _lib.ptr(s_pool), s_pool.stride(0), _lib.ptr(ids64),
+              _lib.ptr(intermediate_states), _lib.ptr(acc), Bsz, T, Hv, D, _stream(dev))
+
+
+# -------------------------------------------------------------- gated norm --
+def rms_norm_gated(hidden_states: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor,
+                   eps: float) -> torch.Tensor:
+    """y = bf16(float(bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))) * silu(float(z)))
+    over the last dim.  hidden_states / gate [..., H, D] bf16 (head dim
+    contiguous, rows of a token contiguous).
+    Reference: _rms_gated_forward, nanovllm/models/qwen3_5.py:121-131."""
+    dev = _check_cuda(hidden_states, gate, weight)
+    _bf16(hidden_states, "hidden_states")
+    _bf16(gate, "gate")
+    D = hidden_states.shape[-1]
+    assert hidden_states.dim() >= 2 and gate.shape == hidden_states.shape
+    w = weight.to(torch.bfloat16).contiguous()
+    assert w.numel() == D
+    H = hidden_states.shape[-2]
+    x2 = hidden_states.reshape(-1, H, D)
+    z2 = gate.reshape(-1, H, D)
+    if x2.stride(2) != 1 or x2.stride(1) != D:
+        x2 = x2.contiguous()
+    if z2.stride(2) != 1 or z2.stride(1) != D:
+        z2 = z2.contiguous()
+    n_tok, H, _ = x2.shape
+    y = torch.empty(n_tok, H, D, dtype=hidden_states.dtype, device=hidden_states.device)
+    _lib.call("gdn_rmsnorm_gated", _lib.ptr(x2), x2.stride(0), _lib.ptr(z2), z2.stride(0), _lib.ptr(w),
+              _lib.ptr(y), n_tok, H, D, float(eps), _stream(dev))
+    return y.view(hidden_states.shape)
+
+
+class Qwen3_5RMSNormGated(torch.nn.Module):
+    """Delta-net output norm on the value head dim, gated by silu(z).
+    Reference: Qwen3_5RMSNormGated, nanovllm/models/qwen3_5.py:697-709."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.ones(hidden_size))
+        self.eps = eps
+
+    def forward(self, hidden_states: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        return rms_norm_gated(hidden_states, gate, self.weight, self.eps)
