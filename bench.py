@@ -1,0 +1,364 @@
+#!/usr/bin/env python3
+"""Benchmark of the GDN layer path on one MI355X.
+
+Headline (`value`): config 1 -- varlen prefill of one GDN layer core
+(fused g/beta + varlen conv + chunked gated delta rule + gated RMSNorm, the
+path between the projections) over 8 sequences with lengths ~U[128, 4096]
+(seed 1; 17,001 tokens), Hk = Hv = 16, d = 128, chunk 64, tokens/s.
+`roofline` is the dominant kernel of that step (the chunk prefill, MFMA
+bound); `cpu_baseline` is this repo's CPU oracle of the same path on a
+bounded slice of the same workload.  Extra objects carry config 2 (batched
+decode, HBM bound), config 3 (65,536-token prefill) and config 4
+(speculative-verify multi-token decode).
+
+Inputs are synthetic, generated with one seeded CPU torch.Generator per
+config in a fixed order, then moved to HBM before the timed region.  Every
+kernel runs inside the timed steps; per-kernel durations come from HIP
+events recorded on the stream the kernels are launched on.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "GDN prefill tokens/s (MFMA util); decode state GB/s vs HBM peak, 1 GPU"
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0       # MI355X dense bf16 MFMA
+BF16 = torch.bfloat16
+
+
+def chunk_flops(n_tokens: int, Hv: int, D: int, C: int = 64) -> float:
+    """Algorithmic chunk-prefill FLOPs per call: N*Hv*[2C(3D+2D) + 6D^2 + (2/3)C^2]
+    (full QK^T/KK^T tiles, W, U, intra-chunk O, three state GEMMs, the solve)."""
+    return float(n_tokens) * Hv * (2 * C * (3 * D + 2 * D) + 6 * D * D + (2.0 / 3.0) * C * C)
+
+
+# ------------------------------------------------------------------ inputs --
+def _params(gen, Hv, D, C):
+    A_log = (torch.rand(Hv, generator=gen) * math.log(16)).to(BF16)
+    dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(BF16)
+    conv_w = (torch.randn(C, 4, generator=gen) * 0.5).to(BF16)
+    norm_w = (1 + 0.02 * torch.randn(D, generator=gen)).to(BF16)
+    return A_log, dt_bias, conv_w, norm_w
+
+
+def make_prefill(seed: int, lens: list[int] | None, Hk=16, Hv=16, D=128, h0_std=0.0, conv_std=0.0):
+    """Config 1 (seed 1, lens ~U[128,4096] x 8) / config 3 (seed 4, 1 x 65536,
+    h0 ~ N(0, 0.1^2), conv prefix ~ N(0,1)).  Draw order: lens, x, z, a, b,
+    A_log, dt_bias, conv_w, norm_w, h0, conv state."""
+    gen = torch.Generator().manual_seed(seed)
+    if lens is None:
+        lens = torch.randint(128, 4097, (8,), generator=gen).tolist()
+    N = sum(lens)
+    C = 2 * Hk * D + Hv * D
+    x = torch.randn(N, C, generator=gen).to(BF16)
+    z = torch.randn(N, Hv * D, generator=gen).to(BF16)
+    a = torch.randn(N, Hv, generator=gen).to(BF16)
+    b = torch.randn(N, Hv, generator=gen).to(BF16)
+    A_log, dt_bias, conv_w, norm_w = _params(gen, Hv, D, C)
+    n = len(lens)
+    h0 = torch.randn(n, Hv, D, D, generator=gen) * h0_std if h0_std else torch.zeros(n, Hv, D, D)
+    cs = (torch.randn(n, C, 3, generator=gen) * conv_std).to(BF16) if conv_std else torch.zeros(n, C, 3, dtype=BF16)
+    return dict(lens=lens, N=N, Hk=Hk, Hv=Hv, D=D, C=C, x=x, z=z, a=a, b=b, A_log=A_log, dt_bias=dt_bias,
+                conv_w=conv_w, norm_w=norm_w, h0=h0, conv_state=cs)
+
+
+def make_decode(seed=2, B=256, slots=512, Hk=16, Hv=16, D=128):
+    """Config 2: ids = randperm(512)[:256], s_pool ~ N(0, 0.1^2) [512,16,128,128],
+    conv_pool ~ N(0,1) [512, 6144, 3]; one token per sequence.
+    Draw order: ids, s_pool, conv_pool, x, z, a, b, A_log, dt_bias, conv_w, norm_w."""
+    gen = torch.Generator().manual_seed(seed)
+    C = 2 * Hk * D + Hv * D
+    ids = torch.randperm(slots, generator=gen)[:B]
+    s_pool = torch.randn(slots, Hv, D, D, generator=gen) * 0.1
+    conv_pool = torch.randn(slots, C, 3, generator=gen).to(BF16)
+    x = torch.randn(B, C, generator=gen).to(BF16)
+    z = torch.randn(B, Hv * D, generator=gen).to(BF16)
+    a = torch.randn(B, Hv, generator=gen).to(BF16)
+    b = torch.randn(B, Hv, generator=gen).to(BF16)
+    A_log, dt_bias, conv_w, norm_w = _params(gen, Hv, D, C)
+    return dict(B=B, Hk=Hk, Hv=Hv, D=D, C=C, ids=ids, s_pool=s_pool, conv_pool=conv_pool, x=x, z=z, a=a, b=b,
+                A_log=A_log, dt_bias=dt_bias, conv_w=conv_w, norm_w=norm_w)
+
+
+def make_spec(seed=3, B=64, T=4, slots=128, Hk=16, Hv=32, D=128):
+    """Config 4: 64 sequences x 4 draft tokens, Hk=16 / Hv=32, pool [128,32,128,128]
+    ~ N(0, 0.1^2), ids = randperm(128)[:64], accepted ~ U{1..4}.
+    Draw order: ids, s_pool, q, k, v, a, b, A_log, dt_bias, accepted."""
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.randperm(slots, generator=gen)[:B]
+    s_pool = torch.randn(slots, Hv, D, D, generator=gen) * 0.1
+    q = torch.randn(B, T, Hk, D, generator=gen).to(BF16)
+    k = torch.randn(B, T, Hk, D, generator=gen).to(BF16)
+    v = torch.randn(B, T, Hv, D, generator=gen).to(BF16)
+    a = torch.randn(B, T, Hv, generator=gen).to(BF16)
+    b = torch.randn(B, T, Hv, generator=gen).to(BF16)
+    A_log = (torch.rand(Hv, generator=gen) * math.log(16)).to(BF16)
+    dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(BF16)
+    accepted = torch.randint(1, T + 1, (B,), generator=gen)
+    return dict(B=B, T=T, Hk=Hk, Hv=Hv, D=D, ids=ids, s_pool=s_pool, q=q, k=k, v=v, a=a, b=b, A_log=A_log,
+                dt_bias=dt_bias, accepted=accepted)
+
+
+# ------------------------------------------------------------------ timing --
+class EventTimer:
+    """HIP events around named kernels on torch's current stream (the stream
+    the kernels are launched on)."""
+
+    def __init__(self):
+        self.open: dict[str, torch.cuda.Event] = {}
+        self.pairs: dict[str, list] = {}
+
+    def start(self, name):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.open[name] = e
+
+    def stop(self, name):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.setdefault(name, []).append((self.open.pop(name), e))
+
+    def reset(self):
+        self.pairs.clear()
+
+    def avg_us(self) -> dict[str, float]:
+        return {k: 1e3 * statistics.fmean(s.elapsed_time(e) for s, e in v) for k, v in self.pairs.items()}
+
+
+def timed_steps(step, K: int) -> float:
+    """Wall-clock seconds of exactly K steps, synchronised on both sides."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+# -------------------------------------------------------------- workloads --
+def prefill_bench(pkg, cfg, dev, K, W):
+    core = pkg.GatedDeltaNetCore(cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
+                                 cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
+    x, z, a, b = (cfg[k].to(dev) for k in ("x", "z", "a", "b"))
+    n = len(cfg["lens"])
+    s_pool = cfg["h0"].to(dev)
+    conv_pool = cfg["conv_state"].to(dev)
+    ids = torch.arange(n, device=dev)
+    lens = cfg["lens"]
+
+    def step():
+        core.prefill_varlen(x, z, b, a, lens, ids, conv_pool, s_pool)
+
+    for _ in range(W):
+        step()
+    timer = EventTimer()
+    core.timer = timer
+    t = timed_steps(step, K)
+    core.timer = None
+    return t / K, timer.avg_us()
+
+
+def decode_bench(pkg, cfg, dev, K, W):
+    core = pkg.GatedDeltaNetCore(cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
+                                 cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
+    x, z, a, b = (cfg[k].to(dev) for k in ("x", "z", "a", "b"))
+    s_pool = cfg["s_pool"].to(dev)
+    conv_pool = cfg["conv_pool"].to(dev)
+    ids = cfg["ids"].to(dev)
+
+    def step():
+        core.decode(x, z, b, a, ids, conv_pool, s_pool)
+
+    for _ in range(W):
+        step()
+    timer = EventTimer()
+    core.timer = timer
+    t = timed_steps(step, K)
+    core.timer = None
+    # the same step replayed from a captured HIP graph (how the engine runs decode)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    t_graph = timed_steps(g.replay, K)
+    return t / K, t_graph / K, timer.avg_us()
+
+
+def spec_bench(pkg, cfg, dev, K, W):
+    B, T, Hv, D = cfg["B"], cfg["T"], cfg["Hv"], cfg["D"]
+    q, k, v, a, b = (cfg[n].to(dev) for n in ("q", "k", "v", "a", "b"))
+    g, beta = pkg.ops.fused_g_beta(b, a, cfg["A_log"].to(dev), cfg["dt_bias"].to(dev), None)
+    s_pool = cfg["s_pool"].to(dev)
+    ids = cfg["ids"].to(dev)
+    acc = cfg["accepted"].to(dev)
+    inter = torch.empty(B, T, Hv, D, D, device=dev)
+    timer = EventTimer()
+
+    def step():
+        timer.start("recurrent_multitoken")
+        pkg.ops.recurrent_gdn_multitoken(q, k, v, g, beta, s_pool, ids, intermediate_states=inter)
+        timer.stop("recurrent_multitoken")
+        timer.start("state_commit")
+        pkg.ops.commit_states(s_pool, ids, inter, acc)
+        timer.stop("state_commit")
+
+    for _ in range(W):
+        step()
+    timer.reset()
+    t = timed_steps(step, K)
+    return t / K, timer.avg_us()
+
+
+def cpu_baseline(cfg, n_seq: int, threads: int):
+    """CPU oracle (fp32 torch restatement of the reference path) on the first
+    n_seq sequences of config 1: 1 warm-up on a 256-token slice, median of 3."""
+    from oracle import gdn_ref
+
+    torch.set_num_threads(threads)
+    lens = cfg["lens"][:n_seq]
+    N = sum(lens)
+    Hk, Hv, D = cfg["Hk"], cfg["Hv"], cfg["D"]
+    args = (cfg["x"][:N], cfg["z"][:N], cfg["b"][:N], cfg["a"][:N])
+    common = (cfg["conv_w"], cfg["A_log"], cfg["dt_bias"], cfg["norm_w"], Hk, Hv, D)
+    gdn_ref.gdn_core_varlen(*(t[:256] for t in args), [256], cfg["conv_state"][:1], cfg["h0"][:1], *common)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        gdn_ref.gdn_core_varlen(*args, lens, cfg["conv_state"][:n_seq], cfg["h0"][:n_seq], *common)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    cpu_name = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": N / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config 1 GDN core (g/beta+conv+chunk rule+gated norm) on its first {n_seq} sequences "
+                      f"({N} tokens, lens {lens}), fp32 torch oracle, median of 3 reps ({t:.2f} s each), "
+                      f"os.cpu_count()={os.cpu_count()}, cpu='{cpu_name}'"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="1,2,3,4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the GDN path shards by value head / by sequence with no "
+              "exchange inside the kernels, so this build reports the single-GPU figure (--gpus 1).",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    import __graft_entry__ as ge
+
+    pkg = ge.load_package()
+    pkg._lib.load()
+    dev = torch.device("cuda:0")
+    K, W = args.steps, args.warmup
+    configs = {int(c) for c in args.configs.split(",") if c}
+    extra = {}
+
+    cfg1 = make_prefill(1, None)
+    N1 = cfg1["N"]
+    t1, k1 = prefill_bench(pkg, cfg1, dev, K, W)
+    chunk_us = k1["chunk_prefill"]
+    flops = chunk_flops(N1, cfg1["Hv"], cfg1["D"])
+    achieved = flops / (chunk_us * 1e-6) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "chunk_prefill_kernel<128,8>", "kernel_us": round(chunk_us, 2),
+                "algorithmic_flop_per_launch": flops}
+    kernels1 = {k: round(v, 2) for k, v in k1.items()}
+
+    if 2 in configs:
+        c2 = make_decode()
+        t2, t2g, k2 = decode_bench(pkg, c2, dev, K, W)
+        rec_us = k2["recurrent_decode"]
+        state_bytes = 2 * c2["B"] * c2["Hv"] * c2["D"] * c2["D"] * 4
+        gbps = state_bytes / (rec_us * 1e-6) / 1e9
+        extra["decode_config2"] = {
+            "ms_per_step": round(t2 * 1e3, 4), "ms_per_step_graph": round(t2g * 1e3, 4),
+            "kernels_us": {k: round(v, 2) for k, v in k2.items()},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "kernel": "recurrent_kernel<128,1>", "algorithmic_bytes_per_launch": state_bytes}}
+        del c2
+    if 3 in configs:
+        c3 = make_prefill(4, [65536], h0_std=0.1, conv_std=1.0)
+        K3 = max(2, K // 4)
+        t3, k3 = prefill_bench(pkg, c3, dev, K3, 1)
+        f3 = chunk_flops(c3["N"], c3["Hv"], c3["D"])
+        a3 = f3 / (k3["chunk_prefill"] * 1e-6) / 1e12
+        extra["long_prefill_config3"] = {
+            "tokens_per_s": round(c3["N"] / t3, 1), "ms_per_step": round(t3 * 1e3, 3), "steps": K3,
+            "kernels_us": {k: round(v, 2) for k, v in k3.items()},
+            "roofline": {"bound": "mfma", "achieved": round(a3, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(a3 / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+        del c3
+    if 4 in configs:
+        c4 = make_spec()
+        t4, k4 = spec_bench(pkg, c4, dev, K, W)
+        rb = (1 + c4["T"]) * c4["B"] * c4["Hv"] * c4["D"] * c4["D"] * 4
+        g4 = rb / (k4["recurrent_multitoken"] * 1e-6) / 1e9
+        extra["spec_verify_config4"] = {
+            "ms_per_step": round(t4 * 1e3, 4), "kernels_us": {k: round(v, 2) for k, v in k4.items()},
+            "roofline": {"bound": "hbm", "achieved": round(g4, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(g4 / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "algorithmic_bytes_per_launch": rb}}
+        del c4
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg1, 3, threads=min(16, os.cpu_count() or 1))
+
+    out = {
+        "metric": METRIC, "value": round(N1 / t1, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(t1 * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "config1: varlen GDN layer-core prefill (fused g/beta + varlen conv1d+SiLU + "
+                               "chunked gated delta rule + gated RMSNorm), 8 seqs lens~U[128,4096] seed 1",
+                   "tokens": N1, "lens": cfg1["lens"], "Hk": 16, "Hv": 16, "head_dim": 128, "chunk": 64,
+                   "conv_channels": cfg1["C"], "state": "fp32, slot pool updated in place",
+                   "precision": "bf16 in/out, fp32 state and accumulation, split-bf16 MFMA for fp32-accurate products",
+                   "parallelism": "single GPU"},
+        "kernels_us": kernels1,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    out.update(extra)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

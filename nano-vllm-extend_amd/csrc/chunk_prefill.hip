@@ -39,10 +39,10 @@ template <int D, int NW>
 struct __align__(16) ChunkSmem {
   uint16_t Kt[D][kC + 8];       // K^T of the chunk (raw bf16), row = key dim
   uint16_t Qs[kC][D + 8];       // Q of the chunk (raw bf16), row = token
+  uint16_t KrW[kC][D + 8];      // K row-major (phases 1-2), then W (phases 5-6)
   uint16_t Tp[kC][kC + 8];      // T' = T diag(beta rk e^G), bf16
   uint16_t Uh[kC][kC + 8];      // T'' = T diag(beta), hi
   uint16_t Ul[kC][kC + 8];      //                     lo
-  uint16_t W[kC][D + 8];        // W, bf16
   uint16_t Ah[kC][kC + 8];      // A_qk hi
   uint16_t Al[kC][kC + 8];      // A_qk lo
   float Lf[kC][kC + 4];         // L (fp32)
@@ -75,18 +75,24 @@ __device__ __forceinline__ s16x8_t perm_frag(const uint16_t* row32, int lg) {
   return cat44(a, b);
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float lo_half(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float hi_half(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
 // hi/lo B fragments from the C fragments of tiles (2j, 2j+1).
 __device__ __forceinline__ void split_frag(const f32x4_t& t0, const f32x4_t& t1, s16x8_t& fh, s16x8_t& fl) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint16_t h, l;
-    gdn::split_bf16(t0[i], h, l);
-    fh[i] = static_cast<short>(h);
-    fl[i] = static_cast<short>(l);
-    gdn::split_bf16(t1[i], h, l);
-    fh[4 + i] = static_cast<short>(h);
-    fl[4 + i] = static_cast<short>(l);
-  }
+  u32x4_t h, l;
+  h[0] = gdn::f2bf2(t0[0], t0[1]);
+  h[1] = gdn::f2bf2(t0[2], t0[3]);
+  h[2] = gdn::f2bf2(t1[0], t1[1]);
+  h[3] = gdn::f2bf2(t1[2], t1[3]);
+  l[0] = gdn::f2bf2(t0[0] - lo_half(h[0]), t0[1] - hi_half(h[0]));
+  l[1] = gdn::f2bf2(t0[2] - lo_half(h[1]), t0[3] - hi_half(h[1]));
+  l[2] = gdn::f2bf2(t1[0] - lo_half(h[2]), t1[1] - hi_half(h[2]));
+  l[3] = gdn::f2bf2(t1[2] - lo_half(h[3]), t1[3] - hi_half(h[3]));
+  fh = __builtin_bit_cast(s16x8_t, h);
+  fl = __builtin_bit_cast(s16x8_t, l);
 }
 
 // acc += A(16x16) B(16x16), fp32 operands in LDS, fp32 matrix cores.
@@ -112,6 +118,57 @@ __device__ __forceinline__ f32x4_t ld16_f32(const float* Cp, int ldc, int lane) 
   return r;
 }
 
+// lower-triangular 16x16 tile index j in [0, 10) -> (mt, nt), mt >= nt
+__device__ __forceinline__ void tri_tile(int j, int& mt, int& nt) {
+  mt = j >= 6 ? 3 : (j >= 3 ? 2 : (j >= 1 ? 1 : 0));
+  nt = j - (mt * (mt + 1)) / 2;
+}
+
+// Global -> register prefetch of one chunk's operands (issued a chunk ahead).
+template <int D, int NW>
+struct Prefetch {
+  static constexpr int NT = 64 * NW;
+  static constexpr int SEG = D / 8;               // 16-byte segments per row
+  static constexpr int KPRE = SEG / NW;           // K segments per lane (lane = token)
+  static constexpr int QPRE = kC * SEG / NT;      // Q segments per thread (row-major)
+  s16x8_t k[KPRE];
+  s16x8_t q[QPRE];
+  uint16_t v[16];  // one VGPR each: packing into vectors here would wait on the loads
+  float g;
+  uint16_t b;  // raw bf16 bits: converting here would force a wait on the load
+
+  // Rows past the chunk end are loaded from the last valid row (always in
+  // bounds, no branches) and zeroed only where the chunk is staged, so no
+  // instruction consumes a loaded value before the next chunk begins.
+  __device__ __forceinline__ void load(const uint16_t* qh, int64_t sq, const uint16_t* kh, int64_t sk,
+                                       const uint16_t* vh, int64_t sv, const float* gp, const uint16_t* bp,
+                                       int Hv, int h, int64_t tok0, int len, int tid, int wave, int lane,
+                                       int lg, int vcol) {
+    const int last = len - 1;
+#pragma unroll
+    for (int j = 0; j < KPRE; ++j) {
+      const int c8 = wave + NW * j;
+      k[j] = *reinterpret_cast<const s16x8_t*>(kh + (tok0 + min(lane, last)) * sk + c8 * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < QPRE; ++j) {
+      const int e = tid + NT * j;
+      const int t = e / SEG, c8 = e % SEG;
+      q[j] = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, last)) * sq + c8 * 8);
+    }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int s = 32 * kt + 8 * lg + i;
+        v[8 * kt + i] = vh[(tok0 + min(s, last)) * sv + vcol];
+      }
+    const int64_t gi = (tok0 + min(lane, last)) * Hv + h;
+    g = gp[gi];
+    b = bp[gi];
+  }
+};
+
 template <int D, int NW>
 __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
@@ -125,7 +182,9 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
   constexpr int KTD = D / 32;  // contraction steps over the key dim
   constexpr int MTD = D / 16;  // 16-row tiles over the key dim
   constexpr int LDF = kC + 4;
+  using PF = Prefetch<D, NW>;
   static_assert(NW >= 4 && D % BV == 0, "chunk kernel shape");
+  static_assert(PF::KPRE * NW == PF::SEG && PF::QPRE * NT == kC * PF::SEG, "prefetch tiling");
 
   __shared__ ChunkSmem<D, NW> sm;
 
@@ -136,16 +195,16 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
   const int r = static_cast<int>(wi / (static_cast<int64_t>(NVB) * Hv));
   const int kh = h / (Hv / Hk);
 
-  // state / output column of this lane: rows 16*mt + 4*(lane>>4) + i of S
-  const int vcol0 = vb * BV + 16 * (threadIdx.x >> 6) + (threadIdx.x & 15);
-  const int lg0 = (threadIdx.x & 63) >> 4;
-
   const int64_t bos = cu[r];
   const int64_t seqlen = cu[r + 1] - bos;
   const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
   const uint16_t* kh_ = k + static_cast<int64_t>(kh) * D;
   const uint16_t* vh = v + static_cast<int64_t>(h) * D;
   const int64_t srow = ids ? ids[r] : r;
+
+  // state / output column of this lane: rows 16*mt + 4*(lane>>4) + i of S
+  const int vcol0 = vb * BV + 16 * (threadIdx.x >> 6) + (threadIdx.x & 15);
+  const int lg0 = (threadIdx.x & 63) >> 4;
 
   // ---- state slice: S[mt] holds rows 16mt + 4lg + i, column vcol ----
   f32x4_t S[MTD];
@@ -159,6 +218,11 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
 #pragma unroll
     for (int mt = 0; mt < MTD; ++mt) S[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+
+  PF pf;
+  if (seqlen > 0)
+    pf.load(qh, sq, kh_, sk, vh, sv, g, beta, Hv, h, bos, static_cast<int>(min<int64_t>(kC, seqlen)),
+            threadIdx.x, threadIdx.x >> 6, threadIdx.x & 63, (threadIdx.x & 63) >> 4, vcol0);
 
   for (int64_t c0 = 0; c0 < seqlen; c0 += kC) {
     const int len = static_cast<int>(min<int64_t>(kC, seqlen - c0));
@@ -177,13 +241,20 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
     const int vcol = vb * BV + 16 * wave + lr;
     __syncthreads();  // previous chunk's LDS readers are done
 
-    // ---- phase 1: stage K^T, row norms, gates ----
+    // ---- phase 1: stage the prefetched chunk, row norms, gates ----
+    s16x8_t vf[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        vf[kt][i] = 32 * kt + 8 * lg + i < len ? static_cast<short>(pf.v[8 * kt + i]) : static_cast<short>(0);
     {
-      // K: lane = token row, wave strides over 8-wide key-dim segments
       float ss = 0.f;
-      for (int c8 = wave; c8 < D / 8; c8 += NW) {
-        s16x8_t kv8 = zero8();
-        if (lane < len) kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + (tok0 + lane) * sk + c8 * 8);
+#pragma unroll
+      for (int j = 0; j < PF::KPRE; ++j) {
+        const int c8 = wave + NW * j;
+        const s16x8_t kv8 = lane < len ? pf.k[j] : zero8();
+        *reinterpret_cast<s16x8_t*>(&sm.KrW[lane][c8 * 8]) = kv8;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const uint16_t bits = static_cast<uint16_t>(kv8[i]);
@@ -193,41 +264,37 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
         }
       }
       sm.ssk[wave][lane] = ss;
-      // Q: staged row-major, plus row sums of squares
-      constexpr int SEG = D / 8;
-      for (int e = tid; e < kC * SEG; e += NT) {
-        const int t = e / SEG, c8 = e % SEG;
-        float qs = 0.f;
-        s16x8_t qv8 = zero8();
-        if (t < len) {
-          qv8 = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + t) * sq + c8 * 8);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float f = gdn::bf2f(static_cast<uint16_t>(qv8[i]));
-            qs += f * f;
-          }
-        }
+      for (int j = 0; j < PF::QPRE; ++j) {
+        const int e = tid + NT * j;
+        const int t = e / PF::SEG, c8 = e % PF::SEG;
+        const s16x8_t qv8 = t < len ? pf.q[j] : zero8();
         *reinterpret_cast<s16x8_t*>(&sm.Qs[t][c8 * 8]) = qv8;
+        float qs = 0.f;
 #pragma unroll
-        for (int m = SEG / 2; m >= 1; m >>= 1) qs += __shfl_xor(qs, m, 64);
+        for (int i = 0; i < 8; ++i) {
+          const float f = gdn::bf2f(static_cast<uint16_t>(qv8[i]));
+          qs += f * f;
+        }
+#pragma unroll
+        for (int m = PF::SEG / 2; m >= 1; m >>= 1) qs += __shfl_xor(qs, m, 64);
         if (c8 == 0) sm.ssq[t] = qs;
       }
       if (wave == 0) {
-        float gv = 0.f, bv = 0.f;
-        if (lane < len) {
-          const int64_t gi = (tok0 + lane) * Hv + h;
-          gv = g[gi];
-          bv = gdn::bf2f(beta[gi]);
-        }
+        float gv = lane < len ? pf.g : 0.f;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
           const float o_ = __shfl_up(gv, d, 64);
           if (lane >= d) gv += o_;
         }
         sm.G[lane] = gv;
-        sm.bt[lane] = bv;
+        sm.bt[lane] = lane < len ? gdn::bf2f(pf.b) : 0.f;
       }
     }
+    // issue the next chunk's loads now: their latency hides behind this chunk
+    if (c0 + kC < seqlen)
+      pf.load(qh, sq, kh_, sk, vh, sv, g, beta, Hv, h, tok0 + kC,
+              static_cast<int>(min<int64_t>(kC, seqlen - c0 - kC)), tid, wave, lane, lg, vcol);
     __syncthreads();
     if (tid < kC) {
       const int t = tid;
@@ -247,54 +314,31 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
     }
     __syncthreads();
 
-    // ---- phase 2: K K^T -> L (fp32), Q K^T -> A_qk (hi/lo), lower tiles ----
-    {
-      constexpr int NJ = (20 + NW - 1) / NW;
+    // ---- phase 2a: K K^T -> L (fp32), lower-triangular tiles ----
+    for (int j = wave; j < 10; j += NW) {
+      int mt, nt;
+      tri_tile(j, mt, nt);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jj = 0; jj < NJ; ++jj) {
-        const int j = wave + NW * jj;
-        if (j >= 20) break;
-        const bool is_q = j >= 10;
-        int jt = is_q ? j - 10 : j;
-        // lower-triangular tile index -> (mt, nt)
-        int mt = 0;
-        while (jt >= mt + 1) { jt -= mt + 1; ++mt; }
-        const int nt = jt;
-        const int ta = 16 * mt + lr;
-        const int tb = 16 * nt + lr;
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      for (int kt = 0; kt < KTD; ++kt) {
+        const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * mt + lr][32 * kt + 8 * lg]);
+        const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
+        acc = gdn::mfma16x16x32(a8, b8, acc);
+      }
+      const int s = 16 * nt + lr;
+      const float rks = sm.rk[s];
+      const float Gs = sm.G[s];
 #pragma unroll
-        for (int kt = 0; kt < KTD; ++kt) {
-          s16x8_t a8;
-          if (is_q) a8 = *reinterpret_cast<const s16x8_t*>(&sm.Qs[ta][32 * kt + 8 * lg]);
-          else a8 = ta < len ? *reinterpret_cast<const s16x8_t*>(kh_ + (tok0 + ta) * sk + 32 * kt + 8 * lg) : zero8();
-          const s16x8_t b8 = tb < len ? *reinterpret_cast<const s16x8_t*>(kh_ + (tok0 + tb) * sk + 32 * kt + 8 * lg) : zero8();
-          acc = gdn::mfma16x16x32(a8, b8, acc);
-        }
-        const int s = 16 * nt + lr;
-        const float rks = sm.rk[s];
-        const float Gs = sm.G[s];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = 16 * mt + 4 * lg + i;
-          const float decay = expf(sm.G[t] - Gs);
-          if (!is_q) {
-            sm.Lf[t][s] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * decay : 0.f;
-          } else {
-            const float a = s <= t ? acc[i] * sm.rq[t] * scale * rks * decay : 0.f;
-            uint16_t hi, lo;
-            gdn::split_bf16(a, hi, lo);
-            sm.Ah[t][s] = hi;
-            sm.Al[t][s] = lo;
-          }
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * mt + 4 * lg + i;
+        sm.Lf[t][s] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * expf(sm.G[t] - Gs) : 0.f;
       }
     }
     __syncthreads();
 
-    // ---- phase 3: T = (I + L)^-1, blocked 16x16, fp32 ----
+    // ---- phase 2b / solve step 1: wave 0 inverts the diagonal blocks while
+    //      the other waves form A_qk = lower(Q K^T) (hi/lo) ----
     if (wave == 0) {
-      // diagonal blocks by forward substitution: lane -> (block, column)
       const int bb = lane >> 4, c = lane & 15, base = 16 * bb;
       float x[16];
 #pragma unroll
@@ -313,6 +357,30 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
       }
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) sm.Tf[base + rr][base + c] = x[rr];
+    } else {
+      for (int j = wave - 1; j < 10; j += NW - 1) {
+        int mt, nt;
+        tri_tile(j, mt, nt);
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kt = 0; kt < KTD; ++kt) {
+          const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Qs[16 * mt + lr][32 * kt + 8 * lg]);
+          const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
+          acc = gdn::mfma16x16x32(a8, b8, acc);
+        }
+        const int s = 16 * nt + lr;
+        const float rks = sm.rk[s] * scale;
+        const float Gs = sm.G[s];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * mt + 4 * lg + i;
+          const float a = s <= t ? acc[i] * sm.rq[t] * rks * expf(sm.G[t] - Gs) : 0.f;
+          uint16_t hi, lo;
+          gdn::split_bf16(a, hi, lo);
+          sm.Ah[t][s] = hi;
+          sm.Al[t][s] = lo;
+        }
+      }
     }
     __syncthreads();
     // first sub-diagonal: T(j+1, j) = -T(j+1,j+1) L(j+1,j) T(j,j)
@@ -368,24 +436,34 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
     }
     __syncthreads();
 
-    // ---- phase 4: T' (bf16) and T'' (hi/lo); zero the upper tiles of A_qk ----
-    for (int e = tid; e < kC * kC; e += NT) {
-      const int t = e >> 6, s = e & 63;
-      const bool lower = (s >> 4) <= (t >> 4);
-      const float tv = lower ? sm.Tf[t][s] : 0.f;
-      sm.Tp[t][s] = gdn::f2bf(tv * sm.cW[s]);
-      uint16_t hi, lo;
-      gdn::split_bf16(tv * sm.bt[s], hi, lo);
-      sm.Uh[t][s] = hi;
-      sm.Ul[t][s] = lo;
+    // ---- phase 4: T' (bf16) and T'' (hi/lo), 4 columns per thread; zero the
+    //      upper tiles of A_qk ----
+    for (int e4 = tid; e4 < kC * (kC / 4); e4 += NT) {
+      const int t = e4 >> 4, s0 = (e4 & 15) * 4;
+      const bool lower = (s0 >> 4) <= (t >> 4);
+      float4 tv = lower ? *reinterpret_cast<const float4*>(&sm.Tf[t][s0]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 cw = *reinterpret_cast<const float4*>(&sm.cW[s0]);
+      const float4 cb = *reinterpret_cast<const float4*>(&sm.bt[s0]);
+      uint2 tp;
+      tp.x = gdn::f2bf2(tv.x * cw.x, tv.y * cw.y);
+      tp.y = gdn::f2bf2(tv.z * cw.z, tv.w * cw.w);
+      *reinterpret_cast<uint2*>(&sm.Tp[t][s0]) = tp;
+      const float u0 = tv.x * cb.x, u1 = tv.y * cb.y, u2 = tv.z * cb.z, u3 = tv.w * cb.w;
+      uint2 uh, ul;
+      uh.x = gdn::f2bf2(u0, u1);
+      uh.y = gdn::f2bf2(u2, u3);
+      ul.x = gdn::f2bf2(u0 - lo_half(uh.x), u1 - hi_half(uh.x));
+      ul.y = gdn::f2bf2(u2 - lo_half(uh.y), u3 - hi_half(uh.y));
+      *reinterpret_cast<uint2*>(&sm.Uh[t][s0]) = uh;
+      *reinterpret_cast<uint2*>(&sm.Ul[t][s0]) = ul;
       if (!lower) {
-        sm.Ah[t][s] = 0;
-        sm.Al[t][s] = 0;
+        *reinterpret_cast<uint2*>(&sm.Ah[t][s0]) = make_uint2(0u, 0u);
+        *reinterpret_cast<uint2*>(&sm.Al[t][s0]) = make_uint2(0u, 0u);
       }
     }
     __syncthreads();
 
-    // ---- phase 5: W = T' K (shared by all waves, to LDS) ----
+    // ---- phase 5: W = T' K (shared by all waves; overwrites K row-major) ----
     {
       constexpr int NJ = (4 * MTD + NW - 1) / NW;
 #pragma unroll
@@ -401,22 +479,10 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
           acc = gdn::mfma16x16x32(a8, b8, acc);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm.W[16 * mt + 4 * lg + i][16 * nt + lr] = gdn::f2bf(acc[i]);
-      }
-    }
-    // V fragments of this wave's columns (contraction over tokens), issued
-    // before the barrier so their latency overlaps the wait.
-    s16x8_t vf[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int s = 32 * kt + 8 * lg + i;
-        vf[kt][i] = s < len ? static_cast<short>(vh[(tok0 + s) * sv + vcol]) : static_cast<short>(0);
+        for (int i = 0; i < 4; ++i) sm.KrW[16 * mt + 4 * lg + i][16 * nt + lr] = gdn::f2bf(acc[i]);
       }
     }
     __syncthreads();
-
     // ---- phase 6: per-wave state chain (registers only) ----
     {
       // W S and Q S with S split hi/lo per contraction step (key dim)
@@ -432,7 +498,7 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
         split_frag(S[2 * kt], S[2 * kt + 1], sh, sl);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-          const s16x8_t wa = perm_frag(&sm.W[16 * mt + lr][32 * kt], lg);
+          const s16x8_t wa = perm_frag(&sm.KrW[16 * mt + lr][32 * kt], lg);
           const s16x8_t qa = perm_frag(&sm.Qs[16 * mt + lr][32 * kt], lg);
           ws[mt] = gdn::mfma16x16x32(wa, sh, ws[mt]);
           ws[mt] = gdn::mfma16x16x32(wa, sl, ws[mt]);

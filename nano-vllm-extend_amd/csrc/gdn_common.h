@@ -10,16 +10,25 @@
 
 namespace gdn {
 
-// ---- bf16 <-> fp32 (bit exact with torch: round-to-nearest-even, quiet NaN) ----
+// ---- bf16 <-> fp32 ----
+// float -> bf16 uses the gfx950 hardware conversion (v_cvt_pk_bf16_f32,
+// round-to-nearest-even), which matches torch's rounding for every non-NaN
+// value.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float bf2f(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// two conversions in one instruction: low half = a, high half = b
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // hi/lo split of an fp32 value into two bf16 terms: x ~= hi + lo with

@@ -19,6 +19,7 @@ directly (no gather / scatter copies).
 """
 from __future__ import annotations
 
+import contextlib
 import os
 from dataclasses import dataclass
 
@@ -71,12 +72,24 @@ class GatedDeltaNetCore:
         self.conv_w = conv_weight.reshape(self.conv_dim, self.K)
         self.A_log, self.dt_bias, self.norm_w, self.eps = A_log, dt_bias, norm_weight, eps
         self.sw = switches or Switches.from_env()
+        # Optional per-kernel timer: an object with start(name) / stop(name)
+        # that records device events on the current stream (bench.py).
+        self.timer = None
         if not self.sw.fla_chunk:
             raise NotImplementedError("FLA_CHUNK=0 selects the reference's pure-torch chunk port, "
                                       "which is not part of this build")
         if not self.sw.inplace and not self.sw.fla_recurrent:
             raise NotImplementedError("FLA_RECURRENT=0 selects the reference's pure-torch recurrent "
                                       "port, which is not part of this build")
+
+    @contextlib.contextmanager
+    def _timed(self, name: str):
+        if self.timer is None:
+            yield
+            return
+        self.timer.start(name)
+        yield
+        self.timer.stop(name)
 
     def _to(self, dev):
         if self.conv_w.device != dev:
@@ -88,7 +101,8 @@ class GatedDeltaNetCore:
     # ---------------------------------------------------------------- gates --
     def _g_beta(self, b, a, mask):
         if self.sw.gbeta:
-            return ops.fused_g_beta(b, a, self.A_log, self.dt_bias, mask)
+            with self._timed("g_beta"):
+                return ops.fused_g_beta(b, a, self.A_log, self.dt_bias, mask)
         beta = b.sigmoid()
         g = -self.A_log.float().exp() * F.softplus(a.float() + self.dt_bias.float())
         if mask is not None:
@@ -96,7 +110,8 @@ class GatedDeltaNetCore:
         return g, beta
 
     def _norm(self, core, z):
-        return ops.rms_norm_gated(core, z, self.norm_w, self.eps)
+        with self._timed("rmsnorm_gated"):
+            return ops.rms_norm_gated(core, z, self.norm_w, self.eps)
 
     # --------------------------------------------------------------- decode --
     def decode(self, mixed, z, b, a, ids, conv_cache, s_cache):
@@ -108,7 +123,8 @@ class GatedDeltaNetCore:
         Hk, Hv, D = self.Hk, self.Hv, self.D
         g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
         if self.sw.conv_kernel:
-            y = ops.conv_decode_step(mixed, conv_cache, ids, self.conv_w)
+            with self._timed("conv_decode"):
+                y = ops.conv_decode_step(mixed, conv_cache, ids, self.conv_w)
         else:
             window = torch.cat([conv_cache[ids], mixed.unsqueeze(-1)], dim=-1)
             conv_cache[ids] = window[..., 1:]
@@ -119,7 +135,8 @@ class GatedDeltaNetCore:
         v = y[:, 2 * kd:].view(B, 1, Hv, D)
         g1, b1 = g.view(B, 1, Hv), beta.view(B, 1, Hv)
         if self.sw.inplace:
-            out = ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_cache, ids)
+            with self._timed("recurrent_decode"):
+                out = ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_cache, ids)
         else:
             out, new_s = ops.recurrent_gated_delta_rule(q, k, v, g1, b1, s_cache[ids])
             s_cache[ids] = new_s
@@ -136,13 +153,15 @@ class GatedDeltaNetCore:
         g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
         cu_gpu, lens_gpu, _, cu64_gpu = varlen_meta(lens_q, mixed.device)
         if self.sw.conv_kernel:
-            q, k, v = ops.causal_conv_silu_varlen_parts(mixed, conv_cache, self.conv_w, lens_gpu, cu_gpu[:-1],
-                                                        self.key_dim, state_ids=ids)
+            with self._timed("conv_varlen"):
+                q, k, v = ops.causal_conv_silu_varlen_parts(mixed, conv_cache, self.conv_w, lens_gpu, cu_gpu[:-1],
+                                                            self.key_dim, state_ids=ids)
         else:
             q, k, v = self._conv_varlen_eager(mixed, lens_q, ids, conv_cache)
-        o, _ = ops.chunk_gated_delta_rule_varlen(q.view(N, Hk, D), k.view(N, Hk, D), v.view(N, Hv, D),
-                                                 g, beta, cu64_gpu, s_cache, state_ids=ids,
-                                                 final_state=s_cache)
+        with self._timed("chunk_prefill"):
+            o, _ = ops.chunk_gated_delta_rule_varlen(q.view(N, Hk, D), k.view(N, Hk, D), v.view(N, Hv, D),
+                                                     g, beta, cu64_gpu, s_cache, state_ids=ids,
+                                                     final_state=s_cache)
         return self._norm(o, z.view(N, Hv, D))
 
     def _conv_varlen_eager(self, mixed, lens_q, ids, conv_cache):
