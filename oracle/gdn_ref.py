@@ -64,17 +64,17 @@ def conv_silu_window(window: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
 
 def conv_varlen(x: torch.Tensor, state: torch.Tensor, w: torch.Tensor, lens: list[int]):
     """Varlen causal conv + SiLU (nanovllm/models/qwen3_5.py:402-456).
-    x [N, C] bf16, state [n, C, K-1] bf16, w [C, K] bf16.
-    Returns (y [N, C] bf16, new_state [n, C, K-1] bf16)."""
+    x [N, C], state [n, C, K-1], w [C, K] (bf16 in the model; any float dtype).
+    Returns (y [N, C] in x's dtype, new_state [n, C, K-1])."""
     N, C = x.shape
     K = w.shape[-1]
-    y = torch.empty(N, C, dtype=BF16)
+    y = torch.empty(N, C, dtype=x.dtype)
     new_state = state.clone()
     off = 0
     for r, T in enumerate(lens):
         xs = x[off:off + T].float().t()                              # [C, T]
         window = torch.cat([state[r].float(), xs], dim=1)            # [C, K-1+T]
-        y[off:off + T] = conv_silu_window(window, w.float()).t().to(BF16)
+        y[off:off + T] = conv_silu_window(window, w.float()).t().to(x.dtype)
         raw = torch.cat([state[r], x[off:off + T].t()], dim=1)       # bf16 bits
         new_state[r] = _roll_bits(raw[:, T:T + K - 1])
         off += T
@@ -84,31 +84,31 @@ def conv_varlen(x: torch.Tensor, state: torch.Tensor, w: torch.Tensor, lens: lis
 def conv_decode(x: torch.Tensor, pool: torch.Tensor, ids: list[int], w: torch.Tensor):
     """Single-token conv + SiLU with in-place roll (qwen3_5.py:515-543):
     y = silu(x*w[K-1] + sum_i s[i]*w[i]); s <- [s1, s2, x] (bit copies).
-    Returns (y [B, C] bf16, new_pool)."""
+    Returns (y [B, C] in x's dtype, new_pool)."""
     B, C = x.shape
     K = w.shape[-1]
     pool = pool.clone()
-    y = torch.empty(B, C, dtype=BF16)
+    y = torch.empty(B, C, dtype=x.dtype)
     for b, slot in enumerate(ids):
         s = pool[slot].float()                                        # [C, K-1]
         acc = x[b].float() * w[:, K - 1].float()
         for i in range(K - 1):
             acc = acc + s[:, i] * w[:, i].float()
-        y[b] = (acc * torch.sigmoid(acc)).to(BF16)
+        y[b] = (acc * torch.sigmoid(acc)).to(x.dtype)
         pool[slot] = torch.cat([pool[slot][:, 1:], x[b].unsqueeze(1)], dim=1)
     return y, pool
 
 
 def conv_padded(x: torch.Tensor, state: torch.Tensor, w: torch.Tensor, endp: list[int]):
     """Padded conv + SiLU with per-row writeback at endp (qwen3_5.py:249-297).
-    x [n, C, T] bf16.  Returns (y [n, C, T] bf16, new_state)."""
+    x [n, C, T].  Returns (y [n, C, T] in x's dtype, new_state)."""
     n, C, T = x.shape
     K = w.shape[-1]
-    y = torch.empty(n, C, T, dtype=BF16)
+    y = torch.empty(n, C, T, dtype=x.dtype)
     new_state = state.clone()
     for r in range(n):
         window = torch.cat([state[r].float(), x[r].float()], dim=1)
-        y[r] = conv_silu_window(window, w.float()).to(BF16)
+        y[r] = conv_silu_window(window, w.float()).to(x.dtype)
         e = endp[r]
         if e >= 0:
             raw = torch.cat([state[r], x[r]], dim=1)
@@ -219,13 +219,15 @@ def recurrent_rule(q, k, v, g, beta, h0=None, scale=None, use_l2norm=True, keep_
 
 # -------------------------------------------------------------- gated norm --
 def rms_norm_gated(x: torch.Tensor, z: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    """Eager order of _rms_gated_forward (qwen3_5.py:121-131): bf16 inputs,
-    fp32 norm rounded to bf16, bf16 weight product, fp32 silu gate, bf16 out."""
+    """Eager order of _rms_gated_forward (qwen3_5.py:121-131) in the input
+    dtype (bf16 in the model): fp32 norm rounded to the input dtype, weight
+    product in the input dtype, fp32 silu gate, output in the input dtype."""
+    dt = x.dtype
     xf = x.float()
     var = xf.pow(2).mean(-1, keepdim=True)
-    n = (xf * torch.rsqrt(var + eps)).to(BF16)
-    wn = (w.to(BF16) * n)                                              # bf16 x bf16 -> bf16
-    return (wn.float() * F.silu(z.float())).to(BF16)
+    n = (xf * torch.rsqrt(var + eps)).to(dt)
+    wn = w.to(dt) * n
+    return (wn.float() * F.silu(z.float())).to(dt)
 
 
 # ------------------------------------------------------------ layer core --

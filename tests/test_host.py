@@ -1,0 +1,97 @@
+"""Host-side logic of the package: slot bookkeeping, varlen metadata, A/B
+switches, the reference-module install hook, and the no-CPU-path rule.
+CPU only."""
+import os
+import subprocess
+import sys
+import types
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_linear_state_pool_alloc_free_reuse(pkg):
+    pool = pkg.LinearStatePool(3)
+    a, b, c = pool.alloc(), pool.alloc(), pool.alloc()
+    assert (a, b, c) == (0, 1, 2) and pool.num_free == 0
+    with pytest.raises(AssertionError):
+        pool.alloc()
+    pool.free(b)
+    assert pool.num_free == 1 and pool.alloc() == b       # freed slot is reused
+
+
+def test_state_pools_layout_dummy_slot_and_reset(pkg):
+    pools = pkg.allocate_state_pools(4, L=3, H=2, K=8, V=8, conv_dim=24, conv_kernel=4, device="cpu")
+    assert pools.s_pool.shape == (5, 3, 2, 8, 8) and pools.s_pool.dtype == torch.float32
+    assert pools.conv_pool.shape == (5, 3, 24, 3) and pools.conv_pool.dtype == torch.bfloat16
+    assert pools.dummy_slot == 4
+    s1, c1 = pools.layer(1)
+    # per-layer views: slot stride spans all layers, heads/rows dense
+    assert s1.stride(0) == 3 * 2 * 8 * 8 and s1.stride(1) == 64 and s1.stride(3) == 1
+    assert c1.stride(0) == 3 * 24 * 3 and c1.stride(1) == 3
+    pools.s_pool.fill_(1.0)
+    pools.conv_pool.fill_(1.0)
+    pkg.reset_linear_states(pools, torch.tensor([2]))
+    assert torch.all(pools.s_pool[2] == 0) and torch.all(pools.conv_pool[2] == 0)
+    assert torch.all(pools.s_pool[[0, 1, 3, 4]] == 1)
+
+
+def test_varlen_meta_cached(pkg):
+    m1 = pkg.varlen_meta([3, 5, 2], "cpu")
+    cu, lens, cu64_cpu, cu64 = m1
+    assert cu.tolist() == [0, 3, 8, 10] and lens.tolist() == [3, 5, 2]
+    assert cu.dtype == torch.int32 and cu64.dtype == torch.int64 and cu64_cpu.tolist() == [0, 3, 8, 10]
+    assert pkg.varlen_meta([3, 5, 2], "cpu") is m1        # reused by every layer of the step
+
+
+def test_switches_from_env(pkg, monkeypatch):
+    monkeypatch.setenv("NANOVLLM_GDN_GBETA", "0")
+    monkeypatch.setenv("NANOVLLM_GDN_VARLEN", "0")
+    sw = pkg.Switches.from_env()
+    assert not sw.gbeta and not sw.varlen and sw.inplace and sw.conv_kernel
+    monkeypatch.setenv("FLA_CHUNK", "0")
+    w = torch.zeros(3 * 2 * 64, 4, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        pkg.GatedDeltaNetCore(2, 2, 64, w, torch.zeros(2), torch.zeros(2), torch.ones(64))
+
+
+def test_install_rebinds_reference_call_sites(pkg):
+    mod = types.ModuleType("qwen3_5_stub")
+    mod.fused_g_beta = mod.conv_decode_step = lambda *a: None
+    mod._HAS_FLA = False
+    prev = pkg.integration.install(mod)
+    assert mod.fused_g_beta is pkg.ops.fused_g_beta
+    assert mod.causal_conv_silu_varlen is pkg.ops.causal_conv_silu_varlen
+    assert mod.recurrent_gdn_inplace is pkg.ops.recurrent_gdn_inplace
+    assert mod._fla_chunk is pkg.ops.chunk_gated_delta_rule and mod._HAS_FLA
+    assert mod._rms_gated_forward is pkg.ops.rms_norm_gated
+    pkg.integration.uninstall(mod, prev)
+    assert mod._HAS_FLA is False
+
+
+def test_ops_have_no_cpu_path(pkg):
+    a = torch.zeros(4, 2, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        pkg.ops.fused_g_beta(a, a, torch.zeros(2), torch.zeros(2), None)
+    x = torch.zeros(2, 1, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        pkg.ops.recurrent_gated_delta_rule(x, x, x, g=torch.zeros(2, 1, 2), beta=torch.zeros(2, 1, 2,
+                                           dtype=torch.bfloat16))
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    code = ("import os, sys; sys.path.insert(0, %r); os.environ['GDN_MI355X_LIB'] = %r\n"
+            "import __graft_entry__ as ge\npkg = ge.load_package()\n"
+            "try:\n    pkg._lib.load()\nexcept pkg._lib.GDNLibraryError as e:\n    print('LOUD', e)\n"
+            % (str(ROOT), str(tmp_path / "missing.so")))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert "LOUD" in r.stdout, r.stderr
