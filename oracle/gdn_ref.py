@@ -50,19 +50,24 @@ def _roll_bits(x: torch.Tensor) -> torch.Tensor:
     return (x.float() + 0.0).to(x.dtype)
 
 
-def conv_silu_window(window: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+def conv_silu_window(window: torch.Tensor, w: torch.Tensor, eager_dtype=None) -> torch.Tensor:
     """window [C, K-1+T] fp32 (state then inputs), w [C, K] -> silu(conv) [C, T].
-    y[c,t] = silu(sum_i w[c,i] * window[c, t+i]) (qwen3_5.py:286-292)."""
+    y[c,t] = silu(sum_i w[c,i] * window[c, t+i]) (qwen3_5.py:286-292).
+    eager_dtype (e.g. bf16) restates the eager F.silu(F.conv1d(...)) chain of
+    the NANOVLLM_CONV_TRITON=0 path (qwen3_5.py:1020-1024, :1057-1065): the
+    conv sum is rounded to that dtype before the SiLU."""
     C, L = window.shape
     K = w.shape[1]
     T = L - (K - 1)
     acc = torch.zeros(C, T, dtype=torch.float32)
     for i in range(K):
         acc += window[:, i:i + T] * w[:, i:i + 1].float()
+    if eager_dtype is not None:
+        acc = acc.to(eager_dtype).float()
     return acc * torch.sigmoid(acc)
 
 
-def conv_varlen(x: torch.Tensor, state: torch.Tensor, w: torch.Tensor, lens: list[int]):
+def conv_varlen(x: torch.Tensor, state: torch.Tensor, w: torch.Tensor, lens: list[int], eager: bool = False):
     """Varlen causal conv + SiLU (nanovllm/models/qwen3_5.py:402-456).
     x [N, C], state [n, C, K-1], w [C, K] (bf16 in the model; any float dtype).
     Returns (y [N, C] in x's dtype, new_state [n, C, K-1])."""
@@ -74,14 +79,14 @@ def conv_varlen(x: torch.Tensor, state: torch.Tensor, w: torch.Tensor, lens: lis
     for r, T in enumerate(lens):
         xs = x[off:off + T].float().t()                              # [C, T]
         window = torch.cat([state[r].float(), xs], dim=1)            # [C, K-1+T]
-        y[off:off + T] = conv_silu_window(window, w.float()).t().to(x.dtype)
+        y[off:off + T] = conv_silu_window(window, w.float(), x.dtype if eager else None).t().to(x.dtype)
         raw = torch.cat([state[r], x[off:off + T].t()], dim=1)       # bf16 bits
-        new_state[r] = _roll_bits(raw[:, T:T + K - 1])
+        new_state[r] = raw[:, T:T + K - 1] if eager else _roll_bits(raw[:, T:T + K - 1])
         off += T
     return y, new_state
 
 
-def conv_decode(x: torch.Tensor, pool: torch.Tensor, ids: list[int], w: torch.Tensor):
+def conv_decode(x: torch.Tensor, pool: torch.Tensor, ids: list[int], w: torch.Tensor, eager: bool = False):
     """Single-token conv + SiLU with in-place roll (qwen3_5.py:515-543):
     y = silu(x*w[K-1] + sum_i s[i]*w[i]); s <- [s1, s2, x] (bit copies).
     Returns (y [B, C] in x's dtype, new_pool)."""
@@ -94,6 +99,8 @@ def conv_decode(x: torch.Tensor, pool: torch.Tensor, ids: list[int], w: torch.Te
         acc = x[b].float() * w[:, K - 1].float()
         for i in range(K - 1):
             acc = acc + s[:, i] * w[:, i].float()
+        if eager:
+            acc = acc.to(x.dtype).float()
         y[b] = (acc * torch.sigmoid(acc)).to(x.dtype)
         pool[slot] = torch.cat([pool[slot][:, 1:], x[b].unsqueeze(1)], dim=1)
     return y, pool
@@ -232,14 +239,14 @@ def rms_norm_gated(x: torch.Tensor, z: torch.Tensor, w: torch.Tensor, eps: float
 
 # ------------------------------------------------------------ layer core --
 def gdn_core_varlen(mixed, z, b, a, lens, conv_state, h0, conv_w, A_log, dt_bias, norm_w,
-                    Hk, Hv, D, eps=1e-6):
+                    Hk, Hv, D, eps=1e-6, conv_eager=False):
     """The GDN layer between its projections for one varlen prefill group
     (qwen3_5.py:922-965 without in_proj / out_proj): g/beta, conv + SiLU,
     chunk rule with initial states, gated norm.
     Returns (core [N, Hv, D] bf16, new conv states, final states)."""
     N = mixed.shape[0]
     g, beta = g_beta(b, a, A_log, dt_bias)
-    y, new_conv = conv_varlen(mixed, conv_state, conv_w, lens)
+    y, new_conv = conv_varlen(mixed, conv_state, conv_w, lens, eager=conv_eager)
     kd = Hk * D
     qh = y[:, :kd].reshape(N, Hk, D)
     kh = y[:, kd:2 * kd].reshape(N, Hk, D)
@@ -253,13 +260,13 @@ def gdn_core_varlen(mixed, z, b, a, lens, conv_state, h0, conv_w, A_log, dt_bias
 
 
 def gdn_core_decode(mixed, z, b, a, ids, conv_pool, s_pool, conv_w, A_log, dt_bias, norm_w,
-                    Hk, Hv, D, eps=1e-6):
+                    Hk, Hv, D, eps=1e-6, conv_eager=False):
     """One decode step of the GDN layer core against the slot pools
     (qwen3_5.py:967-1030, T = 1, in-place path).
     Returns (core [B, Hv, D] bf16, new conv pool, new state pool)."""
     B = mixed.shape[0]
     g, beta = g_beta(b, a, A_log, dt_bias)
-    y, conv_pool = conv_decode(mixed, conv_pool, ids, conv_w)
+    y, conv_pool = conv_decode(mixed, conv_pool, ids, conv_w, eager=conv_eager)
     kd = Hk * D
     q = y[:, :kd].reshape(B, 1, Hk, D)
     k = y[:, kd:2 * kd].reshape(B, 1, Hk, D)

@@ -9,9 +9,17 @@ BF16 = torch.bfloat16
 
 # Tolerances of the north-star contract: bf16 outputs max-abs 2e-2 and
 # mean-rel 1e-3; fp32 final states rel (Frobenius) 1e-3; bookkeeping exact.
+# The max-abs bound is applied per element as max(2e-2, `ulps` bf16 ulps of
+# the reference value): for |y| >= 2.56 a single rounding flip of a bf16
+# output already exceeds 2e-2, whatever computed it.  Kernel outputs use one
+# ulp.  Gated-norm (layer) outputs use four: one from a flip of the norm's
+# bf16 input plus the norm's own three roundings (n, w*n, y); such elements
+# must also stay rare (fraction beyond one ulp < 1e-4), so a systematic error
+# cannot hide in the budget.
 OUT_MAX_ABS = 2e-2
 OUT_MEAN_REL = 1e-3
 STATE_REL = 1e-3
+BF16_ULP_REL = 2.0 ** -7
 
 
 def max_abs(a, b) -> float:
@@ -30,9 +38,22 @@ def state_rel(a, b) -> float:
     return (a - b).norm().item() / den if den > 0 else (a - b).norm().item()
 
 
-def assert_out(a, b, tag=""):
-    ma, mr = max_abs(a, b), mean_rel(a, b)
-    assert ma <= OUT_MAX_ABS and mr <= OUT_MEAN_REL, f"{tag}: max-abs {ma:.3e}, mean-rel {mr:.3e}"
+def excess_abs(a, b, ulps: int = 1) -> float:
+    """Largest |a - b| beyond the per-element bound max(2e-2, ulps * bf16 ulp of b)."""
+    a, b = a.float().cpu(), b.float().cpu()
+    if not a.numel():
+        return 0.0
+    bound = torch.clamp(b.abs() * (ulps * BF16_ULP_REL), min=OUT_MAX_ABS)
+    return ((a - b).abs() - bound).max().item()
+
+
+def assert_out(a, b, tag="", ulps: int = 1):
+    ma, mr, ex = max_abs(a, b), mean_rel(a, b), excess_abs(a, b, ulps)
+    assert ex <= 0 and mr <= OUT_MEAN_REL, f"{tag}: max-abs {ma:.3e} (excess over bound {ex:.3e}), mean-rel {mr:.3e}"
+    if ulps > 1:
+        af, bf = a.float().cpu(), b.float().cpu()
+        far = ((af - bf).abs() > torch.clamp(bf.abs() * BF16_ULP_REL, min=OUT_MAX_ABS)).float().mean().item()
+        assert far < 1e-4, f"{tag}: {far:.2e} of elements beyond one ulp"
 
 
 def assert_state(a, b, tag=""):

@@ -1,0 +1,246 @@
+"""GPU parity of the GDN layer core (GatedDeltaNetCore) and of the BASELINE
+configs at full size, against the CPU oracle; plus the reference's stress
+invariants restated at kernel level (nanovllm tests/stress_qwen35.py:63-78):
+graph == eager, chunked prefill == one-shot, batched == solo, and
+prefill-then-decode == a longer prefill."""
+import pytest
+import torch
+
+import bench
+from helpers import BF16, assert_out, assert_state, state_rel
+from oracle import gdn_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(gen, Hk, Hv, D):
+    import math
+    C = 2 * Hk * D + Hv * D
+    conv_w = (torch.randn(C, 4, generator=gen) * 0.5).to(BF16)
+    A_log = (torch.rand(Hv, generator=gen) * math.log(16)).to(BF16)
+    dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(BF16)
+    norm_w = (1 + 0.02 * torch.randn(D, generator=gen)).to(BF16)
+    return C, conv_w, A_log, dt_bias, norm_w
+
+
+def _rows(gen, N, C, Hv, D):
+    return (torch.randn(N, C, generator=gen).to(BF16), torch.randn(N, Hv * D, generator=gen).to(BF16),
+            torch.randn(N, Hv, generator=gen).to(BF16), torch.randn(N, Hv, generator=gen).to(BF16))
+
+
+def _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w, **sw):
+    switches = pkg.Switches(**sw) if sw else pkg.Switches()
+    return pkg.GatedDeltaNetCore(Hk, Hv, D, conv_w.to(dev), A_log.to(dev), dt_bias.to(dev), norm_w.to(dev),
+                                 switches=switches)
+
+
+SWITCH_SETS = [
+    {},
+    {"gbeta": False},
+    {"conv_kernel": False},
+    {"inplace": False},
+    {"varlen": False},
+]
+
+
+@pytest.mark.parametrize("sw", SWITCH_SETS, ids=lambda s: ",".join(f"{k}={v}" for k, v in s.items()) or "default")
+@pytest.mark.parametrize("Hk,Hv", [(4, 4), (2, 4)])
+def test_layer_forward_mixed_batch(pkg, dev, sw, Hk, Hv):
+    """Decode prefix (lens == 1) + varlen prefill rows in one step, pools indexed by slot."""
+    gen = torch.Generator().manual_seed(31)
+    D = 128
+    C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
+    lens = [1, 1, 1, 70, 3, 200, 64]
+    N = sum(lens)
+    mixed, z, b, a = _rows(gen, N, C, Hv, D)
+    slots = 12
+    conv_pool = torch.randn(slots, C, 3, generator=gen).to(BF16)
+    s_pool = torch.randn(slots, Hv, D, D, generator=gen) * 0.1
+    ids = torch.tensor([9, 2, 7, 0, 5, 11, 3])
+    # oracle: decode rows, then the varlen prefill group, each on its slots
+    ref_conv, ref_s = conv_pool.clone(), s_pool.clone()
+    eager = sw.get("conv_kernel") is False        # eager F.conv1d chain: bf16 rounding before SiLU
+    core_d, ref_conv, ref_s = gdn_ref.gdn_core_decode(mixed[:3], z[:3], b[:3], a[:3], ids[:3].tolist(), ref_conv,
+                                                      ref_s, conv_w, A_log, dt_bias, norm_w, Hk, Hv, D,
+                                                      conv_eager=eager)
+    pids = ids[3:]
+    core_p, new_conv, new_s = gdn_ref.gdn_core_varlen(mixed[3:], z[3:], b[3:], a[3:], lens[3:], ref_conv[pids],
+                                                      ref_s[pids], conv_w, A_log, dt_bias, norm_w, Hk, Hv, D,
+                                                      conv_eager=eager)
+    ref_conv[pids], ref_s[pids] = new_conv, new_s
+    ref = torch.cat([core_d.reshape(3, -1), core_p.reshape(N - 3, -1)])
+
+    core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w, **sw)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+    cp, sp = conv_pool.to(dev), s_pool.to(dev)
+    out = core.forward(mixed.to(dev), z.to(dev), b.to(dev), a.to(dev), cu, max(lens), ids.to(dev), cp, sp,
+                       lens_q=lens)
+    assert out.shape == (N, Hv * D)
+    assert_out(out.cpu(), ref, "layer forward", ulps=4)
+    assert torch.equal(cp.cpu(), ref_conv), "conv pool bookkeeping"
+    assert_state(sp.cpu(), ref_s, "state pool")
+    untouched = [i for i in range(slots) if i not in ids.tolist()]
+    assert torch.equal(sp.cpu()[untouched], s_pool[untouched])
+
+
+def test_decode_graph_replay_equals_eager(pkg, dev):
+    """The decode step captured in a HIP graph and replayed, with eager work
+    in between, matches the eager step bit for bit on every replay."""
+    gen = torch.Generator().manual_seed(32)
+    Hk = Hv = 16
+    D, B, slots = 128, 48, 64
+    C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
+    mixed, z, b, a = (t.to(dev) for t in _rows(gen, B, C, Hv, D))
+    ids = torch.full((B,), slots - 1, dtype=torch.int64)         # pad rows -> dummy slot
+    ids[:-8] = torch.randperm(slots - 1, generator=gen)[:B - 8]  # real rows: distinct live slots
+    ids = ids.to(dev)
+    conv0 = torch.randn(slots, C, 3, generator=gen).to(BF16).to(dev)
+    s0 = (torch.randn(slots, Hv, D, D, generator=gen) * 0.1).to(dev)
+    core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w)
+    cg, sg = conv0.clone(), s0.clone()
+    ce, se = conv0.clone(), s0.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        core.decode(mixed, z, b, a, ids, cg, sg)                  # warm-up (also on the eager copy)
+    torch.cuda.current_stream().wait_stream(stream)
+    core.decode(mixed, z, b, a, ids, ce, se)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out_g = core.decode(mixed, z, b, a, ids, cg, sg)
+    real = ids[:-8]
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        out_e = core.decode(mixed, z, b, a, ids, ce, se)
+        _ = (mixed.float() * 2).sum()                            # unrelated eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out_g[:-8], out_e[:-8]), f"replay {rep}: outputs differ"
+        assert torch.equal(sg[real], se[real]), f"replay {rep}: state pool differs"
+        assert torch.equal(cg[real], ce[real]), f"replay {rep}: conv pool differs"
+
+
+def test_chunked_prefill_equals_one_shot_and_batched_equals_solo(pkg, dev):
+    gen = torch.Generator().manual_seed(33)
+    Hk = Hv = 4
+    D = 128
+    C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
+    lens = [300, 77, 129]
+    N = sum(lens)
+    mixed, z, b, a = (t.to(dev) for t in _rows(gen, N, C, Hv, D))
+    core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w)
+    slots = 4
+    ids = torch.tensor([2, 0, 3], device=dev)
+    # one shot, batched
+    cp1 = torch.zeros(slots, C, 3, dtype=BF16, device=dev)
+    sp1 = torch.zeros(slots, Hv, D, D, device=dev)
+    out1 = core.prefill_varlen(mixed, z, b, a, lens, ids, cp1, sp1)
+    # solo, each sequence alone
+    cp2, sp2 = torch.zeros_like(cp1), torch.zeros_like(sp1)
+    outs, off = [], 0
+    for r, T in enumerate(lens):
+        outs.append(core.prefill_varlen(mixed[off:off + T], z[off:off + T], b[off:off + T], a[off:off + T], [T],
+                                        ids[r:r + 1], cp2, sp2))
+        off += T
+    assert torch.equal(torch.cat(outs), out1) and torch.equal(cp1, cp2) and torch.equal(sp1, sp2)
+    # chunked: the first sequence prefilled in two calls (split inside a chunk)
+    cp3, sp3 = torch.zeros_like(cp1), torch.zeros_like(sp1)
+    o_a = core.prefill_varlen(mixed[:100], z[:100], b[:100], a[:100], [100], ids[:1], cp3, sp3)
+    o_b = core.prefill_varlen(mixed[100:300], z[100:300], b[100:300], a[100:300], [200], ids[:1], cp3, sp3)
+    assert_out(torch.cat([o_a, o_b]).cpu(), out1[:300].cpu(), "chunked == one-shot", ulps=4)
+    assert torch.equal(cp3[2], cp1[2])
+    assert state_rel(sp3[2].cpu(), sp1[2].cpu()) < 1e-4
+
+
+def test_prefill_then_decode_equals_longer_prefill(pkg, dev):
+    gen = torch.Generator().manual_seed(34)
+    Hk = Hv = 4
+    D = 128
+    C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
+    T = 150
+    mixed, z, b, a = (t.to(dev) for t in _rows(gen, T + 1, C, Hv, D))
+    core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w)
+    ids = torch.tensor([1], device=dev)
+    cp = torch.zeros(2, C, 3, dtype=BF16, device=dev)
+    sp = torch.zeros(2, Hv, D, D, device=dev)
+    core.prefill_varlen(mixed[:T], z[:T], b[:T], a[:T], [T], ids, cp, sp)
+    o_dec = core.decode(mixed[T:], z[T:], b[T:], a[T:], ids, cp, sp)
+    cp2, sp2 = torch.zeros_like(cp), torch.zeros_like(sp)
+    o_all = core.prefill_varlen(mixed, z, b, a, [T + 1], ids, cp2, sp2)
+    assert_out(o_dec.cpu(), o_all[T:].cpu(), "decode after prefill", ulps=4)
+    assert torch.equal(cp, cp2)
+    assert state_rel(sp[1].cpu(), sp2[1].cpu()) < 1e-4
+
+
+# --------------------------------------------------------- BASELINE configs --
+def _prefill_config(pkg, dev, cfg):
+    core = _core(pkg, dev, cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"], cfg["A_log"], cfg["dt_bias"],
+                 cfg["norm_w"])
+    n = len(cfg["lens"])
+    cp, sp = cfg["conv_state"].to(dev), cfg["h0"].to(dev)
+    out = core.prefill_varlen(cfg["x"].to(dev), cfg["z"].to(dev), cfg["b"].to(dev), cfg["a"].to(dev), cfg["lens"],
+                              torch.arange(n, device=dev), cp, sp)
+    torch.cuda.synchronize()
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    ref, ref_conv, ref_s = gdn_ref.gdn_core_varlen(cfg["x"], cfg["z"], cfg["b"], cfg["a"], cfg["lens"],
+                                                   cfg["conv_state"], cfg["h0"], cfg["conv_w"], cfg["A_log"],
+                                                   cfg["dt_bias"], cfg["norm_w"], cfg["Hk"], cfg["Hv"], cfg["D"])
+    assert_out(out.cpu(), ref, "prefill output", ulps=4)
+    assert torch.equal(cp.cpu(), ref_conv), "conv state"
+    for r in range(n):
+        assert_state(sp[r].cpu(), ref_s[r], f"final state of sequence {r}")
+
+
+def test_config1_varlen_prefill_full(pkg, dev):
+    print("config 1: 8 seqs ~U[128,4096] seed 1", flush=True)
+    _prefill_config(pkg, dev, bench.make_prefill(1, None))
+
+
+def test_config3_long_prefill_full(pkg, dev):
+    print("config 3: 1 x 65536 tokens, h0 ~ N(0, 0.1^2), conv prefix", flush=True)
+    _prefill_config(pkg, dev, bench.make_prefill(4, [65536], h0_std=0.1, conv_std=1.0))
+
+
+def test_config2_decode_full(pkg, dev):
+    print("config 2: B=256 over 512 slots", flush=True)
+    c = bench.make_decode()
+    core = _core(pkg, dev, c["Hk"], c["Hv"], c["D"], c["conv_w"], c["A_log"], c["dt_bias"], c["norm_w"])
+    cp, sp = c["conv_pool"].to(dev), c["s_pool"].to(dev)
+    out = core.decode(c["x"].to(dev), c["z"].to(dev), c["b"].to(dev), c["a"].to(dev), c["ids"].to(dev), cp, sp)
+    torch.cuda.synchronize()
+    ref, ref_conv, ref_s = gdn_ref.gdn_core_decode(c["x"], c["z"], c["b"], c["a"], c["ids"].tolist(),
+                                                   c["conv_pool"], c["s_pool"], c["conv_w"], c["A_log"],
+                                                   c["dt_bias"], c["norm_w"], c["Hk"], c["Hv"], c["D"])
+    assert_out(out.cpu(), ref, "decode output", ulps=4)
+    assert torch.equal(cp.cpu().view(torch.int16), ref_conv.view(torch.int16)), "conv pool roll"
+    spc = sp.cpu()
+    ids = c["ids"]
+    assert_state(spc[ids], ref_s[ids], "decoded slots")
+    untouched = torch.ones(spc.shape[0], dtype=torch.bool)
+    untouched[ids] = False
+    assert torch.equal(spc[untouched], c["s_pool"][untouched]), "untouched slots must be bit-identical"
+
+
+def test_config4_spec_verify_full(pkg, dev):
+    print("config 4: 64 seqs x 4 draft tokens, Hk=16 Hv=32", flush=True)
+    c = bench.make_spec()
+    B, T, Hv, D = c["B"], c["T"], c["Hv"], c["D"]
+    g, beta = gdn_ref.g_beta(c["b"], c["a"], c["A_log"], c["dt_bias"])
+    pool = c["s_pool"].to(dev)
+    inter = torch.empty(B, T, Hv, D, D, device=dev)
+    o = pkg.ops.recurrent_gdn_multitoken(c["q"].to(dev), c["k"].to(dev), c["v"].to(dev), g.to(dev), beta.to(dev),
+                                         pool, c["ids"].to(dev), intermediate_states=inter)
+    pkg.ops.commit_states(pool, c["ids"].to(dev), inter, c["accepted"].to(dev))
+    torch.cuda.synchronize()
+    ids = c["ids"]
+    ro, _, rstates = gdn_ref.recurrent_rule(c["q"], c["k"], c["v"], g, beta.float(), c["s_pool"][ids],
+                                            keep_states=True)
+    assert_out(o.cpu(), ro.to(BF16), "spec-verify outputs")
+    interc = inter.cpu()
+    for t in range(T):
+        assert_state(interc[:, t], rstates[:, t], f"intermediate state {t}")
+    poolc = pool.cpu()
+    for i in range(B):
+        acc = int(c["accepted"][i])
+        assert torch.equal(poolc[ids[i]], interc[i, acc - 1]), "rollback restores the accepted prefix state"
