@@ -111,13 +111,23 @@ int gdn_conv_padded(const uint16_t* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
  *         h0 == hT (in-place update of a slot pool) is allowed.
  *   o     [N, Hv, D] bf16 contiguous
  *   l2norm != 0: q, k rows are L2-normalised in fp32 (eps 1e-6) first.
- * D must be 64 or 128.
+ *   workspace: device buffer of at least gdn_chunk_prefill_workspace_size()
+ *         bytes, 256-byte aligned, owned by the caller.  It receives the
+ *         per-(chunk, head) intermediates of the state-independent phase;
+ *         contents need no initialisation and are dead after the call.
+ * D must be 64 or 128.  Two launches on `stream` (chunk-local phase over all
+ * chunks in parallel, then the sequential state chain per sequence and head).
  */
 int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k, int64_t sk_tok,
                       const uint16_t* v, int64_t sv_tok, const float* g, const uint16_t* beta,
                       const float* h0, float* hT, const int64_t* state_ids, int64_t state_stride,
                       const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv, int D,
-                      float scale, int l2norm, uint16_t* o, void* stream);
+                      float scale, int l2norm, uint16_t* o, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes gdn_chunk_prefill needs for N packed tokens in n_seqs
+ * sequences (an upper bound over the sequence lengths); -1 on bad args. */
+int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
 
 /*
  * Recurrent gated delta rule for decode: T >= 1 tokens per sequence, state

@@ -42,12 +42,16 @@ SIGNATURES: dict[str, list] = {
     "gdn_conv_decode": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i32, _i32, _i32, _p],
     "gdn_conv_padded": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _p],
     "gdn_chunk_prefill": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _i64,
-                          _i32, _i32, _i32, _f32, _i32, _p, _p],
+                          _i32, _i32, _i32, _f32, _i32, _p, _p, _i64, _p],
+    "gdn_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],
     "gdn_recurrent": [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
                       _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     "gdn_state_commit": [_p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _p],
     "gdn_rmsnorm_gated": [_p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p],
 }
+
+# entry points whose return type is not int (status)
+RESTYPES = {"gdn_chunk_prefill_workspace_size": ctypes.c_int64}
 
 _LIB: ctypes.CDLL | None = None
 
@@ -68,7 +72,7 @@ def load() -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_int
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
     v = lib.gdn_abi_version()
     if v != ABI_VERSION:
         raise GDNLibraryError(f"ABI mismatch: library {v}, bindings {ABI_VERSION}")

@@ -1,16 +1,22 @@
-// Chunked gated delta rule over packed varlen sequences, chunk size 64,
-// fully fused: one workgroup walks all chunks of one (sequence, value head,
-// v-block) and keeps its slice of the fp32 recurrent state in registers.
+// Chunked gated delta rule over packed varlen sequences, chunk size 64.
 //
 // Per chunk (rows t, s in [0, 64); G = inclusive cumsum of g in the chunk,
-// gamma = G[63]; k^, q^ = L2-normalised rows; follows the torch port at
-// nanovllm/models/qwen3_5.py:152-227):
+// gamma = G[63]; k^, q^ = L2-normalised rows; the algorithm of the torch
+// port at nanovllm/models/qwen3_5.py:152-227):
 //   L    = strict_lower( beta_t k^_t.k^_s e^{G_t-G_s} )
 //   T    = (I + L)^-1                       (the reference's forward substitution)
 //   W    = T diag(beta e^G) K^,   U = T diag(beta) V
 //   Vn   = U - W S
 //   O    = diag(e^G) Q^ S + lower_incl( q^_t.k^_s e^{G_t-G_s} ) Vn
 //   S   <- e^gamma S + K^T diag(e^{gamma-G}) Vn
+//
+// Two kernels.  Everything that does not depend on the recurrent state S
+// (K K^T, Q K^T, the triangular inverse, W, U) is independent across
+// chunks, so chunk_local_kernel computes it for every (chunk, value head)
+// in parallel and writes one record per chunk-head into a workspace.
+// chunk_chain_kernel then walks each (sequence, value head) chunk by chunk
+// with its slice of S in registers; only the S-dependent products are left
+// on that sequential path.
 //
 // Numerics.  q, k, v arrive in bf16, which is exact as an MFMA operand, and
 // the L2 norm is a per-row scale; so K K^T, Q K^T, W = T' K_raw and the K
@@ -35,24 +41,16 @@ using gdn::s16x8_t;
 
 constexpr int kC = 64;  // chunk size
 
-template <int D, int NW>
-struct __align__(16) ChunkSmem {
-  uint16_t Kt[D][kC + 8];       // K^T of the chunk (raw bf16), row = key dim
-  uint16_t Qs[kC][D + 8];       // Q of the chunk (raw bf16), row = token
-  uint16_t KrW[kC][D + 8];      // K row-major (phases 1-2), then W (phases 5-6)
-  uint16_t Tp[kC][kC + 8];      // T' = T diag(beta rk e^G), bf16
-  uint16_t Uh[kC][kC + 8];      // T'' = T diag(beta), hi
-  uint16_t Ul[kC][kC + 8];      //                     lo
-  uint16_t Ah[kC][kC + 8];      // A_qk hi
-  uint16_t Al[kC][kC + 8];      // A_qk lo
-  float Lf[kC][kC + 4];         // L (fp32)
-  float Tf[kC][kC + 4];         // T (fp32), lower blocks only
-  float scr[4][16][20];         // per-wave 16x16 scratch of the solve
-  float G[kC], bt[kC], rk[kC], rq[kC];
-  float cW[kC], cQ[kC], cK[kC];
-  float ssk[NW][kC];
-  float ssq[kC];
-  float eg_last;
+// ---- workspace record of one (chunk, value head), byte offsets ----
+template <int D>
+struct Rec {
+  static constexpr int64_t W = 0;                        // bf16 [64][D]    W = T' K_raw
+  static constexpr int64_t KT = W + 64 * D * 2;          // bf16 [D][64]    K_raw^T
+  static constexpr int64_t AH = KT + D * 64 * 2;         // bf16 [64][64]   A_qk hi
+  static constexpr int64_t AL = AH + 64 * 64 * 2;        // bf16 [64][64]   A_qk lo
+  static constexpr int64_t U = AL + 64 * 64 * 2;         // fp32 C fragments of U = T'' V
+  static constexpr int64_t VEC = U + 64 * D * 4;         // fp32 cQ[64], cK[64], e^gamma
+  static constexpr int64_t BYTES = (VEC + 144 * 4 + 255) / 256 * 256;
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -124,89 +122,515 @@ __device__ __forceinline__ void tri_tile(int j, int& mt, int& nt) {
   nt = j - (mt * (mt + 1)) / 2;
 }
 
-// Global -> register prefetch of one chunk's operands (issued a chunk ahead).
-template <int D, int NW>
-struct Prefetch {
-  static constexpr int NT = 64 * NW;
-  static constexpr int SEG = D / 8;               // 16-byte segments per row
-  static constexpr int KPRE = SEG / NW;           // K segments per lane (lane = token)
-  static constexpr int QPRE = kC * SEG / NT;      // Q segments per thread (row-major)
-  s16x8_t k[KPRE];
-  s16x8_t q[QPRE];
-  uint16_t v[16];  // one VGPR each: packing into vectors here would wait on the loads
-  float g;
-  uint16_t b;  // raw bf16 bits: converting here would force a wait on the load
+__device__ __forceinline__ int64_t chunks_of(int64_t len) { return (len + kC - 1) / kC; }
 
-  // Rows past the chunk end are loaded from the last valid row (always in
-  // bounds, no branches) and zeroed only where the chunk is staged, so no
-  // instruction consumes a loaded value before the next chunk begins.
-  __device__ __forceinline__ void load(const uint16_t* qh, int64_t sq, const uint16_t* kh, int64_t sk,
-                                       const uint16_t* vh, int64_t sv, const float* gp, const uint16_t* bp,
-                                       int Hv, int h, int64_t tok0, int len, int tid, int wave, int lane,
-                                       int lg, int vcol) {
-    const int last = len - 1;
+// Flat chunk index -> (sequence, chunk within it), by one wave scanning the
+// per-sequence chunk counts.  Returns false past the last chunk.
+__device__ bool locate_chunk(const int64_t* __restrict__ cu, int n_seqs, int64_t c, int* seq_out,
+                             int64_t* j_out) {
+  __shared__ int s_seq;
+  __shared__ long long s_j;
+  if (threadIdx.x == 0) { s_seq = -1; s_j = 0; }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int per = (n_seqs + 63) / 64;
+    const int beg = min(lane * per, n_seqs);
+    const int end = min(beg + per, n_seqs);
+    long long local = 0;
+    for (int r = beg; r < end; ++r) local += chunks_of(cu[r + 1] - cu[r]);
+    long long incl = local;
 #pragma unroll
-    for (int j = 0; j < KPRE; ++j) {
-      const int c8 = wave + NW * j;
-      k[j] = *reinterpret_cast<const s16x8_t*>(kh + (tok0 + min(lane, last)) * sk + c8 * 8);
+    for (int d = 1; d < 64; d <<= 1) {
+      const long long o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
     }
-#pragma unroll
-    for (int j = 0; j < QPRE; ++j) {
-      const int e = tid + NT * j;
-      const int t = e / SEG, c8 = e % SEG;
-      q[j] = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, last)) * sq + c8 * 8);
-    }
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int s = 32 * kt + 8 * lg + i;
-        v[8 * kt + i] = vh[(tok0 + min(s, last)) * sv + vcol];
+    const long long excl = incl - local;
+    if (c >= excl && c < incl) {
+      long long acc = excl;
+      for (int r = beg; r < end; ++r) {
+        const long long nc = chunks_of(cu[r + 1] - cu[r]);
+        if (c < acc + nc) { s_seq = r; s_j = c - acc; break; }
+        acc += nc;
       }
-    const int64_t gi = (tok0 + min(lane, last)) * Hv + h;
-    g = gp[gi];
-    b = bp[gi];
+    }
   }
+  __syncthreads();
+  *seq_out = s_seq;
+  *j_out = s_j;
+  return s_seq >= 0;
+}
+
+// ============================================================ local kernel ==
+template <int D, int NW>
+struct __align__(16) LocalSmem {
+  uint16_t Kt[D][kC + 8];       // K^T of the chunk (raw bf16), row = key dim
+  uint16_t KrW[kC][D + 8];      // K row-major (KK^T, QK^T), then W
+  uint16_t Qs[kC][D + 8];       // Q row-major (raw bf16)
+  uint16_t Tp[kC][kC + 8];      // T' = T diag(beta rk e^G), bf16
+  uint16_t Uh[kC][kC + 8];      // T'' = T diag(beta), hi
+  uint16_t Ul[kC][kC + 8];      //                     lo
+  uint16_t Ah[kC][kC + 8];      // A_qk hi
+  uint16_t Al[kC][kC + 8];      // A_qk lo
+  float Lf[kC][kC + 4];         // L (fp32)
+  float Tf[kC][kC + 4];         // T (fp32), lower blocks only
+  float scr[4][16][20];         // per-wave 16x16 scratch of the solve
+  float G[kC], bt[kC], rk[kC], rq[kC];
+  float cW[kC], cQ[kC], cK[kC];
+  float ssk[NW][kC];
+  float ssq[kC];
+  float eg_last;
 };
 
+// grid = 8 * ceil(nc_bound * Hv / 8); block = 64 * NW.
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
+__global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
     const uint16_t* __restrict__ v, int64_t sv, const float* __restrict__ g,
-    const uint16_t* __restrict__ beta, const float* h0, float* hT, const int64_t* __restrict__ ids,
-    int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hk, int Hv, float scale,
-    int l2norm, uint16_t* __restrict__ o) {
+    const uint16_t* __restrict__ beta, const int64_t* __restrict__ cu, int n_seqs, int64_t nc_bound,
+    int Hk, int Hv, float scale, int l2norm, uint8_t* __restrict__ ws) {
   constexpr int NT = 64 * NW;
-  constexpr int BV = 16 * NW;
-  constexpr int NVB = D / BV;
-  constexpr int KTD = D / 32;  // contraction steps over the key dim
-  constexpr int MTD = D / 16;  // 16-row tiles over the key dim
+  constexpr int KTD = D / 32;
+  constexpr int MTD = D / 16;
   constexpr int LDF = kC + 4;
-  using PF = Prefetch<D, NW>;
-  static_assert(NW >= 4 && D % BV == 0, "chunk kernel shape");
-  static_assert(PF::KPRE * NW == PF::SEG && PF::QPRE * NT == kC * PF::SEG, "prefetch tiling");
+  constexpr int SEG = D / 8;                 // 16-byte segments per row
+  static_assert(NW >= 4, "the solve uses four waves");
+  __shared__ LocalSmem<D, NW> sm;
 
-  __shared__ ChunkSmem<D, NW> sm;
-
-  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(n_seqs) * Hv * NVB);
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, nc_bound * Hv);
   if (wi < 0) return;
-  const int vb = static_cast<int>(wi % NVB);
-  const int h = static_cast<int>((wi / NVB) % Hv);
-  const int r = static_cast<int>(wi / (static_cast<int64_t>(NVB) * Hv));
+  const int h = static_cast<int>(wi % Hv);
+  const int64_t cidx = wi / Hv;
+  int r;
+  int64_t jc;
+  if (!locate_chunk(cu, n_seqs, cidx, &r, &jc)) return;
+  const int64_t tok0 = cu[r] + jc * kC;
+  const int len = static_cast<int>(min<int64_t>(kC, cu[r + 1] - tok0));
   const int kh = h / (Hv / Hk);
-
-  const int64_t bos = cu[r];
-  const int64_t seqlen = cu[r + 1] - bos;
   const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
   const uint16_t* kh_ = k + static_cast<int64_t>(kh) * D;
   const uint16_t* vh = v + static_cast<int64_t>(h) * D;
+  uint8_t* rec = ws + (cidx * Hv + h) * Rec<D>::BYTES;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int lr = lane & 15;
+  const int lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // ---- phase 1: stage K (both layouts) and Q, row norms, gates ----
+  {
+    float ss = 0.f;
+    const int row = min(lane, len - 1);
+#pragma unroll
+    for (int j = 0; j < SEG / NW; ++j) {
+      const int c8 = wave + NW * j;
+      s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + (tok0 + row) * sk + c8 * 8);
+      if (lane >= len) kv8 = zero8();
+      *reinterpret_cast<s16x8_t*>(&sm.KrW[lane][c8 * 8]) = kv8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t bits = static_cast<uint16_t>(kv8[i]);
+        sm.Kt[c8 * 8 + i][lane] = bits;
+        const float f = gdn::bf2f(bits);
+        ss += f * f;
+      }
+    }
+    sm.ssk[wave][lane] = ss;
+#pragma unroll
+    for (int j = 0; j < kC * SEG / NT; ++j) {
+      const int e = tid + NT * j;
+      const int t = e / SEG, c8 = e % SEG;
+      s16x8_t qv8 = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, len - 1)) * sq + c8 * 8);
+      if (t >= len) qv8 = zero8();
+      *reinterpret_cast<s16x8_t*>(&sm.Qs[t][c8 * 8]) = qv8;
+      float qs = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float f = gdn::bf2f(static_cast<uint16_t>(qv8[i]));
+        qs += f * f;
+      }
+#pragma unroll
+      for (int m = SEG / 2; m >= 1; m >>= 1) qs += __shfl_xor(qs, m, 64);
+      if (c8 == 0) sm.ssq[t] = qs;
+    }
+    if (wave == 0) {
+      float gv = 0.f, bv = 0.f;
+      if (lane < len) {
+        const int64_t gi = (tok0 + lane) * Hv + h;
+        gv = g[gi];
+        bv = gdn::bf2f(beta[gi]);
+      }
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o_ = __shfl_up(gv, d, 64);
+        if (lane >= d) gv += o_;
+      }
+      sm.G[lane] = gv;
+      sm.bt[lane] = bv;
+    }
+  }
+  __syncthreads();
+  if (tid < kC) {
+    const int t = tid;
+    float ssk = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) ssk += sm.ssk[w][t];
+    const float rk = l2norm ? rsqrtf(ssk + 1e-6f) : 1.0f;
+    const float rq = l2norm ? rsqrtf(sm.ssq[t] + 1e-6f) : 1.0f;
+    const float Gt = sm.G[t];
+    const float Gl = sm.G[kC - 1];
+    sm.rk[t] = rk;
+    sm.rq[t] = rq;
+    sm.cW[t] = sm.bt[t] * rk * expf(Gt);
+    sm.cQ[t] = rq * scale * expf(Gt);
+    sm.cK[t] = rk * expf(Gl - Gt);
+    if (t == 0) sm.eg_last = expf(Gl);
+  }
+  __syncthreads();
+
+  // ---- phase 2a: K K^T -> L (fp32), lower-triangular tiles ----
+  for (int j = wave; j < 10; j += NW) {
+    int mt, nt;
+    tri_tile(j, mt, nt);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < KTD; ++kt) {
+      const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * mt + lr][32 * kt + 8 * lg]);
+      const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
+      acc = gdn::mfma16x16x32(a8, b8, acc);
+    }
+    const int s = 16 * nt + lr;
+    const float rks = sm.rk[s];
+    const float Gs = sm.G[s];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * mt + 4 * lg + i;
+      sm.Lf[t][s] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * expf(sm.G[t] - Gs) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2b / solve step 1: wave 0 inverts the diagonal blocks while
+  //      the other waves form A_qk = lower(Q K^T) (hi/lo) ----
+  if (wave == 0) {
+    const int bb = lane >> 4, c = lane & 15, base = 16 * bb;
+    float x[16];
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const float4* lrow = reinterpret_cast<const float4*>(&sm.Lf[base + rr][base]);
+      float lv[16];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 f = lrow[q4];
+        lv[4 * q4] = f.x; lv[4 * q4 + 1] = f.y; lv[4 * q4 + 2] = f.z; lv[4 * q4 + 3] = f.w;
+      }
+      float acc = rr == c ? 1.f : 0.f;
+#pragma unroll
+      for (int jj = 0; jj < rr; ++jj) acc -= lv[jj] * x[jj];
+      x[rr] = acc;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) sm.Tf[base + rr][base + c] = x[rr];
+  } else {
+    for (int j = wave - 1; j < 10; j += NW - 1) {
+      int mt, nt;
+      tri_tile(j, mt, nt);
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < KTD; ++kt) {
+        const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Qs[16 * mt + lr][32 * kt + 8 * lg]);
+        const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
+        acc = gdn::mfma16x16x32(a8, b8, acc);
+      }
+      const int s = 16 * nt + lr;
+      const float rks = sm.rk[s] * scale;
+      const float Gs = sm.G[s];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * mt + 4 * lg + i;
+        const float a = s <= t ? acc[i] * sm.rq[t] * rks * expf(sm.G[t] - Gs) : 0.f;
+        uint16_t hi, lo;
+        gdn::split_bf16(a, hi, lo);
+        sm.Ah[t][s] = hi;
+        sm.Al[t][s] = lo;
+      }
+    }
+  }
+  __syncthreads();
+  // first sub-diagonal: T(j+1, j) = -T(j+1,j+1) L(j+1,j) T(j,j)
+  if (wave < 3) {
+    const int j = wave, i = j + 1;
+    f32x4_t p = {0.f, 0.f, 0.f, 0.f};
+    p = mm16_f32(p, &sm.Lf[16 * i][16 * j], LDF, &sm.Tf[16 * j][16 * j], LDF, lane);
+    st16_f32(&sm.scr[wave][0][0], 20, p, 1.f, lane);
+    wave_sync();
+    f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
+    t2 = mm16_f32(t2, &sm.Tf[16 * i][16 * i], LDF, &sm.scr[wave][0][0], 20, lane);
+    st16_f32(&sm.Tf[16 * i][16 * j], LDF, t2, -1.f, lane);
+  } else if (wave == 3) {
+    f32x4_t p = {0.f, 0.f, 0.f, 0.f};
+    p = mm16_f32(p, &sm.Lf[48][0], LDF, &sm.Tf[0][0], LDF, lane);  // L30 T00
+    st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
+  }
+  __syncthreads();
+  // second sub-diagonal: T20, T31; partial sum for T30
+  if (wave == 0) {
+    f32x4_t p = {0.f, 0.f, 0.f, 0.f};
+    p = mm16_f32(p, &sm.Lf[32][0], LDF, &sm.Tf[0][0], LDF, lane);    // L20 T00
+    p = mm16_f32(p, &sm.Lf[32][16], LDF, &sm.Tf[16][0], LDF, lane);  // L21 T10
+    st16_f32(&sm.scr[0][0][0], 20, p, 1.f, lane);
+    wave_sync();
+    f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
+    t2 = mm16_f32(t2, &sm.Tf[32][32], LDF, &sm.scr[0][0][0], 20, lane);
+    st16_f32(&sm.Tf[32][0], LDF, t2, -1.f, lane);
+  } else if (wave == 1) {
+    f32x4_t p = {0.f, 0.f, 0.f, 0.f};
+    p = mm16_f32(p, &sm.Lf[48][16], LDF, &sm.Tf[16][16], LDF, lane);  // L31 T11
+    p = mm16_f32(p, &sm.Lf[48][32], LDF, &sm.Tf[32][16], LDF, lane);  // L32 T21
+    st16_f32(&sm.scr[1][0][0], 20, p, 1.f, lane);
+    wave_sync();
+    f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
+    t2 = mm16_f32(t2, &sm.Tf[48][48], LDF, &sm.scr[1][0][0], 20, lane);
+    st16_f32(&sm.Tf[48][16], LDF, t2, -1.f, lane);
+  } else if (wave == 3) {
+    f32x4_t p = ld16_f32(&sm.scr[3][0][0], 20, lane);
+    p = mm16_f32(p, &sm.Lf[48][16], LDF, &sm.Tf[16][0], LDF, lane);  // + L31 T10
+    st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
+  }
+  __syncthreads();
+  // third sub-diagonal: T30
+  if (wave == 3) {
+    f32x4_t p = ld16_f32(&sm.scr[3][0][0], 20, lane);
+    p = mm16_f32(p, &sm.Lf[48][32], LDF, &sm.Tf[32][0], LDF, lane);  // + L32 T20
+    st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
+    wave_sync();
+    f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
+    t2 = mm16_f32(t2, &sm.Tf[48][48], LDF, &sm.scr[3][0][0], 20, lane);
+    st16_f32(&sm.Tf[48][0], LDF, t2, -1.f, lane);
+  }
+  __syncthreads();
+
+  // ---- phase 4: T' (bf16) and T'' (hi/lo), 4 columns per thread; zero the
+  //      upper tiles of A_qk ----
+  for (int e4 = tid; e4 < kC * (kC / 4); e4 += NT) {
+    const int t = e4 >> 4, s0 = (e4 & 15) * 4;
+    const bool lower = (s0 >> 4) <= (t >> 4);
+    float4 tv = lower ? *reinterpret_cast<const float4*>(&sm.Tf[t][s0]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 cw = *reinterpret_cast<const float4*>(&sm.cW[s0]);
+    const float4 cb = *reinterpret_cast<const float4*>(&sm.bt[s0]);
+    uint2 tp;
+    tp.x = gdn::f2bf2(tv.x * cw.x, tv.y * cw.y);
+    tp.y = gdn::f2bf2(tv.z * cw.z, tv.w * cw.w);
+    *reinterpret_cast<uint2*>(&sm.Tp[t][s0]) = tp;
+    const float u0 = tv.x * cb.x, u1 = tv.y * cb.y, u2 = tv.z * cb.z, u3 = tv.w * cb.w;
+    uint2 uh, ul;
+    uh.x = gdn::f2bf2(u0, u1);
+    uh.y = gdn::f2bf2(u2, u3);
+    ul.x = gdn::f2bf2(u0 - lo_half(uh.x), u1 - hi_half(uh.x));
+    ul.y = gdn::f2bf2(u2 - lo_half(uh.y), u3 - hi_half(uh.y));
+    *reinterpret_cast<uint2*>(&sm.Uh[t][s0]) = uh;
+    *reinterpret_cast<uint2*>(&sm.Ul[t][s0]) = ul;
+    if (!lower) {
+      *reinterpret_cast<uint2*>(&sm.Ah[t][s0]) = make_uint2(0u, 0u);
+      *reinterpret_cast<uint2*>(&sm.Al[t][s0]) = make_uint2(0u, 0u);
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 5: W = T' K (-> LDS, overwrites K row-major) and
+  //      U = T'' V (C fragments straight to the record) ----
+  {
+    constexpr int NJ = (4 * MTD + NW - 1) / NW;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      const int j = wave + NW * jj;
+      if (j >= 4 * MTD) break;
+      const int mt = j % 4, nt = j / 4;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Tp[16 * mt + lr][32 * kt + 8 * lg]);
+        const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.Kt[16 * nt + lr][32 * kt + 8 * lg]);
+        acc = gdn::mfma16x16x32(a8, b8, acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm.KrW[16 * mt + 4 * lg + i][16 * nt + lr] = gdn::f2bf(acc[i]);
+    }
+    // U tiles: column tile nt (16 value columns) x 4 row tiles; record layout
+    // [nt][mt][lane] float4, i.e. exactly the C fragments the chain kernel holds
+    float4* urec = reinterpret_cast<float4*>(rec + Rec<D>::U);
+    for (int nt = wave; nt < MTD; nt += NW) {
+      s16x8_t vf[2];
+      const int col = 16 * nt + lr;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int s = 32 * kt + 8 * lg + i;
+          const short x = static_cast<short>(vh[(tok0 + min(s, len - 1)) * sv + col]);
+          vf[kt][i] = s < len ? x : static_cast<short>(0);
+        }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        f32x4_t u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const s16x8_t ah = *reinterpret_cast<const s16x8_t*>(&sm.Uh[16 * mt + lr][32 * kt + 8 * lg]);
+          const s16x8_t al = *reinterpret_cast<const s16x8_t*>(&sm.Ul[16 * mt + lr][32 * kt + 8 * lg]);
+          u = gdn::mfma16x16x32(ah, vf[kt], u);
+          u = gdn::mfma16x16x32(al, vf[kt], u);
+        }
+        urec[(nt * 4 + mt) * 64 + lane] = make_float4(u[0], u[1], u[2], u[3]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- record: W, K^T, A_qk hi/lo (16-byte copies), vectors ----
+  {
+    uint4* wrec = reinterpret_cast<uint4*>(rec + Rec<D>::W);
+    for (int e = tid; e < kC * SEG; e += NT) {
+      const int t = e / SEG, c8 = e % SEG;
+      wrec[e] = *reinterpret_cast<const uint4*>(&sm.KrW[t][c8 * 8]);
+    }
+    uint4* krec = reinterpret_cast<uint4*>(rec + Rec<D>::KT);
+    for (int e = tid; e < D * (kC / 8); e += NT) {
+      const int d = e / (kC / 8), c8 = e % (kC / 8);
+      krec[e] = *reinterpret_cast<const uint4*>(&sm.Kt[d][c8 * 8]);
+    }
+    uint4* ahrec = reinterpret_cast<uint4*>(rec + Rec<D>::AH);
+    uint4* alrec = reinterpret_cast<uint4*>(rec + Rec<D>::AL);
+    for (int e = tid; e < kC * (kC / 8); e += NT) {
+      const int t = e / (kC / 8), c8 = e % (kC / 8);
+      ahrec[e] = *reinterpret_cast<const uint4*>(&sm.Ah[t][c8 * 8]);
+      alrec[e] = *reinterpret_cast<const uint4*>(&sm.Al[t][c8 * 8]);
+    }
+    float* vrec = reinterpret_cast<float*>(rec + Rec<D>::VEC);
+    if (tid < kC) {
+      vrec[tid] = sm.cQ[tid];
+      vrec[kC + tid] = sm.cK[tid];
+    }
+    if (tid == 0) vrec[2 * kC] = sm.eg_last;
+  }
+}
+
+// ============================================================ chain kernel ==
+template <int D, int NW>
+struct __align__(16) ChainSmem {
+  uint16_t Kt[D][kC + 8];
+  uint16_t Qs[kC][D + 8];
+  uint16_t W[kC][D + 8];
+  uint16_t Ah[kC][kC + 8];
+  uint16_t Al[kC][kC + 8];
+  float cQ[kC], cK[kC];
+  float eg_last;
+};
+
+// Per-chunk operands the whole workgroup shares, moved global -> registers a
+// chunk ahead, then registers -> LDS.  16-byte segments, NSEG per thread.
+template <int D, int NW>
+struct ChainPrefetch {
+  static constexpr int NT = 64 * NW;
+  static constexpr int SEG = D / 8;
+  static constexpr int W_SEGS = kC * SEG;           // W   [64][D]
+  static constexpr int K_SEGS = D * (kC / 8);       // K^T [D][64]
+  static constexpr int A_SEGS = kC * (kC / 8);      // A_qk hi, lo [64][64]
+  static constexpr int Q_SEGS = kC * SEG;           // Q   [64][D] (raw input)
+  static constexpr int REC_SEGS = W_SEGS + K_SEGS + 2 * A_SEGS;
+  static constexpr int TOTAL = REC_SEGS + Q_SEGS;
+  static constexpr int NSEG = TOTAL / NT;
+  static_assert(TOTAL % NT == 0 && REC_SEGS % NT == 0 && W_SEGS % NT == 0 && K_SEGS % NT == 0 &&
+                A_SEGS % NT == 0, "segment tiling");
+  s16x8_t seg[NSEG];
+  f32x4_t u[4];
+  float vec;
+
+  __device__ __forceinline__ void load(const uint8_t* rec, const uint16_t* qh, int64_t sq, int64_t tok0, int len,
+                                       int tid, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < NSEG; ++j) {
+      const int e = tid + NT * j;
+      if (j < REC_SEGS / NT) {
+        seg[j] = reinterpret_cast<const s16x8_t*>(rec)[e];  // W, K^T, A hi, A lo are contiguous
+      } else {
+        const int qe = e - REC_SEGS;
+        const int t = qe / SEG, c8 = qe % SEG;
+        seg[j] = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, len - 1)) * sq + c8 * 8);
+      }
+    }
+    const float4* urec = reinterpret_cast<const float4*>(rec + Rec<D>::U);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const float4 f = urec[(wave * 4 + mt) * 64 + lane];
+      u[mt] = f32x4_t{f.x, f.y, f.z, f.w};
+    }
+    vec = reinterpret_cast<const float*>(rec + Rec<D>::VEC)[min(tid, 2 * kC)];
+  }
+
+  __device__ __forceinline__ void stage(ChainSmem<D, NW>& sm, int tid) const {
+#pragma unroll
+    for (int j = 0; j < NSEG; ++j) {
+      const int e = tid + NT * j;
+      if (j < W_SEGS / NT) {
+        *reinterpret_cast<s16x8_t*>(&sm.W[e / SEG][(e % SEG) * 8]) = seg[j];
+      } else if (j < (W_SEGS + K_SEGS) / NT) {
+        const int x = e - W_SEGS;
+        *reinterpret_cast<s16x8_t*>(&sm.Kt[x / (kC / 8)][(x % (kC / 8)) * 8]) = seg[j];
+      } else if (j < (W_SEGS + K_SEGS + A_SEGS) / NT) {
+        const int x = e - W_SEGS - K_SEGS;
+        *reinterpret_cast<s16x8_t*>(&sm.Ah[x / (kC / 8)][(x % (kC / 8)) * 8]) = seg[j];
+      } else if (j < REC_SEGS / NT) {
+        const int x = e - W_SEGS - K_SEGS - A_SEGS;
+        *reinterpret_cast<s16x8_t*>(&sm.Al[x / (kC / 8)][(x % (kC / 8)) * 8]) = seg[j];
+      } else {
+        const int x = e - REC_SEGS;
+        *reinterpret_cast<s16x8_t*>(&sm.Qs[x / SEG][(x % SEG) * 8]) = seg[j];
+      }
+    }
+    if (tid < kC) sm.cQ[tid] = vec;
+    else if (tid < 2 * kC) sm.cK[tid - kC] = vec;
+    else if (tid == 2 * kC) sm.eg_last = vec;
+  }
+};
+
+// grid = 8 * ceil(n_seqs * Hv / 8); block = 64 * NW; wave w owns the state
+// columns [16w, 16w + 16) of value head h.
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void chunk_chain_kernel(
+    const uint16_t* __restrict__ q, int64_t sq, const uint8_t* __restrict__ ws,
+    const float* h0, float* hT, const int64_t* __restrict__ ids, int64_t sstride,
+    const int64_t* __restrict__ cu, int n_seqs, int Hk, int Hv, uint16_t* __restrict__ o) {
+  constexpr int KTD = D / 32;
+  constexpr int MTD = D / 16;
+  static_assert(16 * NW == D, "one wave per 16 state columns");
+  using PF = ChainPrefetch<D, NW>;
+  __shared__ ChainSmem<D, NW> sm;
+  __shared__ long long s_base;
+
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(n_seqs) * Hv);
+  if (wi < 0) return;
+  const int h = static_cast<int>(wi % Hv);
+  const int r = static_cast<int>(wi / Hv);
+  const int kh = h / (Hv / Hk);
+  const int64_t bos = cu[r];
+  const int64_t seqlen = cu[r + 1] - bos;
+  const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
   const int64_t srow = ids ? ids[r] : r;
 
-  // state / output column of this lane: rows 16*mt + 4*(lane>>4) + i of S
-  const int vcol0 = vb * BV + 16 * (threadIdx.x >> 6) + (threadIdx.x & 15);
-  const int lg0 = (threadIdx.x & 63) >> 4;
+  // first workspace chunk of this sequence: sum of earlier sequences' chunks
+  if (threadIdx.x < 64) {
+    long long part = 0;
+    for (int rr = threadIdx.x; rr < r; rr += 64) part += chunks_of(cu[rr + 1] - cu[rr]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+    if (threadIdx.x == 0) s_base = part;
+  }
+  __syncthreads();
+  const int64_t cbase = s_base;
 
-  // ---- state slice: S[mt] holds rows 16mt + 4lg + i, column vcol ----
+  const int vcol0 = 16 * (threadIdx.x >> 6) + (threadIdx.x & 15);
+  const int lg0 = (threadIdx.x & 63) >> 4;
   f32x4_t S[MTD];
   if (h0) {
     const float* hp = h0 + srow * sstride + static_cast<int64_t>(h) * D * D + vcol0;
@@ -221,16 +645,16 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
 
   PF pf;
   if (seqlen > 0)
-    pf.load(qh, sq, kh_, sk, vh, sv, g, beta, Hv, h, bos, static_cast<int>(min<int64_t>(kC, seqlen)),
-            threadIdx.x, threadIdx.x >> 6, threadIdx.x & 63, (threadIdx.x & 63) >> 4, vcol0);
+    pf.load(ws + (cbase * Hv + h) * Rec<D>::BYTES, qh, sq, bos, static_cast<int>(min<int64_t>(kC, seqlen)),
+            threadIdx.x, threadIdx.x >> 6, threadIdx.x & 63);
 
-  for (int64_t c0 = 0; c0 < seqlen; c0 += kC) {
+  int64_t jc = 0;
+  for (int64_t c0 = 0; c0 < seqlen; c0 += kC, ++jc) {
     const int len = static_cast<int>(min<int64_t>(kC, seqlen - c0));
     const int64_t tok0 = bos + c0;
-    // Re-derive the lane indices from an opaque copy each chunk.  Otherwise
-    // the compiler hoists every lane-dependent LDS / global address of the
-    // loop body out of the loop and keeps them all live in VGPRs, which
-    // spills; rebuilt here they cost a few ALU ops per chunk instead.
+    // Re-derive the lane indices from an opaque copy each chunk: otherwise the
+    // compiler hoists every lane-dependent address out of the loop and keeps
+    // them all live in VGPRs, which spills.
     int tid_l = static_cast<int>(threadIdx.x);
     asm volatile("" : "+v"(tid_l));
     const int tid = tid_l;
@@ -238,258 +662,22 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
     const int lr = lane & 15;
     const int lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid_l >> 6);
-    const int vcol = vb * BV + 16 * wave + lr;
+    const int vcol = 16 * wave + lr;
     __syncthreads();  // previous chunk's LDS readers are done
-
-    // ---- phase 1: stage the prefetched chunk, row norms, gates ----
-    s16x8_t vf[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        vf[kt][i] = 32 * kt + 8 * lg + i < len ? static_cast<short>(pf.v[8 * kt + i]) : static_cast<short>(0);
-    {
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < PF::KPRE; ++j) {
-        const int c8 = wave + NW * j;
-        const s16x8_t kv8 = lane < len ? pf.k[j] : zero8();
-        *reinterpret_cast<s16x8_t*>(&sm.KrW[lane][c8 * 8]) = kv8;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint16_t bits = static_cast<uint16_t>(kv8[i]);
-          sm.Kt[c8 * 8 + i][lane] = bits;
-          const float f = gdn::bf2f(bits);
-          ss += f * f;
-        }
-      }
-      sm.ssk[wave][lane] = ss;
-#pragma unroll
-      for (int j = 0; j < PF::QPRE; ++j) {
-        const int e = tid + NT * j;
-        const int t = e / PF::SEG, c8 = e % PF::SEG;
-        const s16x8_t qv8 = t < len ? pf.q[j] : zero8();
-        *reinterpret_cast<s16x8_t*>(&sm.Qs[t][c8 * 8]) = qv8;
-        float qs = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float f = gdn::bf2f(static_cast<uint16_t>(qv8[i]));
-          qs += f * f;
-        }
-#pragma unroll
-        for (int m = PF::SEG / 2; m >= 1; m >>= 1) qs += __shfl_xor(qs, m, 64);
-        if (c8 == 0) sm.ssq[t] = qs;
-      }
-      if (wave == 0) {
-        float gv = lane < len ? pf.g : 0.f;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const float o_ = __shfl_up(gv, d, 64);
-          if (lane >= d) gv += o_;
-        }
-        sm.G[lane] = gv;
-        sm.bt[lane] = lane < len ? gdn::bf2f(pf.b) : 0.f;
-      }
-    }
-    // issue the next chunk's loads now: their latency hides behind this chunk
+    pf.stage(sm, tid);
+    const f32x4_t U[4] = {pf.u[0], pf.u[1], pf.u[2], pf.u[3]};
     if (c0 + kC < seqlen)
-      pf.load(qh, sq, kh_, sk, vh, sv, g, beta, Hv, h, tok0 + kC,
-              static_cast<int>(min<int64_t>(kC, seqlen - c0 - kC)), tid, wave, lane, lg, vcol);
-    __syncthreads();
-    if (tid < kC) {
-      const int t = tid;
-      float ssk = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) ssk += sm.ssk[w][t];
-      const float rk = l2norm ? rsqrtf(ssk + 1e-6f) : 1.0f;
-      const float rq = l2norm ? rsqrtf(sm.ssq[t] + 1e-6f) : 1.0f;
-      const float Gt = sm.G[t];
-      const float Gl = sm.G[kC - 1];
-      sm.rk[t] = rk;
-      sm.rq[t] = rq;
-      sm.cW[t] = sm.bt[t] * rk * expf(Gt);
-      sm.cQ[t] = rq * scale * expf(Gt);
-      sm.cK[t] = rk * expf(Gl - Gt);
-      if (t == 0) sm.eg_last = expf(Gl);
-    }
+      pf.load(ws + ((cbase + jc + 1) * Hv + h) * Rec<D>::BYTES, qh, sq, tok0 + kC,
+              static_cast<int>(min<int64_t>(kC, seqlen - c0 - kC)), tid, wave, lane);
     __syncthreads();
 
-    // ---- phase 2a: K K^T -> L (fp32), lower-triangular tiles ----
-    for (int j = wave; j < 10; j += NW) {
-      int mt, nt;
-      tri_tile(j, mt, nt);
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kt = 0; kt < KTD; ++kt) {
-        const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * mt + lr][32 * kt + 8 * lg]);
-        const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
-        acc = gdn::mfma16x16x32(a8, b8, acc);
-      }
-      const int s = 16 * nt + lr;
-      const float rks = sm.rk[s];
-      const float Gs = sm.G[s];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * mt + 4 * lg + i;
-        sm.Lf[t][s] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * expf(sm.G[t] - Gs) : 0.f;
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 2b / solve step 1: wave 0 inverts the diagonal blocks while
-    //      the other waves form A_qk = lower(Q K^T) (hi/lo) ----
-    if (wave == 0) {
-      const int bb = lane >> 4, c = lane & 15, base = 16 * bb;
-      float x[16];
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const float4* lrow = reinterpret_cast<const float4*>(&sm.Lf[base + rr][base]);
-        float lv[16];
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const float4 f = lrow[q4];
-          lv[4 * q4] = f.x; lv[4 * q4 + 1] = f.y; lv[4 * q4 + 2] = f.z; lv[4 * q4 + 3] = f.w;
-        }
-        float acc = rr == c ? 1.f : 0.f;
-#pragma unroll
-        for (int jj = 0; jj < rr; ++jj) acc -= lv[jj] * x[jj];
-        x[rr] = acc;
-      }
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) sm.Tf[base + rr][base + c] = x[rr];
-    } else {
-      for (int j = wave - 1; j < 10; j += NW - 1) {
-        int mt, nt;
-        tri_tile(j, mt, nt);
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kt = 0; kt < KTD; ++kt) {
-          const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Qs[16 * mt + lr][32 * kt + 8 * lg]);
-          const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
-          acc = gdn::mfma16x16x32(a8, b8, acc);
-        }
-        const int s = 16 * nt + lr;
-        const float rks = sm.rk[s] * scale;
-        const float Gs = sm.G[s];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = 16 * mt + 4 * lg + i;
-          const float a = s <= t ? acc[i] * sm.rq[t] * rks * expf(sm.G[t] - Gs) : 0.f;
-          uint16_t hi, lo;
-          gdn::split_bf16(a, hi, lo);
-          sm.Ah[t][s] = hi;
-          sm.Al[t][s] = lo;
-        }
-      }
-    }
-    __syncthreads();
-    // first sub-diagonal: T(j+1, j) = -T(j+1,j+1) L(j+1,j) T(j,j)
-    if (wave < 3) {
-      const int j = wave, i = j + 1;
-      f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-      p = mm16_f32(p, &sm.Lf[16 * i][16 * j], LDF, &sm.Tf[16 * j][16 * j], LDF, lane);
-      st16_f32(&sm.scr[wave][0][0], 20, p, 1.f, lane);
-      wave_sync();
-      f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-      t2 = mm16_f32(t2, &sm.Tf[16 * i][16 * i], LDF, &sm.scr[wave][0][0], 20, lane);
-      st16_f32(&sm.Tf[16 * i][16 * j], LDF, t2, -1.f, lane);
-    } else if (wave == 3) {
-      f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-      p = mm16_f32(p, &sm.Lf[48][0], LDF, &sm.Tf[0][0], LDF, lane);  // L30 T00
-      st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
-    }
-    __syncthreads();
-    // second sub-diagonal: T20, T31; partial sum for T30
-    if (wave == 0) {
-      f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-      p = mm16_f32(p, &sm.Lf[32][0], LDF, &sm.Tf[0][0], LDF, lane);    // L20 T00
-      p = mm16_f32(p, &sm.Lf[32][16], LDF, &sm.Tf[16][0], LDF, lane);  // L21 T10
-      st16_f32(&sm.scr[0][0][0], 20, p, 1.f, lane);
-      wave_sync();
-      f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-      t2 = mm16_f32(t2, &sm.Tf[32][32], LDF, &sm.scr[0][0][0], 20, lane);
-      st16_f32(&sm.Tf[32][0], LDF, t2, -1.f, lane);
-    } else if (wave == 1) {
-      f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-      p = mm16_f32(p, &sm.Lf[48][16], LDF, &sm.Tf[16][16], LDF, lane);  // L31 T11
-      p = mm16_f32(p, &sm.Lf[48][32], LDF, &sm.Tf[32][16], LDF, lane);  // L32 T21
-      st16_f32(&sm.scr[1][0][0], 20, p, 1.f, lane);
-      wave_sync();
-      f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-      t2 = mm16_f32(t2, &sm.Tf[48][48], LDF, &sm.scr[1][0][0], 20, lane);
-      st16_f32(&sm.Tf[48][16], LDF, t2, -1.f, lane);
-    } else if (wave == 3) {
-      f32x4_t p = ld16_f32(&sm.scr[3][0][0], 20, lane);
-      p = mm16_f32(p, &sm.Lf[48][16], LDF, &sm.Tf[16][0], LDF, lane);  // + L31 T10
-      st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
-    }
-    __syncthreads();
-    // third sub-diagonal: T30
-    if (wave == 3) {
-      f32x4_t p = ld16_f32(&sm.scr[3][0][0], 20, lane);
-      p = mm16_f32(p, &sm.Lf[48][32], LDF, &sm.Tf[32][0], LDF, lane);  // + L32 T20
-      st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
-      wave_sync();
-      f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-      t2 = mm16_f32(t2, &sm.Tf[48][48], LDF, &sm.scr[3][0][0], 20, lane);
-      st16_f32(&sm.Tf[48][0], LDF, t2, -1.f, lane);
-    }
-    __syncthreads();
-
-    // ---- phase 4: T' (bf16) and T'' (hi/lo), 4 columns per thread; zero the
-    //      upper tiles of A_qk ----
-    for (int e4 = tid; e4 < kC * (kC / 4); e4 += NT) {
-      const int t = e4 >> 4, s0 = (e4 & 15) * 4;
-      const bool lower = (s0 >> 4) <= (t >> 4);
-      float4 tv = lower ? *reinterpret_cast<const float4*>(&sm.Tf[t][s0]) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float4 cw = *reinterpret_cast<const float4*>(&sm.cW[s0]);
-      const float4 cb = *reinterpret_cast<const float4*>(&sm.bt[s0]);
-      uint2 tp;
-      tp.x = gdn::f2bf2(tv.x * cw.x, tv.y * cw.y);
-      tp.y = gdn::f2bf2(tv.z * cw.z, tv.w * cw.w);
-      *reinterpret_cast<uint2*>(&sm.Tp[t][s0]) = tp;
-      const float u0 = tv.x * cb.x, u1 = tv.y * cb.y, u2 = tv.z * cb.z, u3 = tv.w * cb.w;
-      uint2 uh, ul;
-      uh.x = gdn::f2bf2(u0, u1);
-      uh.y = gdn::f2bf2(u2, u3);
-      ul.x = gdn::f2bf2(u0 - lo_half(uh.x), u1 - hi_half(uh.x));
-      ul.y = gdn::f2bf2(u2 - lo_half(uh.y), u3 - hi_half(uh.y));
-      *reinterpret_cast<uint2*>(&sm.Uh[t][s0]) = uh;
-      *reinterpret_cast<uint2*>(&sm.Ul[t][s0]) = ul;
-      if (!lower) {
-        *reinterpret_cast<uint2*>(&sm.Ah[t][s0]) = make_uint2(0u, 0u);
-        *reinterpret_cast<uint2*>(&sm.Al[t][s0]) = make_uint2(0u, 0u);
-      }
-    }
-    __syncthreads();
-
-    // ---- phase 5: W = T' K (shared by all waves; overwrites K row-major) ----
-    {
-      constexpr int NJ = (4 * MTD + NW - 1) / NW;
-#pragma unroll
-      for (int jj = 0; jj < NJ; ++jj) {
-        const int j = wave + NW * jj;
-        if (j >= 4 * MTD) break;
-        const int mt = j % 4, nt = j / 4;
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Tp[16 * mt + lr][32 * kt + 8 * lg]);
-          const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.Kt[16 * nt + lr][32 * kt + 8 * lg]);
-          acc = gdn::mfma16x16x32(a8, b8, acc);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sm.KrW[16 * mt + 4 * lg + i][16 * nt + lr] = gdn::f2bf(acc[i]);
-      }
-    }
-    __syncthreads();
-    // ---- phase 6: per-wave state chain (registers only) ----
+    // ---- per-wave state chain (registers only) ----
     {
       // W S and Q S with S split hi/lo per contraction step (key dim)
-      f32x4_t ws[4], qs[4];
+      f32x4_t wsum[4], qs[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        ws[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        wsum[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         qs[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
@@ -498,30 +686,22 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
         split_frag(S[2 * kt], S[2 * kt + 1], sh, sl);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-          const s16x8_t wa = perm_frag(&sm.KrW[16 * mt + lr][32 * kt], lg);
+          const s16x8_t wa = perm_frag(&sm.W[16 * mt + lr][32 * kt], lg);
           const s16x8_t qa = perm_frag(&sm.Qs[16 * mt + lr][32 * kt], lg);
-          ws[mt] = gdn::mfma16x16x32(wa, sh, ws[mt]);
-          ws[mt] = gdn::mfma16x16x32(wa, sl, ws[mt]);
+          wsum[mt] = gdn::mfma16x16x32(wa, sh, wsum[mt]);
+          wsum[mt] = gdn::mfma16x16x32(wa, sl, wsum[mt]);
           qs[mt] = gdn::mfma16x16x32(qa, sh, qs[mt]);
           qs[mt] = gdn::mfma16x16x32(qa, sl, qs[mt]);
         }
       }
-      // U = T'' V, Vn = U - W S, O_inter = diag(cQ) Q S
+      // Vn = U - W S, O_inter = diag(cQ) Q S
       f32x4_t vn[4], oo[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        f32x4_t u = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const s16x8_t ah = *reinterpret_cast<const s16x8_t*>(&sm.Uh[16 * mt + lr][32 * kt + 8 * lg]);
-          const s16x8_t al = *reinterpret_cast<const s16x8_t*>(&sm.Ul[16 * mt + lr][32 * kt + 8 * lg]);
-          u = gdn::mfma16x16x32(ah, vf[kt], u);
-          u = gdn::mfma16x16x32(al, vf[kt], u);
-        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 16 * mt + 4 * lg + i;
-          vn[mt][i] = u[i] - ws[mt][i];
+          vn[mt][i] = U[mt][i] - wsum[mt][i];
           oo[mt][i] = sm.cQ[t] * qs[mt][i];
         }
       }
@@ -585,39 +765,57 @@ __global__ __launch_bounds__(64 * NW) void chunk_prefill_kernel(
   }
 }
 
-template <int D, int NW>
+template <int D, int NWL, int NWC>
 int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, const uint16_t* v,
                  int64_t sv, const float* g, const uint16_t* beta, const float* h0, float* hT,
-                 const int64_t* ids, int64_t sstride, const int64_t* cu, int n_seqs, int Hk,
-                 int Hv, float scale, int l2norm, uint16_t* o, hipStream_t stream) {
-  constexpr int NVB = D / (16 * NW);
-  const int64_t work = static_cast<int64_t>(n_seqs) * Hv * NVB;
-  const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  chunk_prefill_kernel<D, NW><<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, stream>>>(
-      q, sq, k, sk, v, sv, g, beta, h0, hT, ids, sstride, cu, n_seqs, Hk, Hv, scale, l2norm, o);
+                 const int64_t* ids, int64_t sstride, const int64_t* cu, int n_seqs, int64_t nc_bound,
+                 int Hk, int Hv, float scale, int l2norm, uint16_t* o, uint8_t* ws, hipStream_t stream) {
+  const int64_t lwork = nc_bound * Hv;
+  const int64_t lgrid = gdn::kNumXcd * ((lwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
+  chunk_local_kernel<D, NWL><<<dim3(static_cast<unsigned>(lgrid)), dim3(64 * NWL), 0, stream>>>(
+      q, sq, k, sk, v, sv, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws);
+  const int st = gdn_launch_status();
+  if (st != GDN_OK) return st;
+  const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv;
+  const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
+  chunk_chain_kernel<D, NWC><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * NWC), 0, stream>>>(
+      q, sq, ws, h0, hT, ids, sstride, cu, n_seqs, Hk, Hv, o);
   return gdn_launch_status();
 }
 
+int64_t record_bytes(int D) { return D == 128 ? Rec<128>::BYTES : Rec<64>::BYTES; }
+
 }  // namespace
+
+extern "C" int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D) {
+  if (N < 0 || n_seqs < 0 || Hv <= 0 || (D != 64 && D != 128)) return -1;
+  const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
+  return nc_bound * Hv * record_bytes(D);
+}
 
 extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k,
                                  int64_t sk_tok, const uint16_t* v, int64_t sv_tok, const float* g,
                                  const uint16_t* beta, const float* h0, float* hT,
                                  const int64_t* state_ids, int64_t state_stride,
                                  const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv,
-                                 int D, float scale, int l2norm, uint16_t* o, void* stream) {
+                                 int D, float scale, int l2norm, uint16_t* o, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
   if (n_seqs < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
   if (n_seqs == 0) return GDN_OK;
-  if (!q || !k || !v || !g || !beta || !cu_seqlens || !o) return GDN_ERR_INVALID_ARG;
-  // 16-byte row fragments of q / k and float state rows
+  if (!q || !k || !v || !g || !beta || !cu_seqlens || !o || !workspace) return GDN_ERR_INVALID_ARG;
+  // 16-byte row fragments of q / k, float state rows, 256-byte workspace records
   if (sq_tok % 8 || sk_tok % 8 || reinterpret_cast<uintptr_t>(q) % 16 ||
-      reinterpret_cast<uintptr_t>(k) % 16 || ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
+      reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(workspace) % 256 ||
+      ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
     return GDN_ERR_INVALID_ARG;
+  const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
+  if (workspace_bytes < nc_bound * Hv * record_bytes(D)) return GDN_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
   if (D == 128)
-    return launch_chunk<128, 8>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids,
-                                state_stride, cu_seqlens, n_seqs, Hk, Hv, scale, l2norm, o, s);
-  return launch_chunk<64, 4>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids,
-                             state_stride, cu_seqlens, n_seqs, Hk, Hv, scale, l2norm, o, s);
+    return launch_chunk<128, 8, 8>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
+                                   cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, s);
+  return launch_chunk<64, 4, 4>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
+                                cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, s);
 }

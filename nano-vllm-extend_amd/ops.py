@@ -227,10 +227,16 @@ def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     if scale is None:
         scale = D ** -0.5
     o = torch.empty(N, Hv, D, dtype=v.dtype, device=v.device)
+    # per-(chunk, head) records of the chunk-local phase; the caching
+    # allocator's blocks are 512-byte aligned, the kernels need 256
+    ws_bytes = _lib.load().gdn_chunk_prefill_workspace_size(N, n, Hv, D)
+    if ws_bytes < 0:
+        raise ValueError(f"unsupported chunk shape N={N} n_seqs={n} Hv={Hv} D={D}")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     _lib.call("gdn_chunk_prefill", _lib.ptr(q), q.stride(0), _lib.ptr(k), k.stride(0), _lib.ptr(v),
               v.stride(0), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0), _lib.ptr(hT), _lib.ptr(ids),
               sstride, _lib.ptr(cu), n, N, Hk, Hv, D, float(scale), int(bool(use_qk_l2norm_in_kernel)),
-              _lib.ptr(o), _stream(dev))
+              _lib.ptr(o), _lib.ptr(ws), ws_bytes, _stream(dev))
     return o, hT
 
 

@@ -16,7 +16,7 @@ def _declared():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"\bint\s+(gdn_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.S):
+    for m in re.finditer(r"\b(?:int|int64_t)\s+(gdn_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.S):
         args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
         decls[m.group(1)] = len(args)
     return decls
@@ -25,7 +25,8 @@ def _declared():
 def test_header_declares_entry_points():
     d = _declared()
     for name in ("gdn_abi_version", "gdn_g_beta", "gdn_conv_varlen", "gdn_conv_decode", "gdn_conv_padded",
-                 "gdn_chunk_prefill", "gdn_recurrent", "gdn_state_commit", "gdn_rmsnorm_gated"):
+                 "gdn_chunk_prefill", "gdn_chunk_prefill_workspace_size", "gdn_recurrent", "gdn_state_commit",
+                 "gdn_rmsnorm_gated"):
         assert name in d
 
 
@@ -61,13 +62,13 @@ def test_argument_validation_before_launch(pkg):
     _lib = pkg._lib
     # unsupported head dim
     assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, 1, 64,
-                                 1, 1, 96, 1.0, 1, None, None) == _lib.GDN_ERR_UNSUPPORTED
+                                 1, 1, 96, 1.0, 1, None, None, 0, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_recurrent(None, 0, 0, None, 0, 0, None, 0, 0, None, None, None, 0, None, 0, None, None,
                              None, 1, 1, 1, 1, 32, 1.0, 1, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_rmsnorm_gated(None, 0, None, 0, None, None, 4, 1, 256, 1e-6, None) == _lib.GDN_ERR_UNSUPPORTED
     # head grouping must divide
     assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, 1, 64,
-                                 3, 4, 128, 1.0, 1, None, None) == _lib.GDN_ERR_INVALID_ARG
+                                 3, 4, 128, 1.0, 1, None, None, 0, None) == _lib.GDN_ERR_INVALID_ARG
     # conv width other than 4, and misaligned channel counts
     assert lib.gdn_conv_decode(None, 0, None, 0, 0, None, None, None, 0, 1, 64, 3, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_conv_varlen(None, 0, None, 0, 0, None, None, None, 8, None, None, 1, 4, 30, 4,
