@@ -37,6 +37,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file additions.  The chunk kernels read MFMA operands from LDS in long
+# runs with one wave per SIMD; the ILP-oriented scheduler batches those reads
+# ahead of their MFMAs instead of waiting on each pair in turn.
+FILE_FLAGS = {
+    "chunk_prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -51,7 +59,7 @@ def _torch_lib_dir() -> Path:
 
 
 def _compile(src: Path, obj: Path, extra: list[str]) -> tuple[Path, str]:
-    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")

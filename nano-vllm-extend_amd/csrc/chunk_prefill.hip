@@ -41,17 +41,38 @@ using gdn::s16x8_t;
 
 constexpr int kC = 64;  // chunk size
 
-// ---- workspace record of one (chunk, value head), byte offsets ----
+// ---- workspace record of one (chunk, value head) ----
+// A sequence of 1 KiB blocks.  Each bf16 block is one MFMA A operand of the
+// chain kernel in lane order (lane l's 8 values at bytes [16 l, 16 l + 16)),
+// already in the permuted contraction order of perm_frag; so the chain stages
+// a record with linear 16-byte copies and reads every operand with one
+// conflict-free 16-byte LDS read per lane.
+//   W   [mt][kt]   rows 16 mt.. of W = T' K_raw, key dims 32 kt..
+//   Q   [mt][kt]   raw bf16 q rows (zero past the sequence end)
+//   K   [mt][kt]   key dims 16 mt.. of K_raw^T, tokens 32 kt..
+//   AH, AL         the six (mt, kt) blocks of lower(A_qk) with 32 kt <= 16 mt + 15
+//   VEC            fp32 cQ[64], cK[64], e^gamma
+//   U   [nt][mt]   fp32 C fragments of U = T'' V (value columns 16 nt..)
+// Blocks [0, SHARED) are what every wave of a chain workgroup reads; U is
+// per wave.
 template <int D>
 struct Rec {
-  static constexpr int64_t W = 0;                        // bf16 [64][D]    W = T' K_raw
-  static constexpr int64_t KT = W + 64 * D * 2;          // bf16 [D][64]    K_raw^T
-  static constexpr int64_t AH = KT + D * 64 * 2;         // bf16 [64][64]   A_qk hi
-  static constexpr int64_t AL = AH + 64 * 64 * 2;        // bf16 [64][64]   A_qk lo
-  static constexpr int64_t U = AL + 64 * 64 * 2;         // fp32 C fragments of U = T'' V
-  static constexpr int64_t VEC = U + 64 * D * 4;         // fp32 cQ[64], cK[64], e^gamma
-  static constexpr int64_t BYTES = (VEC + 144 * 4 + 255) / 256 * 256;
+  static constexpr int KTD = D / 32;
+  static constexpr int MTD = D / 16;
+  static constexpr int W = 0;
+  static constexpr int Q = W + 4 * KTD;
+  static constexpr int K = Q + 4 * KTD;
+  static constexpr int AH = K + 2 * MTD;
+  static constexpr int AL = AH + 6;
+  static constexpr int VEC = AL + 6;
+  static constexpr int SHARED = VEC + 1;
+  static constexpr int U = SHARED;
+  static constexpr int BLOCKS = U + 4 * MTD;
+  static constexpr int64_t BYTES = static_cast<int64_t>(BLOCKS) * 1024;
 };
+
+// block of lower(A_qk) tile (mt, kt), 32 kt <= 16 mt + 15
+__device__ __forceinline__ int a_block(int mt, int kt) { return mt < 2 ? mt : 2 * mt - 2 + kt; }
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -459,7 +480,7 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
     }
     // U tiles: column tile nt (16 value columns) x 4 row tiles; record layout
     // [nt][mt][lane] float4, i.e. exactly the C fragments the chain kernel holds
-    float4* urec = reinterpret_cast<float4*>(rec + Rec<D>::U);
+    float4* urec = reinterpret_cast<float4*>(rec + Rec<D>::U * 1024);
     for (int nt = wave; nt < MTD; nt += NW) {
       s16x8_t vf[2];
       const int col = 16 * nt + lr;
@@ -487,26 +508,29 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
   }
   __syncthreads();
 
-  // ---- record: W, K^T, A_qk hi/lo (16-byte copies), vectors ----
+  // ---- record: operand blocks in lane order (see Rec) ----
   {
-    uint4* wrec = reinterpret_cast<uint4*>(rec + Rec<D>::W);
-    for (int e = tid; e < kC * SEG; e += NT) {
-      const int t = e / SEG, c8 = e % SEG;
-      wrec[e] = *reinterpret_cast<const uint4*>(&sm.KrW[t][c8 * 8]);
+    s16x8_t* blk = reinterpret_cast<s16x8_t*>(rec);
+    for (int e = tid; e < Rec<D>::VEC * 64; e += NT) {
+      const int b = e >> 6, l = e & 63, flr = l & 15, flg = l >> 4;
+      const uint16_t* row;
+      if (b < Rec<D>::Q) {
+        const int mt = b / KTD, kt = b % KTD;
+        row = &sm.KrW[16 * mt + flr][32 * kt];
+      } else if (b < Rec<D>::K) {
+        const int x = b - Rec<D>::Q, mt = x / KTD, kt = x % KTD;
+        row = &sm.Qs[16 * mt + flr][32 * kt];
+      } else if (b < Rec<D>::AH) {
+        const int x = b - Rec<D>::K, mt = x >> 1, kt = x & 1;
+        row = &sm.Kt[16 * mt + flr][32 * kt];
+      } else {
+        const int x = b < Rec<D>::AL ? b - Rec<D>::AH : b - Rec<D>::AL;
+        const int mt = x < 2 ? x : 2 + ((x - 2) >> 1), kt = x < 2 ? 0 : ((x - 2) & 1);
+        row = b < Rec<D>::AL ? &sm.Ah[16 * mt + flr][32 * kt] : &sm.Al[16 * mt + flr][32 * kt];
+      }
+      blk[e] = perm_frag(row, flg);
     }
-    uint4* krec = reinterpret_cast<uint4*>(rec + Rec<D>::KT);
-    for (int e = tid; e < D * (kC / 8); e += NT) {
-      const int d = e / (kC / 8), c8 = e % (kC / 8);
-      krec[e] = *reinterpret_cast<const uint4*>(&sm.Kt[d][c8 * 8]);
-    }
-    uint4* ahrec = reinterpret_cast<uint4*>(rec + Rec<D>::AH);
-    uint4* alrec = reinterpret_cast<uint4*>(rec + Rec<D>::AL);
-    for (int e = tid; e < kC * (kC / 8); e += NT) {
-      const int t = e / (kC / 8), c8 = e % (kC / 8);
-      ahrec[e] = *reinterpret_cast<const uint4*>(&sm.Ah[t][c8 * 8]);
-      alrec[e] = *reinterpret_cast<const uint4*>(&sm.Al[t][c8 * 8]);
-    }
-    float* vrec = reinterpret_cast<float*>(rec + Rec<D>::VEC);
+    float* vrec = reinterpret_cast<float*>(rec + Rec<D>::VEC * 1024);
     if (tid < kC) {
       vrec[tid] = sm.cQ[tid];
       vrec[kC + tid] = sm.cK[tid];
@@ -516,107 +540,62 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
 }
 
 // ============================================================ chain kernel ==
+// Double-buffered LDS copy of one chunk's record: the shared blocks plus the
+// U blocks of the workgroup's NW column tiles.
 template <int D, int NW>
 struct __align__(16) ChainSmem {
-  uint16_t Kt[D][kC + 8];
-  uint16_t Qs[kC][D + 8];
-  uint16_t W[kC][D + 8];
-  uint16_t Ah[kC][kC + 8];
-  uint16_t Al[kC][kC + 8];
-  float cQ[kC], cK[kC];
-  float eg_last;
+  static constexpr int NB = Rec<D>::SHARED + 4 * NW;  // 1 KiB blocks per chunk
+  s16x8_t buf[2][NB][64];
 };
 
-// Per-chunk operands the whole workgroup shares, moved global -> registers a
-// chunk ahead, then registers -> LDS.  16-byte segments, NSEG per thread.
+constexpr int kChainLoaders = 2;  // loader waves per chain workgroup
+
+// One loader wave's share of a chunk's copy, global -> LDS with no registers:
+// shared blocks b = li, li + kChainLoaders, ..., then the U blocks of the
+// workgroup's column tiles.  rec already includes the lane's 16-byte offset;
+// the hardware writes lane l's 16 bytes at dst block + 16 l.
 template <int D, int NW>
-struct ChainPrefetch {
-  static constexpr int NT = 64 * NW;
-  static constexpr int SEG = D / 8;
-  static constexpr int W_SEGS = kC * SEG;           // W   [64][D]
-  static constexpr int K_SEGS = D * (kC / 8);       // K^T [D][64]
-  static constexpr int A_SEGS = kC * (kC / 8);      // A_qk hi, lo [64][64]
-  static constexpr int Q_SEGS = kC * SEG;           // Q   [64][D] (raw input)
-  static constexpr int REC_SEGS = W_SEGS + K_SEGS + 2 * A_SEGS;
-  static constexpr int TOTAL = REC_SEGS + Q_SEGS;
-  static constexpr int NSEG = TOTAL / NT;
-  static_assert(TOTAL % NT == 0 && REC_SEGS % NT == 0 && W_SEGS % NT == 0 && K_SEGS % NT == 0 &&
-                A_SEGS % NT == 0, "segment tiling");
-  s16x8_t seg[NSEG];
-  f32x4_t u[4];
-  float vec;
+__device__ __forceinline__ void copy_record(const uint8_t* rec, s16x8_t (*dst)[64], int li, int cb) {
+  using R = Rec<D>;
+  for (int b = li; b < R::SHARED; b += kChainLoaders)
+    __builtin_amdgcn_global_load_lds(rec + b * 1024, &dst[b][0], 16, 0, 0);
+  const uint8_t* urec = rec + static_cast<int64_t>(R::U + 4 * NW * cb) * 1024;
+  for (int b = li; b < 4 * NW; b += kChainLoaders)
+    __builtin_amdgcn_global_load_lds(urec + b * 1024, &dst[R::SHARED + b][0], 16, 0, 0);
+}
 
-  __device__ __forceinline__ void load(const uint8_t* rec, const uint16_t* qh, int64_t sq, int64_t tok0, int len,
-                                       int tid, int wave, int lane) {
-#pragma unroll
-    for (int j = 0; j < NSEG; ++j) {
-      const int e = tid + NT * j;
-      if (j < REC_SEGS / NT) {
-        seg[j] = reinterpret_cast<const s16x8_t*>(rec)[e];  // W, K^T, A hi, A lo are contiguous
-      } else {
-        const int qe = e - REC_SEGS;
-        const int t = qe / SEG, c8 = qe % SEG;
-        seg[j] = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, len - 1)) * sq + c8 * 8);
-      }
-    }
-    const float4* urec = reinterpret_cast<const float4*>(rec + Rec<D>::U);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const float4 f = urec[(wave * 4 + mt) * 64 + lane];
-      u[mt] = f32x4_t{f.x, f.y, f.z, f.w};
-    }
-    vec = reinterpret_cast<const float*>(rec + Rec<D>::VEC)[min(tid, 2 * kC)];
-  }
-
-  __device__ __forceinline__ void stage(ChainSmem<D, NW>& sm, int tid) const {
-#pragma unroll
-    for (int j = 0; j < NSEG; ++j) {
-      const int e = tid + NT * j;
-      if (j < W_SEGS / NT) {
-        *reinterpret_cast<s16x8_t*>(&sm.W[e / SEG][(e % SEG) * 8]) = seg[j];
-      } else if (j < (W_SEGS + K_SEGS) / NT) {
-        const int x = e - W_SEGS;
-        *reinterpret_cast<s16x8_t*>(&sm.Kt[x / (kC / 8)][(x % (kC / 8)) * 8]) = seg[j];
-      } else if (j < (W_SEGS + K_SEGS + A_SEGS) / NT) {
-        const int x = e - W_SEGS - K_SEGS;
-        *reinterpret_cast<s16x8_t*>(&sm.Ah[x / (kC / 8)][(x % (kC / 8)) * 8]) = seg[j];
-      } else if (j < REC_SEGS / NT) {
-        const int x = e - W_SEGS - K_SEGS - A_SEGS;
-        *reinterpret_cast<s16x8_t*>(&sm.Al[x / (kC / 8)][(x % (kC / 8)) * 8]) = seg[j];
-      } else {
-        const int x = e - REC_SEGS;
-        *reinterpret_cast<s16x8_t*>(&sm.Qs[x / SEG][(x % SEG) * 8]) = seg[j];
-      }
-    }
-    if (tid < kC) sm.cQ[tid] = vec;
-    else if (tid < 2 * kC) sm.cK[tid - kC] = vec;
-    else if (tid == 2 * kC) sm.eg_last = vec;
-  }
-};
-
-// grid = 8 * ceil(n_seqs * Hv / 8); block = 64 * NW; wave w owns the state
-// columns [16w, 16w + 16) of value head h.
+// grid = 8 * ceil(n_seqs * Hv * NCB / 8), NCB = D / (16 NW);
+// block = 64 (NW + kChainLoaders).
+// Workgroup (sequence r, value head h, column block cb).  Waves 0..NW-1
+// compute: wave w owns the state columns [16 nt, 16 nt + 16), nt = cb NW + w.
+// Value columns of S evolve independently, so the column blocks of one head
+// never communicate.  Waves NW.. only move data: they copy chunk j + 1's
+// record into the other LDS buffer (global -> LDS, no registers) while the
+// compute waves work on chunk j; one barrier per chunk hands the buffers over.
+// The compute waves issue no loads at all inside the loop.  Two loader waves
+// keep a whole record in flight (a wave can have at most 63 loads
+// outstanding).
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void chunk_chain_kernel(
-    const uint16_t* __restrict__ q, int64_t sq, const uint8_t* __restrict__ ws,
-    const float* h0, float* hT, const int64_t* __restrict__ ids, int64_t sstride,
-    const int64_t* __restrict__ cu, int n_seqs, int Hk, int Hv, uint16_t* __restrict__ o) {
-  constexpr int KTD = D / 32;
-  constexpr int MTD = D / 16;
-  static_assert(16 * NW == D, "one wave per 16 state columns");
-  using PF = ChainPrefetch<D, NW>;
-  __shared__ ChainSmem<D, NW> sm;
+__global__ __launch_bounds__(64 * (NW + kChainLoaders)) void chunk_chain_kernel(
+    const uint8_t* __restrict__ ws, const float* h0, float* hT, const int64_t* __restrict__ ids,
+    int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hv, uint16_t* __restrict__ o) {
+  using R = Rec<D>;
+  using SM = ChainSmem<D, NW>;
+  constexpr int KTD = R::KTD;
+  constexpr int MTD = R::MTD;
+  constexpr int NCB = MTD / NW;
+  static_assert(MTD % NW == 0, "column blocks tile the head");
+  __shared__ SM sm;
   __shared__ long long s_base;
 
-  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(n_seqs) * Hv);
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(n_seqs) * Hv * NCB);
   if (wi < 0) return;
-  const int h = static_cast<int>(wi % Hv);
-  const int r = static_cast<int>(wi / Hv);
-  const int kh = h / (Hv / Hk);
+  const int cb = static_cast<int>(wi % NCB);
+  const int h = static_cast<int>((wi / NCB) % Hv);
+  const int r = static_cast<int>(wi / (static_cast<int64_t>(NCB) * Hv));
   const int64_t bos = cu[r];
   const int64_t seqlen = cu[r + 1] - bos;
-  const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
-  const int64_t srow = ids ? ids[r] : r;
+  const int64_t nch = chunks_of(seqlen);
 
   // first workspace chunk of this sequence: sum of earlier sequences' chunks
   if (threadIdx.x < 64) {
@@ -629,7 +608,27 @@ __global__ __launch_bounds__(64 * NW) void chunk_chain_kernel(
   __syncthreads();
   const int64_t cbase = s_base;
 
-  const int vcol0 = 16 * (threadIdx.x >> 6) + (threadIdx.x & 15);
+  const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (wave_id >= NW) {
+    // ---- loader waves: nch + 1 barriers, matching the compute waves ----
+    const int lane = threadIdx.x & 63;
+    const int li = wave_id - NW;
+    const uint8_t* rec0 = ws + (cbase * Hv + h) * R::BYTES + lane * 16;
+    if (nch > 0) copy_record<D, NW>(rec0, sm.buf[0], li, cb);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed in LDS
+    gdn::lds_barrier();
+    for (int64_t j = 0; j < nch; ++j) {
+      if (j + 1 < nch) copy_record<D, NW>(rec0 + (j + 1) * Hv * R::BYTES, sm.buf[(j + 1) & 1], li, cb);
+      __builtin_amdgcn_s_waitcnt(0);
+      gdn::lds_barrier();
+    }
+    return;
+  }
+
+  // ---- compute waves ----
+  const int64_t srow = ids ? ids[r] : r;
+  const int nt0 = cb * NW + (threadIdx.x >> 6);
+  const int vcol0 = 16 * nt0 + (threadIdx.x & 15);
   const int lg0 = (threadIdx.x & 63) >> 4;
   f32x4_t S[MTD];
   if (h0) {
@@ -642,14 +641,10 @@ __global__ __launch_bounds__(64 * NW) void chunk_chain_kernel(
 #pragma unroll
     for (int mt = 0; mt < MTD; ++mt) S[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+  gdn::lds_barrier();  // chunk 0 is in buffer 0
 
-  PF pf;
-  if (seqlen > 0)
-    pf.load(ws + (cbase * Hv + h) * Rec<D>::BYTES, qh, sq, bos, static_cast<int>(min<int64_t>(kC, seqlen)),
-            threadIdx.x, threadIdx.x >> 6, threadIdx.x & 63);
-
-  int64_t jc = 0;
-  for (int64_t c0 = 0; c0 < seqlen; c0 += kC, ++jc) {
+  for (int64_t jc = 0; jc < nch; ++jc) {
+    const int64_t c0 = jc * kC;
     const int len = static_cast<int>(min<int64_t>(kC, seqlen - c0));
     const int64_t tok0 = bos + c0;
     // Re-derive the lane indices from an opaque copy each chunk: otherwise the
@@ -657,103 +652,105 @@ __global__ __launch_bounds__(64 * NW) void chunk_chain_kernel(
     // them all live in VGPRs, which spills.
     int tid_l = static_cast<int>(threadIdx.x);
     asm volatile("" : "+v"(tid_l));
-    const int tid = tid_l;
     const int lane = tid_l & 63;
-    const int lr = lane & 15;
     const int lg = lane >> 4;
-    const int wave = __builtin_amdgcn_readfirstlane(tid_l >> 6);
-    const int vcol = 16 * wave + lr;
-    __syncthreads();  // previous chunk's LDS readers are done
-    pf.stage(sm, tid);
-    const f32x4_t U[4] = {pf.u[0], pf.u[1], pf.u[2], pf.u[3]};
-    if (c0 + kC < seqlen)
-      pf.load(ws + ((cbase + jc + 1) * Hv + h) * Rec<D>::BYTES, qh, sq, tok0 + kC,
-              static_cast<int>(min<int64_t>(kC, seqlen - c0 - kC)), tid, wave, lane);
-    __syncthreads();
+    const int lr = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid_l >> 6);
+    const int nt = cb * NW + w;
+    const int vcol4 = 16 * nt + 4 * lg;  // first of the lane's 4 output columns
+    const s16x8_t(*blk)[64] = sm.buf[jc & 1];
+    f32x4_t U[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) U[mt] = __builtin_bit_cast(f32x4_t, blk[R::SHARED + 4 * w + mt][lane]);
+    const float* vec = reinterpret_cast<const float*>(&blk[R::VEC][0]);
 
-    // ---- per-wave state chain (registers only) ----
-    {
-      // W S and Q S with S split hi/lo per contraction step (key dim)
-      f32x4_t wsum[4], qs[4];
+    // W S (Vn = U - W S) and, transposed, O^T = S^T Q^T: the fragments of S
+    // serve as the B operand of the first and the A operand of the second, the
+    // Q blocks as A and B operand respectively.  The transposed output tile
+    // gives each lane 4 consecutive value columns of one token.
+    f32x4_t wsum[4], ot[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      wsum[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      ot[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int kt = 0; kt < KTD; ++kt) {
+      s16x8_t sh, sl;
+      split_frag(S[2 * kt], S[2 * kt + 1], sh, sl);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        wsum[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        qs[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int kt = 0; kt < KTD; ++kt) {
-        s16x8_t sh, sl;
-        split_frag(S[2 * kt], S[2 * kt + 1], sh, sl);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const s16x8_t wa = perm_frag(&sm.W[16 * mt + lr][32 * kt], lg);
-          const s16x8_t qa = perm_frag(&sm.Qs[16 * mt + lr][32 * kt], lg);
-          wsum[mt] = gdn::mfma16x16x32(wa, sh, wsum[mt]);
-          wsum[mt] = gdn::mfma16x16x32(wa, sl, wsum[mt]);
-          qs[mt] = gdn::mfma16x16x32(qa, sh, qs[mt]);
-          qs[mt] = gdn::mfma16x16x32(qa, sl, qs[mt]);
-        }
-      }
-      // Vn = U - W S, O_inter = diag(cQ) Q S
-      f32x4_t vn[4], oo[4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = 16 * mt + 4 * lg + i;
-          vn[mt][i] = U[mt][i] - wsum[mt][i];
-          oo[mt][i] = sm.cQ[t] * qs[mt][i];
-        }
-      }
-      // Vn and Vn' = diag(cK) Vn as B fragments (contraction over tokens)
-      s16x8_t vh_[2], vl_[2], ph[2], pl[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        split_frag(vn[2 * kt], vn[2 * kt + 1], vh_[kt], vl_[kt]);
-        f32x4_t p0, p1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p0[i] = vn[2 * kt][i] * sm.cK[32 * kt + 4 * lg + i];
-          p1[i] = vn[2 * kt + 1][i] * sm.cK[32 * kt + 16 + 4 * lg + i];
-        }
-        split_frag(p0, p1, ph[kt], pl[kt]);
-      }
-      // O += A_qk Vn (lower-triangular: skip the all-zero upper k-steps)
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int ta = 16 * mt + lr;
-        f32x4_t acc = oo[mt];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          if (32 * kt > 16 * mt + 15) break;
-          const s16x8_t ah = perm_frag(&sm.Ah[ta][32 * kt], lg);
-          const s16x8_t al = perm_frag(&sm.Al[ta][32 * kt], lg);
-          acc = gdn::mfma16x16x32(ah, vh_[kt], acc);
-          acc = gdn::mfma16x16x32(ah, vl_[kt], acc);
-          acc = gdn::mfma16x16x32(al, vh_[kt], acc);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = 16 * mt + 4 * lg + i;
-          if (t < len) o[((tok0 + t) * Hv + h) * D + vcol] = gdn::f2bf(acc[i]);
-        }
-      }
-      // S <- e^gamma S + K^T Vn'
-      const float eg = sm.eg_last;
-#pragma unroll
-      for (int mt = 0; mt < MTD; ++mt) {
-        f32x4_t acc;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = S[mt][i] * eg;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const s16x8_t ka = perm_frag(&sm.Kt[16 * mt + lr][32 * kt], lg);
-          acc = gdn::mfma16x16x32(ka, ph[kt], acc);
-          acc = gdn::mfma16x16x32(ka, pl[kt], acc);
-        }
-        S[mt] = acc;
+        const s16x8_t wa = blk[R::W + mt * KTD + kt][lane];
+        const s16x8_t qa = blk[R::Q + mt * KTD + kt][lane];
+        wsum[mt] = gdn::mfma16x16x32(wa, sh, wsum[mt]);
+        wsum[mt] = gdn::mfma16x16x32(wa, sl, wsum[mt]);
+        ot[mt] = gdn::mfma16x16x32(sh, qa, ot[mt]);
+        ot[mt] = gdn::mfma16x16x32(sl, qa, ot[mt]);
       }
     }
+    // Vn = U - W S;  O^T_inter *= cQ (per token: lane's token 16 mt + lr)
+    f32x4_t vn[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const float cq = vec[16 * mt + lr];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vn[mt][i] = U[mt][i] - wsum[mt][i];
+        ot[mt][i] *= cq;
+      }
+    }
+    // Vn (hi/lo) and Vn' = diag(cK) Vn (hi/lo) fragments, contraction over tokens
+    s16x8_t vh_[2], vl_[2], ph[2], pl[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      split_frag(vn[2 * kt], vn[2 * kt + 1], vh_[kt], vl_[kt]);
+      const f32x4_t ck0 = *reinterpret_cast<const f32x4_t*>(&vec[kC + 32 * kt + 4 * lg]);
+      const f32x4_t ck1 = *reinterpret_cast<const f32x4_t*>(&vec[kC + 32 * kt + 16 + 4 * lg]);
+      f32x4_t p0, p1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p0[i] = vn[2 * kt][i] * ck0[i];
+        p1[i] = vn[2 * kt + 1][i] * ck1[i];
+      }
+      split_frag(p0, p1, ph[kt], pl[kt]);
+    }
+    // O^T += Vn^T A_qk^T (lower-triangular A_qk: only blocks with 32 kt <= 16 mt + 15)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      f32x4_t acc = ot[mt];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        if (32 * kt > 16 * mt + 15) break;
+        const s16x8_t ah = blk[R::AH + a_block(mt, kt)][lane];
+        const s16x8_t al = blk[R::AL + a_block(mt, kt)][lane];
+        acc = gdn::mfma16x16x32(vh_[kt], ah, acc);
+        acc = gdn::mfma16x16x32(vl_[kt], ah, acc);
+        acc = gdn::mfma16x16x32(vh_[kt], al, acc);
+      }
+      const int t = 16 * mt + lr;
+      if (t < len) {
+        uint2 pk;
+        pk.x = gdn::f2bf2(acc[0], acc[1]);
+        pk.y = gdn::f2bf2(acc[2], acc[3]);
+        *reinterpret_cast<uint2*>(&o[((tok0 + t) * Hv + h) * D + vcol4]) = pk;
+      }
+    }
+    // S <- e^gamma S + K^T Vn'
+    const float eg = vec[2 * kC];
+#pragma unroll
+    for (int mt = 0; mt < MTD; ++mt) {
+      f32x4_t acc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = S[mt][i] * eg;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const s16x8_t ka = blk[R::K + mt * 2 + kt][lane];
+        acc = gdn::mfma16x16x32(ka, ph[kt], acc);
+        acc = gdn::mfma16x16x32(ka, pl[kt], acc);
+      }
+      S[mt] = acc;
+    }
+    gdn::lds_barrier();  // done with this buffer; the next chunk is in the other
   }
 
   if (hT) {
@@ -776,10 +773,10 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
       q, sq, k, sk, v, sv, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws);
   const int st = gdn_launch_status();
   if (st != GDN_OK) return st;
-  const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv;
+  const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv * (D / 16 / NWC);
   const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  chunk_chain_kernel<D, NWC><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * NWC), 0, stream>>>(
-      q, sq, ws, h0, hT, ids, sstride, cu, n_seqs, Hk, Hv, o);
+  chunk_chain_kernel<D, NWC><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * (NWC + kChainLoaders)), 0, stream>>>(
+      ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o);
   return gdn_launch_status();
 }
 
@@ -804,9 +801,10 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
   if (n_seqs < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
   if (n_seqs == 0) return GDN_OK;
   if (!q || !k || !v || !g || !beta || !cu_seqlens || !o || !workspace) return GDN_ERR_INVALID_ARG;
-  // 16-byte row fragments of q / k, float state rows, 256-byte workspace records
+  // 16-byte row fragments of q / k, 8-byte output pieces, 256-byte workspace records
   if (sq_tok % 8 || sk_tok % 8 || reinterpret_cast<uintptr_t>(q) % 16 ||
-      reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(workspace) % 256 ||
+      reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(o) % 8 ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 ||
       ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
     return GDN_ERR_INVALID_ARG;
   const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
@@ -814,7 +812,7 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   if (D == 128)
-    return launch_chunk<128, 8, 8>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
+    return launch_chunk<128, 8, 4>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
                                    cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, s);
   return launch_chunk<64, 4, 4>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
                                 cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, s);

@@ -65,6 +65,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---- workgroup barrier ordering LDS only ----
+// __syncthreads() fences every address space, which on gfx950 waits for all
+// outstanding global loads (vmcnt(0)) and so drains a software prefetch at
+// each barrier.  This barrier orders LDS accesses only (lgkmcnt(0)); global
+// loads stay in flight across it.  Global memory written by one wave and read
+// by another still needs __syncthreads().
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---- XCD-aware block remap ----
 // Workgroups are dispatched round-robin over the 8 XCDs (block b lands on XCD
 // b % 8).  Remapping gives each XCD a contiguous range of work items, so the
