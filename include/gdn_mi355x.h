@@ -109,8 +109,8 @@ int gdn_conv_padded(const uint16_t* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
  *         fp32 dense; NULL = zero state.  hT likewise receives the final
  *         state (NULL = not written); row(r) = state_ids ? state_ids[r] : r.
  *         h0 == hT (in-place update of a slot pool) is allowed.
- *   o     [N, Hv, D] bf16 contiguous, 8-byte aligned; q, k 16-byte aligned with
- *         token strides a multiple of 8
+ *   o     [N, Hv, D] bf16 contiguous, 8-byte aligned; q, k, v 16-byte aligned
+ *         with token strides a multiple of 8
  *   l2norm != 0: q, k rows are L2-normalised in fp32 (eps 1e-6) first.
  *   workspace: device buffer of at least gdn_chunk_prefill_workspace_size()
  *         bytes, 256-byte aligned, owned by the caller.  It receives the

@@ -183,39 +183,88 @@ __device__ bool locate_chunk(const int64_t* __restrict__ cu, int n_seqs, int64_t
 }
 
 // ============================================================ local kernel ==
+// Lower 16x16 tile (mt, nt), nt <= mt, of a 64x64 lower-triangular matrix
+// stored as 10 packed tiles; index inverse of tri_tile.
+__device__ __forceinline__ int tix(int mt, int nt) { return (mt * (mt + 1)) / 2 + nt; }
+
+constexpr int kTileLd = 20;  // row stride (floats) of a packed fp32 tile
+
 template <int D, int NW>
 struct __align__(16) LocalSmem {
-  uint16_t Kt[D][kC + 8];       // K^T of the chunk (raw bf16), row = key dim
-  uint16_t KrW[kC][D + 8];      // K row-major (KK^T, QK^T), then W
-  uint16_t Qs[kC][D + 8];       // Q row-major (raw bf16)
-  uint16_t Tp[kC][kC + 8];      // T' = T diag(beta rk e^G), bf16
-  uint16_t Uh[kC][kC + 8];      // T'' = T diag(beta), hi
-  uint16_t Ul[kC][kC + 8];      //                     lo
-  uint16_t Ah[kC][kC + 8];      // A_qk hi
-  uint16_t Al[kC][kC + 8];      // A_qk lo
-  float Lf[kC][kC + 4];         // L (fp32)
-  float Tf[kC][kC + 4];         // T (fp32), lower blocks only
-  float scr[4][16][20];         // per-wave 16x16 scratch of the solve
+  uint16_t Kt[D][kC + 8];  // K^T of the chunk (raw bf16), row = key dim
+  union {
+    uint16_t Kr[kC][D + 8];  // K row-major (raw bf16): K K^T, K Q^T
+    uint16_t Vt[D][kC + 8];  // then V^T (raw bf16): U = T'' V
+  } kv;
+  float Lp[10][16][kTileLd];  // lower tiles of L (fp32)
+  float Tp[10][16][kTileLd];  // lower tiles of T = (I + L)^-1 (fp32)
+  float scr[4][16][kTileLd];  // per-wave 16x16 scratch of the solve
   float G[kC], bt[kC], rk[kC], rq[kC];
   float cW[kC], cQ[kC], cK[kC];
-  float ssk[NW][kC];
-  float ssq[kC];
+  float ssk[kC], ssq[kC];
   float eg_last;
 };
 
-// grid = 8 * ceil(nc_bound * Hv / 8); block = 64 * NW.
+// B fragment of X^T for X = T diag(c) (rows t = 16 mt + lr, contraction over
+// tokens s = 32 kc + 8 lg + j): X[t][s] = T[t][s] c[s], zero above the
+// diagonal tiles.  Read from the packed T tiles, 8 consecutive floats per lane.
+__device__ __forceinline__ void t_row8(const float (*Tp)[16][kTileLd], const float* c, int mt, int kc, int lr,
+                                       int lg, float x[8]) {
+  const int st = 2 * kc + (lg >> 1);  // s tile
+  if (st > mt) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = 0.f;
+    return;
+  }
+  const float4* row = reinterpret_cast<const float4*>(&Tp[tix(mt, st)][lr][(lg & 1) * 8]);
+  const float4* cc = reinterpret_cast<const float4*>(&c[32 * kc + 8 * lg]);
+  const float4 r0 = row[0], r1 = row[1], c0 = cc[0], c1 = cc[1];
+  x[0] = r0.x * c0.x; x[1] = r0.y * c0.y; x[2] = r0.z * c0.z; x[3] = r0.w * c0.w;
+  x[4] = r1.x * c1.x; x[5] = r1.y * c1.y; x[6] = r1.z * c1.z; x[7] = r1.w * c1.w;
+}
+
+__device__ __forceinline__ s16x8_t pack8(const float x[8]) {
+  u32x4_t h;
+  h[0] = gdn::f2bf2(x[0], x[1]);
+  h[1] = gdn::f2bf2(x[2], x[3]);
+  h[2] = gdn::f2bf2(x[4], x[5]);
+  h[3] = gdn::f2bf2(x[6], x[7]);
+  return __builtin_bit_cast(s16x8_t, h);
+}
+
+__device__ __forceinline__ void split8(const float x[8], s16x8_t& hi, s16x8_t& lo) {
+  u32x4_t h, l;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    h[p] = gdn::f2bf2(x[2 * p], x[2 * p + 1]);
+    l[p] = gdn::f2bf2(x[2 * p] - lo_half(h[p]), x[2 * p + 1] - hi_half(h[p]));
+  }
+  hi = __builtin_bit_cast(s16x8_t, h);
+  lo = __builtin_bit_cast(s16x8_t, l);
+}
+
+// grid = 8 * ceil(nc_bound * Hv / 8); block = 64 * NW.  One workgroup per
+// (chunk, value head): computes everything that does not depend on S and
+// writes the chunk's record.  Every record block is produced in registers in
+// the lane order the chain kernel reads (MFMA C fragments of transposed
+// products where needed), so LDS holds only K (both layouts, then V^T) and
+// the fp32 L / T tiles.
+// Two (D = 128) or three (D = 64) workgroups per CU fit in LDS; the second
+// launch bound caps the registers so that as many fit in the register file.
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
+__global__ __launch_bounds__(64 * NW, D == 128 ? 4 : 3) void chunk_local_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
     const uint16_t* __restrict__ v, int64_t sv, const float* __restrict__ g,
     const uint16_t* __restrict__ beta, const int64_t* __restrict__ cu, int n_seqs, int64_t nc_bound,
     int Hk, int Hv, float scale, int l2norm, uint8_t* __restrict__ ws) {
+  using R = Rec<D>;
   constexpr int NT = 64 * NW;
-  constexpr int KTD = D / 32;
-  constexpr int MTD = D / 16;
-  constexpr int LDF = kC + 4;
-  constexpr int SEG = D / 8;                 // 16-byte segments per row
+  constexpr int KTD = R::KTD;
+  constexpr int MTD = R::MTD;
+  constexpr int SEG = D / 8;               // 16-byte segments per row
+  constexpr int NSEG1 = kC * SEG / NT;     // row segments per thread
   static_assert(NW >= 4, "the solve uses four waves");
+  static_assert(kC * SEG % NT == 0 && NT % SEG == 0, "segment tiling");
   __shared__ LocalSmem<D, NW> sm;
 
   const int64_t wi = gdn::xcd_remap(blockIdx.x, nc_bound * Hv);
@@ -231,7 +280,8 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
   const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
   const uint16_t* kh_ = k + static_cast<int64_t>(kh) * D;
   const uint16_t* vh = v + static_cast<int64_t>(h) * D;
-  uint8_t* rec = ws + (cidx * Hv + h) * Rec<D>::BYTES;
+  uint8_t* rec = ws + (cidx * Hv + h) * R::BYTES;
+  s16x8_t* blk = reinterpret_cast<s16x8_t*>(rec);  // blk[b * 64 + lane]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -239,41 +289,43 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
   const int lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // ---- phase 1: stage K (both layouts) and Q, row norms, gates ----
+  // ---- phase 1: K (both layouts), row norms of K and Q, gates; V kept in
+  //      registers until K row-major is dead ----
+  s16x8_t vseg[NSEG1];
   {
-    float ss = 0.f;
-    const int row = min(lane, len - 1);
 #pragma unroll
-    for (int j = 0; j < SEG / NW; ++j) {
-      const int c8 = wave + NW * j;
-      s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + (tok0 + row) * sk + c8 * 8);
-      if (lane >= len) kv8 = zero8();
-      *reinterpret_cast<s16x8_t*>(&sm.KrW[lane][c8 * 8]) = kv8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint16_t bits = static_cast<uint16_t>(kv8[i]);
-        sm.Kt[c8 * 8 + i][lane] = bits;
-        const float f = gdn::bf2f(bits);
-        ss += f * f;
-      }
-    }
-    sm.ssk[wave][lane] = ss;
-#pragma unroll
-    for (int j = 0; j < kC * SEG / NT; ++j) {
+    for (int j = 0; j < NSEG1; ++j) {
       const int e = tid + NT * j;
       const int t = e / SEG, c8 = e % SEG;
-      s16x8_t qv8 = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, len - 1)) * sq + c8 * 8);
-      if (t >= len) qv8 = zero8();
-      *reinterpret_cast<s16x8_t*>(&sm.Qs[t][c8 * 8]) = qv8;
-      float qs = 0.f;
+      const int64_t row = tok0 + min(t, len - 1);
+      s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + row * sk + c8 * 8);
+      s16x8_t qv8 = *reinterpret_cast<const s16x8_t*>(qh + row * sq + c8 * 8);
+      s16x8_t vv8 = *reinterpret_cast<const s16x8_t*>(vh + row * sv + c8 * 8);
+      if (t >= len) {
+        kv8 = zero8();
+        qv8 = zero8();
+        vv8 = zero8();
+      }
+      vseg[j] = vv8;
+      *reinterpret_cast<s16x8_t*>(&sm.kv.Kr[t][c8 * 8]) = kv8;
+      float ks = 0.f, qs = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float f = gdn::bf2f(static_cast<uint16_t>(qv8[i]));
-        qs += f * f;
+        const uint16_t kb = static_cast<uint16_t>(kv8[i]);
+        sm.Kt[c8 * 8 + i][t] = kb;
+        const float kf = gdn::bf2f(kb), qf = gdn::bf2f(static_cast<uint16_t>(qv8[i]));
+        ks += kf * kf;
+        qs += qf * qf;
       }
 #pragma unroll
-      for (int m = SEG / 2; m >= 1; m >>= 1) qs += __shfl_xor(qs, m, 64);
-      if (c8 == 0) sm.ssq[t] = qs;
+      for (int m = SEG / 2; m >= 1; m >>= 1) {
+        ks += __shfl_xor(ks, m, 64);
+        qs += __shfl_xor(qs, m, 64);
+      }
+      if (c8 == 0) {
+        sm.ssk[t] = ks;
+        sm.ssq[t] = qs;
+      }
     }
     if (wave == 0) {
       float gv = 0.f, bv = 0.f;
@@ -291,13 +343,20 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
       sm.bt[lane] = bv;
     }
   }
+  // Q record blocks straight from global: block (mt, kt), lane pieces
+  // q[16 mt + lr][32 kt + 4 lg ..] and [.. + 16 ..] (zero past the end).
+  for (int b = wave; b < 4 * KTD; b += NW) {
+    const int mt = b / KTD, kt = b % KTD;
+    const int t = 16 * mt + lr;
+    const uint16_t* qr = qh + (tok0 + min(t, len - 1)) * sq + 32 * kt;
+    s16x8_t f = perm_frag(qr, lg);
+    if (t >= len) f = zero8();
+    blk[(R::Q + b) * 64 + lane] = f;
+  }
   __syncthreads();
   if (tid < kC) {
     const int t = tid;
-    float ssk = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) ssk += sm.ssk[w][t];
-    const float rk = l2norm ? rsqrtf(ssk + 1e-6f) : 1.0f;
+    const float rk = l2norm ? rsqrtf(sm.ssk[t] + 1e-6f) : 1.0f;
     const float rq = l2norm ? rsqrtf(sm.ssq[t] + 1e-6f) : 1.0f;
     const float Gt = sm.G[t];
     const float Gl = sm.G[kC - 1];
@@ -307,18 +366,27 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
     sm.cQ[t] = rq * scale * expf(Gt);
     sm.cK[t] = rk * expf(Gl - Gt);
     if (t == 0) sm.eg_last = expf(Gl);
+    float* vrec = reinterpret_cast<float*>(rec + R::VEC * 1024);
+    vrec[t] = sm.cQ[t];
+    vrec[kC + t] = sm.cK[t];
+    if (t == 0) vrec[2 * kC] = sm.eg_last;
+  }
+  // K^T record blocks: key rows 16 mt.., tokens 32 kt.. (permuted order)
+  for (int b = wave; b < 2 * MTD; b += NW) {
+    const int mt = b >> 1, kt = b & 1;
+    blk[(R::K + b) * 64 + lane] = perm_frag(&sm.Kt[16 * mt + lr][32 * kt], lg);
   }
   __syncthreads();
 
-  // ---- phase 2a: K K^T -> L (fp32), lower-triangular tiles ----
+  // ---- phase 2a: K K^T -> L (fp32 lower tiles) ----
   for (int j = wave; j < 10; j += NW) {
     int mt, nt;
     tri_tile(j, mt, nt);
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kt = 0; kt < KTD; ++kt) {
-      const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * mt + lr][32 * kt + 8 * lg]);
-      const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
+    for (int kk = 0; kk < KTD; ++kk) {
+      const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.kv.Kr[16 * mt + lr][32 * kk + 8 * lg]);
+      const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.kv.Kr[16 * nt + lr][32 * kk + 8 * lg]);
       acc = gdn::mfma16x16x32(a8, b8, acc);
     }
     const int s = 16 * nt + lr;
@@ -327,19 +395,20 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * mt + 4 * lg + i;
-      sm.Lf[t][s] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * expf(sm.G[t] - Gs) : 0.f;
+      sm.Lp[j][4 * lg + i][lr] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * expf(sm.G[t] - Gs) : 0.f;
     }
   }
   __syncthreads();
 
-  // ---- phase 2b / solve step 1: wave 0 inverts the diagonal blocks while
-  //      the other waves form A_qk = lower(Q K^T) (hi/lo) ----
+  // ---- phase 2b: wave 0 inverts the diagonal blocks; the other waves form
+  //      the A_qk record blocks as C fragments of (K Q^T) tile pairs ----
   if (wave == 0) {
-    const int bb = lane >> 4, c = lane & 15, base = 16 * bb;
+    const int bb = lane >> 4, c = lane & 15;
+    const int dt = tix(bb, bb);
     float x[16];
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
-      const float4* lrow = reinterpret_cast<const float4*>(&sm.Lf[base + rr][base]);
+      const float4* lrow = reinterpret_cast<const float4*>(&sm.Lp[dt][rr][0]);
       float lv[16];
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
@@ -352,190 +421,154 @@ __global__ __launch_bounds__(64 * NW) void chunk_local_kernel(
       x[rr] = acc;
     }
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) sm.Tf[base + rr][base + c] = x[rr];
+    for (int rr = 0; rr < 16; ++rr) sm.Tp[dt][rr][c] = x[rr];
   } else {
-    for (int j = wave - 1; j < 10; j += NW - 1) {
-      int mt, nt;
-      tri_tile(j, mt, nt);
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int b = wave - 1; b < 6; b += NW - 1) {
+      const int mt = b < 2 ? b : 2 + ((b - 2) >> 1);
+      const int kt = b < 2 ? 0 : ((b - 2) & 1);
+      const int t = 16 * mt + lr;  // the lane's query token (C column)
+      // B operand: q row t, key dims 32 kk + 8 lg .. (raw bf16)
+      const uint16_t* qr = qh + (tok0 + min(t, len - 1)) * sq + 8 * lg;
+      s16x8_t qb[KTD];
 #pragma unroll
-      for (int kt = 0; kt < KTD; ++kt) {
-        const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Qs[16 * mt + lr][32 * kt + 8 * lg]);
-        const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.KrW[16 * nt + lr][32 * kt + 8 * lg]);
-        acc = gdn::mfma16x16x32(a8, b8, acc);
-      }
-      const int s = 16 * nt + lr;
-      const float rks = sm.rk[s] * scale;
-      const float Gs = sm.G[s];
+      for (int kk = 0; kk < KTD; ++kk) qb[kk] = *reinterpret_cast<const s16x8_t*>(qr + 32 * kk);
+      const float qscale = sm.rq[t] * scale;
+      const float Gt = sm.G[t];
+      float a[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * mt + 4 * lg + i;
-        const float a = s <= t ? acc[i] * sm.rq[t] * rks * expf(sm.G[t] - Gs) : 0.f;
-        uint16_t hi, lo;
-        gdn::split_bf16(a, hi, lo);
-        sm.Ah[t][s] = hi;
-        sm.Al[t][s] = lo;
+      for (int half = 0; half < 2; ++half) {
+        const int ns = 2 * kt + half;  // key-token tile
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        if (ns <= mt) {
+#pragma unroll
+          for (int kk = 0; kk < KTD; ++kk) {
+            const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.kv.Kr[16 * ns + lr][32 * kk + 8 * lg]);
+            acc = gdn::mfma16x16x32(a8, qb[kk], acc);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int s = 16 * ns + 4 * lg + i;
+          a[4 * half + i] = s <= t ? acc[i] * qscale * sm.rk[s] * expf(Gt - sm.G[s]) : 0.f;
+        }
       }
+      s16x8_t ahi, alo;
+      split8(a, ahi, alo);
+      blk[(R::AH + b) * 64 + lane] = ahi;
+      blk[(R::AL + b) * 64 + lane] = alo;
     }
   }
   __syncthreads();
+  // K row-major is dead: V^T takes its place (read in phase 5, after three
+  // more barriers)
+#pragma unroll
+  for (int j = 0; j < NSEG1; ++j) {
+    const int e = tid + NT * j;
+    const int t = e / SEG, c8 = e % SEG;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sm.kv.Vt[c8 * 8 + i][t] = static_cast<uint16_t>(vseg[j][i]);
+  }
   // first sub-diagonal: T(j+1, j) = -T(j+1,j+1) L(j+1,j) T(j,j)
   if (wave < 3) {
     const int j = wave, i = j + 1;
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lf[16 * i][16 * j], LDF, &sm.Tf[16 * j][16 * j], LDF, lane);
-    st16_f32(&sm.scr[wave][0][0], 20, p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(i, j)][0][0], kTileLd, &sm.Tp[tix(j, j)][0][0], kTileLd, lane);
+    st16_f32(&sm.scr[wave][0][0], kTileLd, p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tf[16 * i][16 * i], LDF, &sm.scr[wave][0][0], 20, lane);
-    st16_f32(&sm.Tf[16 * i][16 * j], LDF, t2, -1.f, lane);
+    t2 = mm16_f32(t2, &sm.Tp[tix(i, i)][0][0], kTileLd, &sm.scr[wave][0][0], kTileLd, lane);
+    st16_f32(&sm.Tp[tix(i, j)][0][0], kTileLd, t2, -1.f, lane);
   } else if (wave == 3) {
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lf[48][0], LDF, &sm.Tf[0][0], LDF, lane);  // L30 T00
-    st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 0)][0][0], kTileLd, &sm.Tp[tix(0, 0)][0][0], kTileLd, lane);  // L30 T00
+    st16_f32(&sm.scr[3][0][0], kTileLd, p, 1.f, lane);
   }
   __syncthreads();
   // second sub-diagonal: T20, T31; partial sum for T30
   if (wave == 0) {
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lf[32][0], LDF, &sm.Tf[0][0], LDF, lane);    // L20 T00
-    p = mm16_f32(p, &sm.Lf[32][16], LDF, &sm.Tf[16][0], LDF, lane);  // L21 T10
-    st16_f32(&sm.scr[0][0][0], 20, p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(2, 0)][0][0], kTileLd, &sm.Tp[tix(0, 0)][0][0], kTileLd, lane);  // L20 T00
+    p = mm16_f32(p, &sm.Lp[tix(2, 1)][0][0], kTileLd, &sm.Tp[tix(1, 0)][0][0], kTileLd, lane);  // L21 T10
+    st16_f32(&sm.scr[0][0][0], kTileLd, p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tf[32][32], LDF, &sm.scr[0][0][0], 20, lane);
-    st16_f32(&sm.Tf[32][0], LDF, t2, -1.f, lane);
+    t2 = mm16_f32(t2, &sm.Tp[tix(2, 2)][0][0], kTileLd, &sm.scr[0][0][0], kTileLd, lane);
+    st16_f32(&sm.Tp[tix(2, 0)][0][0], kTileLd, t2, -1.f, lane);
   } else if (wave == 1) {
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lf[48][16], LDF, &sm.Tf[16][16], LDF, lane);  // L31 T11
-    p = mm16_f32(p, &sm.Lf[48][32], LDF, &sm.Tf[32][16], LDF, lane);  // L32 T21
-    st16_f32(&sm.scr[1][0][0], 20, p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 1)][0][0], kTileLd, &sm.Tp[tix(1, 1)][0][0], kTileLd, lane);  // L31 T11
+    p = mm16_f32(p, &sm.Lp[tix(3, 2)][0][0], kTileLd, &sm.Tp[tix(2, 1)][0][0], kTileLd, lane);  // L32 T21
+    st16_f32(&sm.scr[1][0][0], kTileLd, p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tf[48][48], LDF, &sm.scr[1][0][0], 20, lane);
-    st16_f32(&sm.Tf[48][16], LDF, t2, -1.f, lane);
+    t2 = mm16_f32(t2, &sm.Tp[tix(3, 3)][0][0], kTileLd, &sm.scr[1][0][0], kTileLd, lane);
+    st16_f32(&sm.Tp[tix(3, 1)][0][0], kTileLd, t2, -1.f, lane);
   } else if (wave == 3) {
-    f32x4_t p = ld16_f32(&sm.scr[3][0][0], 20, lane);
-    p = mm16_f32(p, &sm.Lf[48][16], LDF, &sm.Tf[16][0], LDF, lane);  // + L31 T10
-    st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
+    f32x4_t p = ld16_f32(&sm.scr[3][0][0], kTileLd, lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 1)][0][0], kTileLd, &sm.Tp[tix(1, 0)][0][0], kTileLd, lane);  // + L31 T10
+    st16_f32(&sm.scr[3][0][0], kTileLd, p, 1.f, lane);
   }
   __syncthreads();
   // third sub-diagonal: T30
   if (wave == 3) {
-    f32x4_t p = ld16_f32(&sm.scr[3][0][0], 20, lane);
-    p = mm16_f32(p, &sm.Lf[48][32], LDF, &sm.Tf[32][0], LDF, lane);  // + L32 T20
-    st16_f32(&sm.scr[3][0][0], 20, p, 1.f, lane);
+    f32x4_t p = ld16_f32(&sm.scr[3][0][0], kTileLd, lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 2)][0][0], kTileLd, &sm.Tp[tix(2, 0)][0][0], kTileLd, lane);  // + L32 T20
+    st16_f32(&sm.scr[3][0][0], kTileLd, p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tf[48][48], LDF, &sm.scr[3][0][0], 20, lane);
-    st16_f32(&sm.Tf[48][0], LDF, t2, -1.f, lane);
+    t2 = mm16_f32(t2, &sm.Tp[tix(3, 3)][0][0], kTileLd, &sm.scr[3][0][0], kTileLd, lane);
+    st16_f32(&sm.Tp[tix(3, 0)][0][0], kTileLd, t2, -1.f, lane);
   }
   __syncthreads();
 
-  // ---- phase 4: T' (bf16) and T'' (hi/lo), 4 columns per thread; zero the
-  //      upper tiles of A_qk ----
-  for (int e4 = tid; e4 < kC * (kC / 4); e4 += NT) {
-    const int t = e4 >> 4, s0 = (e4 & 15) * 4;
-    const bool lower = (s0 >> 4) <= (t >> 4);
-    float4 tv = lower ? *reinterpret_cast<const float4*>(&sm.Tf[t][s0]) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float4 cw = *reinterpret_cast<const float4*>(&sm.cW[s0]);
-    const float4 cb = *reinterpret_cast<const float4*>(&sm.bt[s0]);
-    uint2 tp;
-    tp.x = gdn::f2bf2(tv.x * cw.x, tv.y * cw.y);
-    tp.y = gdn::f2bf2(tv.z * cw.z, tv.w * cw.w);
-    *reinterpret_cast<uint2*>(&sm.Tp[t][s0]) = tp;
-    const float u0 = tv.x * cb.x, u1 = tv.y * cb.y, u2 = tv.z * cb.z, u3 = tv.w * cb.w;
-    uint2 uh, ul;
-    uh.x = gdn::f2bf2(u0, u1);
-    uh.y = gdn::f2bf2(u2, u3);
-    ul.x = gdn::f2bf2(u0 - lo_half(uh.x), u1 - hi_half(uh.x));
-    ul.y = gdn::f2bf2(u2 - lo_half(uh.y), u3 - hi_half(uh.y));
-    *reinterpret_cast<uint2*>(&sm.Uh[t][s0]) = uh;
-    *reinterpret_cast<uint2*>(&sm.Ul[t][s0]) = ul;
-    if (!lower) {
-      *reinterpret_cast<uint2*>(&sm.Ah[t][s0]) = make_uint2(0u, 0u);
-      *reinterpret_cast<uint2*>(&sm.Al[t][s0]) = make_uint2(0u, 0u);
-    }
-  }
-  __syncthreads();
-
-  // ---- phase 5: W = T' K (-> LDS, overwrites K row-major) and
-  //      U = T'' V (C fragments straight to the record) ----
-  {
-    constexpr int NJ = (4 * MTD + NW - 1) / NW;
+  // ---- phase 5: W blocks as C fragments of W^T = K^T (T diag(cW))^T tile
+  //      pairs, U = (T diag(beta)) V as C fragments (T'' split hi/lo) ----
+  for (int b = wave; b < 4 * KTD; b += NW) {
+    const int mt = b / KTD, kt = b % KTD;
+    s16x8_t tb[2];
 #pragma unroll
-    for (int jj = 0; jj < NJ; ++jj) {
-      const int j = wave + NW * jj;
-      if (j >= 4 * MTD) break;
-      const int mt = j % 4, nt = j / 4;
+    for (int kc = 0; kc < 2; ++kc) {
+      float x[8];
+      t_row8(sm.Tp, sm.cW, mt, kc, lr, lg, x);
+      tb[kc] = pack8(x);
+    }
+    float w8[8];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int nk = 2 * kt + half;  // key tile
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Tp[16 * mt + lr][32 * kt + 8 * lg]);
-        const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.Kt[16 * nt + lr][32 * kt + 8 * lg]);
-        acc = gdn::mfma16x16x32(a8, b8, acc);
+      for (int kc = 0; kc < 2; ++kc) {
+        const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Kt[16 * nk + lr][32 * kc + 8 * lg]);
+        acc = gdn::mfma16x16x32(a8, tb[kc], acc);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sm.KrW[16 * mt + 4 * lg + i][16 * nt + lr] = gdn::f2bf(acc[i]);
+      for (int i = 0; i < 4; ++i) w8[4 * half + i] = acc[i];
     }
-    // U tiles: column tile nt (16 value columns) x 4 row tiles; record layout
-    // [nt][mt][lane] float4, i.e. exactly the C fragments the chain kernel holds
-    float4* urec = reinterpret_cast<float4*>(rec + Rec<D>::U * 1024);
+    blk[(R::W + b) * 64 + lane] = pack8(w8);
+  }
+  {
+    f32x4_t* urec = reinterpret_cast<f32x4_t*>(rec + R::U * 1024);
     for (int nt = wave; nt < MTD; nt += NW) {
-      s16x8_t vf[2];
-      const int col = 16 * nt + lr;
+      s16x8_t vb[2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int s = 32 * kt + 8 * lg + i;
-          const short x = static_cast<short>(vh[(tok0 + min(s, len - 1)) * sv + col]);
-          vf[kt][i] = s < len ? x : static_cast<short>(0);
-        }
+      for (int kc = 0; kc < 2; ++kc) vb[kc] = *reinterpret_cast<const s16x8_t*>(&sm.kv.Vt[16 * nt + lr][32 * kc + 8 * lg]);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         f32x4_t u = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const s16x8_t ah = *reinterpret_cast<const s16x8_t*>(&sm.Uh[16 * mt + lr][32 * kt + 8 * lg]);
-          const s16x8_t al = *reinterpret_cast<const s16x8_t*>(&sm.Ul[16 * mt + lr][32 * kt + 8 * lg]);
-          u = gdn::mfma16x16x32(ah, vf[kt], u);
-          u = gdn::mfma16x16x32(al, vf[kt], u);
+        for (int kc = 0; kc < 2; ++kc) {
+          if (2 * kc > mt) break;  // T'' is zero above the diagonal tiles
+          float x[8];
+          t_row8(sm.Tp, sm.bt, mt, kc, lr, lg, x);
+          s16x8_t ah, al;
+          split8(x, ah, al);
+          u = gdn::mfma16x16x32(ah, vb[kc], u);
+          u = gdn::mfma16x16x32(al, vb[kc], u);
         }
-        urec[(nt * 4 + mt) * 64 + lane] = make_float4(u[0], u[1], u[2], u[3]);
+        urec[(nt * 4 + mt) * 64 + lane] = u;
       }
     }
-  }
-  __syncthreads();
-
-  // ---- record: operand blocks in lane order (see Rec) ----
-  {
-    s16x8_t* blk = reinterpret_cast<s16x8_t*>(rec);
-    for (int e = tid; e < Rec<D>::VEC * 64; e += NT) {
-      const int b = e >> 6, l = e & 63, flr = l & 15, flg = l >> 4;
-      const uint16_t* row;
-      if (b < Rec<D>::Q) {
-        const int mt = b / KTD, kt = b % KTD;
-        row = &sm.KrW[16 * mt + flr][32 * kt];
-      } else if (b < Rec<D>::K) {
-        const int x = b - Rec<D>::Q, mt = x / KTD, kt = x % KTD;
-        row = &sm.Qs[16 * mt + flr][32 * kt];
-      } else if (b < Rec<D>::AH) {
-        const int x = b - Rec<D>::K, mt = x >> 1, kt = x & 1;
-        row = &sm.Kt[16 * mt + flr][32 * kt];
-      } else {
-        const int x = b < Rec<D>::AL ? b - Rec<D>::AH : b - Rec<D>::AL;
-        const int mt = x < 2 ? x : 2 + ((x - 2) >> 1), kt = x < 2 ? 0 : ((x - 2) & 1);
-        row = b < Rec<D>::AL ? &sm.Ah[16 * mt + flr][32 * kt] : &sm.Al[16 * mt + flr][32 * kt];
-      }
-      blk[e] = perm_frag(row, flg);
-    }
-    float* vrec = reinterpret_cast<float*>(rec + Rec<D>::VEC * 1024);
-    if (tid < kC) {
-      vrec[tid] = sm.cQ[tid];
-      vrec[kC + tid] = sm.cK[tid];
-    }
-    if (tid == 0) vrec[2 * kC] = sm.eg_last;
   }
 }
 
@@ -801,9 +834,10 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
   if (n_seqs < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
   if (n_seqs == 0) return GDN_OK;
   if (!q || !k || !v || !g || !beta || !cu_seqlens || !o || !workspace) return GDN_ERR_INVALID_ARG;
-  // 16-byte row fragments of q / k, 8-byte output pieces, 256-byte workspace records
-  if (sq_tok % 8 || sk_tok % 8 || reinterpret_cast<uintptr_t>(q) % 16 ||
-      reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(o) % 8 ||
+  // 16-byte row fragments of q / k / v, 8-byte output pieces, 256-byte workspace records
+  if (sq_tok % 8 || sk_tok % 8 || sv_tok % 8 || reinterpret_cast<uintptr_t>(q) % 16 ||
+      reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(v) % 16 ||
+      reinterpret_cast<uintptr_t>(o) % 8 ||
       reinterpret_cast<uintptr_t>(workspace) % 256 ||
       ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
     return GDN_ERR_INVALID_ARG;

@@ -170,6 +170,12 @@ def _state_view_ok(s: torch.Tensor, H: int, D: int) -> bool:
             and s.stride(1) == D * D and s.stride(2) == D and s.stride(3) == 1)
 
 
+def _rows16(t: torch.Tensor, D: int) -> torch.Tensor:
+    if t.stride(2) != 1 or t.stride(1) != D or t.stride(0) % 8 or t.data_ptr() % 16:
+        return t.contiguous() if not t.is_contiguous() else t.clone()
+    return t
+
+
 def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
                                   beta: torch.Tensor, cu_seqlens: torch.Tensor,
                                   initial_state: torch.Tensor | None = None, *,
@@ -193,8 +199,9 @@ def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     N, Hk, D = k.shape
     Hv = v.shape[1]
     assert q.shape == k.shape and v.shape[0] == N and v.shape[2] == D and Hv % Hk == 0
-    assert q.stride(2) == 1 and k.stride(2) == 1 and v.stride(2) == 1
-    assert q.stride(1) == D and k.stride(1) == D and v.stride(1) == D
+    # the kernels read 16-byte row pieces: head-contiguous rows, 16-byte
+    # aligned, token stride a multiple of 8 elements (else copy once)
+    q, k, v = (_rows16(t, D) for t in (q, k, v))
     g = g.float().contiguous() if g.dtype != torch.float32 else g.contiguous()
     beta = beta.contiguous()
     assert g.shape == (N, Hv) and beta.shape == (N, Hv)
