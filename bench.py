@@ -115,6 +115,21 @@ def make_spec(seed=3, B=64, T=4, slots=128, Hk=16, Hv=32, D=128):
                 dt_bias=dt_bias, accepted=accepted)
 
 
+def _profiled_traffic(name: str):
+    """HBM bytes per launch of a kernel, as measured by the rocprofv3 PMC runs
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's counters) recorded in
+    profiles/<name>_traffic.md on a line `traffic_bytes_per_launch: <int>`;
+    None when no such measurement is committed."""
+    import re
+
+    f = ROOT / "profiles" / f"{name}_traffic.md"
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", f.read_text())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 # ------------------------------------------------------------------ timing --
 class EventTimer:
     """HIP events around named kernels on torch's current stream (the stream
@@ -271,6 +286,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--configs", default="1,2,3,4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB K times (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GDN path shards by value head / by sequence with no "
@@ -280,6 +298,15 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        nbytes = args.copy_calibration << 20
+        src = torch.ones(nbytes // 4, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": nbytes, "bytes_written": nbytes, "launches": args.steps}))
+        return
     import __graft_entry__ as ge
 
     pkg = ge.load_package()
@@ -296,8 +323,10 @@ def main():
     flops = chunk_flops(N1, cfg1["Hv"], cfg1["D"])
     achieved = flops / (chunk_us * 1e-6) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                "kernel": "chunk_prefill_kernel<128,8>", "kernel_us": round(chunk_us, 2),
+                "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                "traffic": _profiled_traffic("chunk_prefill_config1"),
+                "kernel": "chunk prefill = chunk_local_kernel<128,8> + chunk_chain_kernel<128,4> "
+                          "(one launch pair per call)", "kernel_us": round(chunk_us, 2),
                 "algorithmic_flop_per_launch": flops}
     kernels1 = {k: round(v, 2) for k, v in k1.items()}
 
@@ -311,7 +340,8 @@ def main():
             "ms_per_step": round(t2 * 1e3, 4), "ms_per_step_graph": round(t2g * 1e3, 4),
             "kernels_us": {k: round(v, 2) for k, v in k2.items()},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                         "traffic": _profiled_traffic("recurrent_decode_config2"),
                          "kernel": "recurrent_kernel<128,1>", "algorithmic_bytes_per_launch": state_bytes}}
         del c2
     if 3 in configs:
