@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import bench
-from helpers import BF16, assert_out, assert_state, state_rel
+from helpers import BF16, STATE_REL, assert_out, assert_state, state_rel
 from oracle import gdn_ref
 
 pytestmark = pytest.mark.gpu
@@ -150,7 +150,8 @@ def test_chunked_prefill_equals_one_shot_and_batched_equals_solo(pkg, dev):
     o_b = core.prefill_varlen(mixed[100:300], z[100:300], b[100:300], a[100:300], [200], ids[:1], cp3, sp3)
     assert_out(torch.cat([o_a, o_b]).cpu(), out1[:300].cpu(), "chunked == one-shot", ulps=4)
     assert torch.equal(cp3[2], cp1[2])
-    assert state_rel(sp3[2].cpu(), sp1[2].cpu()) < 1e-4
+    # both sides carry the chunk kernel's fp16-operand error (~2e-4 each)
+    assert state_rel(sp3[2].cpu(), sp1[2].cpu()) < STATE_REL
 
 
 def test_prefill_then_decode_equals_longer_prefill(pkg, dev):
@@ -170,7 +171,8 @@ def test_prefill_then_decode_equals_longer_prefill(pkg, dev):
     o_all = core.prefill_varlen(mixed, z, b, a, [T + 1], ids, cp2, sp2)
     assert_out(o_dec.cpu(), o_all[T:].cpu(), "decode after prefill", ulps=4)
     assert torch.equal(cp, cp2)
-    assert state_rel(sp[1].cpu(), sp2[1].cpu()) < 1e-4
+    # both sides carry the chunk kernel's fp16-operand error (~2e-4 each)
+    assert state_rel(sp[1].cpu(), sp2[1].cpu()) < STATE_REL
 
 
 # --------------------------------------------------------- BASELINE configs --
