@@ -270,6 +270,20 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
+  // Waves 1..3 form the A blocks b = wave - 1 and wave + 2 later on; their q
+  // rows (B operands) are loaded now so the loads overlap the whole first half.
+  s16x8_t qpre[2][KTD];
+  if (wave > 0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int b = wave - 1 + 3 * u;
+      const int mt = b < 2 ? b : 2 + ((b - 2) >> 1);
+      const uint16_t* qr = qh + (tok0 + min(16 * mt + lr, len - 1)) * sq + 8 * lg;
+#pragma unroll
+      for (int kk = 0; kk < KTD; ++kk) qpre[u][kk] = *reinterpret_cast<const s16x8_t*>(qr + 32 * kk);
+    }
+  }
+
   // ---- phase 1: K rows, row norms of K and Q, gates ----
 #pragma unroll
   for (int j = 0; j < NSEG1; ++j) {
@@ -351,7 +365,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * mt + 4 * lg + i;
-      sm.Lp[j][4 * lg + i][lr] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * expf(sm.G[t] - Gs) : 0.f;
+      sm.Lp[j][4 * lg + i][lr] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * __expf(sm.G[t] - Gs) : 0.f;
     }
   }
   __syncthreads();
@@ -381,14 +395,14 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   } else {
     // blocks (mt, kt): query rows 16 mt.., key tokens 32 kt.. with 32 kt <= 16 mt + 15
     uint16_t* arec = reinterpret_cast<uint16_t*>(rec + Rec::AQ);
-    for (int b = wave - 1; b < 6; b += NW - 1) {
+    static_assert(NW == 4, "waves 1..3 take two A blocks each");
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int b = wave - 1 + 3 * u;
       const int mt = b < 2 ? b : 2 + ((b - 2) >> 1);
       const int kt = b < 2 ? 0 : ((b - 2) & 1);
       const int t = 16 * mt + lr;  // the lane's query token (C column)
-      const uint16_t* qr = qh + (tok0 + min(t, len - 1)) * sq + 8 * lg;
-      s16x8_t qb[KTD];
-#pragma unroll
-      for (int kk = 0; kk < KTD; ++kk) qb[kk] = *reinterpret_cast<const s16x8_t*>(qr + 32 * kk);
+      const s16x8_t* qb = qpre[u];
       const float qscale = sm.rq[t] * scale;
       const float Gt = sm.G[t];
 #pragma unroll
@@ -406,7 +420,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int s = 16 * ns + 4 * lg + i;
-          a[i] = (s <= t && t < len) ? acc[i] * qscale * sm.rk[s] * expf(Gt - sm.G[s]) : 0.f;
+          a[i] = (s <= t && t < len) ? acc[i] * qscale * sm.rk[s] * __expf(Gt - sm.G[s]) : 0.f;
         }
         // tokens 16 ns + 4 lg .. + 3 sit at the positions of quad qswap
         const int pos = qswap(16 * ns + 4 * lg);
