@@ -325,7 +325,7 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                 "traffic": _profiled_traffic("chunk_prefill_config1"),
-                "kernel": "chunk prefill = chunk_local_kernel<128,8> + chunk_chain_kernel<128,4> "
+                "kernel": "chunk prefill = chunk_prep_kernel<128> + chunk_state_kernel<128> "
                           "(one launch pair per call)", "kernel_us": round(chunk_us, 2),
                 "algorithmic_flop_per_launch": flops}
     kernels1 = {k: round(v, 2) for k, v in k1.items()}
@@ -380,7 +380,8 @@ def main():
                                "chunked gated delta rule + gated RMSNorm), 8 seqs lens~U[128,4096] seed 1",
                    "tokens": N1, "lens": cfg1["lens"], "Hk": 16, "Hv": 16, "head_dim": 128, "chunk": 64,
                    "conv_channels": cfg1["C"], "state": "fp32, slot pool updated in place",
-                   "precision": "bf16 in/out, fp32 state and accumulation, split-bf16 MFMA for fp32-accurate products",
+                   "precision": "bf16 in/out; fp16 matrix-core operands with fp32 accumulation; fp32 state and "
+                                "triangular solve",
                    "parallelism": "single GPU"},
         "kernels_us": kernels1,
         "roofline": roofline,
