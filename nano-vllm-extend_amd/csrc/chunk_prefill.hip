@@ -60,6 +60,7 @@ typedef _Float16 h16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kC = 64;   // chunk size (tokens)
 constexpr int kCB = 64;  // value columns per state workgroup
@@ -106,10 +107,6 @@ __device__ __forceinline__ f32x16_t zero16() {
   return z;
 }
 
-__device__ __forceinline__ h16x8_t ld_h8(const uint16_t* base, int off) {
-  return *reinterpret_cast<const h16x8_t*>(base + off);
-}
-
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -117,26 +114,39 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // ---- record of one (chunk, value head), byte offsets ----
-// T' = T diag(beta e^G / ||k||), T'' = T diag(beta) and A are zero above the
-// diagonal 32x32 blocks; each is stored as its three nonzero 32x32 blocks
-// (0,0), (1,0), (1,1) (block index = row block + column block), fp16, 32-wide
-// rows with swizzled granules (swz<32>), columns in position order (position
-// p holds token qswap(p)).
-//   TW  [3][32][32] fp16   T'
-//   TB  [3][32][32] fp16   T''
-//   AQ  [3][32][32] fp16   A
-//   VEC fp32 [256]         cQ[64] = scale e^{G_t} / ||q_t||,
-//                          cK[64] = e^{gamma - G_t} / ||k_t|| (0 past the sequence end),
-//                          e^gamma
-// The tiles are stored exactly as the state kernel's LDS holds them, so it
-// copies them linearly.
+// Every operand tile is stored in matrix-core fragment order: a fragment is
+// 64 lanes x 16 bytes (8 fp16), lane = row % 32 + 32 * (8-column half of its
+// 16-column k-step), so a wave moves one fragment as one contiguous KiB.
+// Token columns are in position order (position p holds token qswap(p)).
+//   TW  [6] frags      -T' = -T diag(beta e^G / ||k||), block-lower-triangular
+//                      64x64: fragment j = (row tile 0, k-steps 0..1),
+//                      (row tile 1, k-steps 0..3)
+//   TB  [6] frags      T'' = T diag(beta), same order
+//   AQ  [6] frags      A = lower_incl(scale q^.k^ e^{G_t - G_s}), same order
+//   VEC fp32 [256]     cQ[64] = scale e^{G_t} / ||q_t||,
+//                      cK[64] = e^{gamma - G_t} / ||k_t|| (0 past the sequence end),
+//                      e^gamma
+//   QP  [2][D/16]      Q' = diag(cQ) q: [token tile][key step]
 struct Rec {
   static constexpr int TW = 0;
   static constexpr int TB = 6144;
   static constexpr int AQ = 12288;
   static constexpr int VEC = 18432;
-  static constexpr int BYTES = 19456;
+  static constexpr int QP = 19456;
 };
+// bytes of one record (a multiple of 256)
+__host__ __device__ constexpr int64_t rec_bytes(int D) { return Rec::QP + 128LL * D; }
+
+// byte offset of fragment f, lane l
+__device__ __forceinline__ int frag_byte(int f, int l) { return (f * 64 + l) * 16; }
+
+// byte offset of element (row, col) of a block-lower-triangular 64x64 record
+// tile (col / 32 <= row / 32)
+__device__ __forceinline__ int tri_frag_byte(int row, int col) {
+  const int ks = col >> 4;
+  const int j = (row >> 5) == 0 ? ks : 2 + ks;
+  return frag_byte(j, (row & 31) + 32 * ((col >> 3) & 1)) + 2 * (col & 7);
+}
 
 // element offset of (row, col) of a 64x64 block-lower-triangular tile stored
 // as its three nonzero 32x32 blocks (col / 32 <= row / 32)
@@ -181,6 +191,23 @@ __device__ bool locate_chunk(const int64_t* __restrict__ cu, int n_seqs, int64_t
   return s_seq >= 0;
 }
 
+// Identity fragment (bf16 B operand) of k-step h of a 32-wide column tile:
+// lane (n, g) has a 1 at slot e iff 16 h + 8 g + e == col(n), with col(n) = n
+// (natural) or qswap(n) (so output column n receives input column qswap(n)).
+__device__ __forceinline__ s16x8_t ident_frag(int h, int coln, int g) {
+  s16x8_t f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = (16 * h + 8 * g + e == coln) ? static_cast<short>(0x3f80) : static_cast<short>(0);
+  return f;
+}
+
+__device__ __forceinline__ f32x16_t mfma32_bf16(const s16x8_t& a, const s16x8_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gdn::bf16x8_t, a),
+                                                 __builtin_bit_cast(gdn::bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h16x8_t as_h8(const s16x8_t& x) { return __builtin_bit_cast(h16x8_t, x); }
+
 // ============================================================= prep kernel ==
 // acc += A(16x16) B(16x16), fp32 operands in LDS, fp32 matrix cores.
 __device__ __forceinline__ f32x4_t mm16_f32(f32x4_t acc, const float* A, int lda, const float* B, int ldb, int lane) {
@@ -220,7 +247,7 @@ struct __align__(16) PrepSmem {
   float Lp[10][16][kTileLd];      // lower tiles of L
   float Tp[10][16][kTileLd];      // lower tiles of T = (I + L)^-1
   float scr[4][16][kTileLd];      // per-wave scratch of the solve
-  float G[kC], bt[kC], rk[kC], rq[kC], ssk[kC], ssq[kC], cw[kC];
+  float G[kC], bt[kC], rk[kC], rq[kC], ssk[kC], ssq[kC], cw[kC], cq[kC];
 };
 
 // Row t, token quad Q (tokens 4Q..4Q+3) of T, times c[s]: 4 floats.
@@ -262,7 +289,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int kh = h / (Hv / Hk);
   const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
   const uint16_t* kh_ = k + static_cast<int64_t>(kh) * D;
-  uint8_t* rec = ws + (cidx * Hv + h) * Rec::BYTES;
+  uint8_t* rec = ws + (cidx * Hv + h) * rec_bytes(D);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -285,6 +312,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   }
 
   // ---- phase 1: K rows, row norms of K and Q, gates ----
+  s16x8_t qraw[NSEG1];  // this thread's q segments, scaled into Q' once cQ is known
 #pragma unroll
   for (int j = 0; j < NSEG1; ++j) {
     const int e = tid + NT * j;
@@ -296,6 +324,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
       kv8 = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
       qv8 = kv8;
     }
+    qraw[j] = qv8;
     *reinterpret_cast<s16x8_t*>(&sm.Kr[t][c8 * 8]) = kv8;
     float ks = 0.f, qs = 0.f;
 #pragma unroll
@@ -340,13 +369,33 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     const float Gl = sm.G[kC - 1];
     sm.rk[t] = rk;
     sm.rq[t] = rq;
-    sm.cw[t] = sm.bt[t] * rk * expf(Gt);
+    sm.cw[t] = -(sm.bt[t] * rk * expf(Gt));  // -T' is what the record holds
+    const float cqv = rq * scale * expf(Gt);
+    sm.cq[t] = cqv;
     float* vec = reinterpret_cast<float*>(rec + Rec::VEC);
-    vec[t] = rq * scale * expf(Gt);
+    vec[t] = cqv;
     vec[kC + t] = rk * expf(Gl - Gt);
     if (t == 0) vec[2 * kC] = expf(Gl);
   }
   __syncthreads();
+
+  // ---- Q' = diag(cQ) q as fp16, in B-fragment order ----
+  {
+    uint8_t* qrec = rec + Rec::QP;
+#pragma unroll
+    for (int j = 0; j < NSEG1; ++j) {
+      const int e = tid + NT * j;
+      const int t = e / SEG, c8 = e % SEG;
+      const float cqv = sm.cq[t];
+      const u32x4_t x = __builtin_bit_cast(u32x4_t, qraw[j]);
+      u32x4_t y;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = f2h2(lo_half(x[i]) * cqv, hi_half(x[i]) * cqv);
+      const int frag = (t >> 5) * (D / 16) + (c8 >> 1);
+      const int ln = (t & 31) + 32 * (c8 & 1);
+      *reinterpret_cast<u32x4_t*>(qrec + (frag * 64 + ln) * 16) = y;
+    }
+  }
 
   // ---- phase 2a: K K^T -> L (fp32 lower tiles) ----
   for (int j = wave; j < 10; j += NW) {
@@ -394,7 +443,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     for (int rr = 0; rr < 16; ++rr) sm.Tp[dt][rr][c] = x[rr];
   } else {
     // blocks (mt, kt): query rows 16 mt.., key tokens 32 kt.. with 32 kt <= 16 mt + 15
-    uint16_t* arec = reinterpret_cast<uint16_t*>(rec + Rec::AQ);
+    uint8_t* arec = rec + Rec::AQ;
     static_assert(NW == 4, "waves 1..3 take two A blocks each");
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -427,7 +476,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
         uint2 pk;
         pk.x = f2h2(a[0], a[1]);
         pk.y = f2h2(a[2], a[3]);
-        *reinterpret_cast<uint2*>(&arec[tri_off(t, pos)]) = pk;
+        *reinterpret_cast<uint2*>(arec + tri_frag_byte(t, pos)) = pk;
       }
     }
   }
@@ -485,12 +534,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   }
   __syncthreads();
 
-  // ---- T' = T diag(beta e^G / ||k||), T'' = T diag(beta): fp16 granules of 8
-  //      column positions (two token quads each), swizzled ----
-  uint16_t* twrec = reinterpret_cast<uint16_t*>(rec + Rec::TW);
-  uint16_t* tbrec = reinterpret_cast<uint16_t*>(rec + Rec::TB);
+  // ---- -T' = -T diag(beta e^G / ||k||), T'' = T diag(beta): fp16 granules of 8
+  //      column positions (two token quads each) ----
   for (int e = tid; e < 2 * kC * 8; e += NT) {
-    const int which = e >> 9;  // 0: T', 1: T''
+    const int which = e >> 9;  // 0: -T', 1: T''
     const int t = (e >> 3) & 63, gp = e & 7;
     if ((gp >> 2) > (t >> 5)) continue;  // above the diagonal blocks: not stored
     const float* c = which ? sm.bt : sm.cw;
@@ -501,249 +548,308 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     pk.y = f2h2(a.z, a.w);
     pk.z = f2h2(b.x, b.y);
     pk.w = f2h2(b.z, b.w);
-    *reinterpret_cast<uint4*>(&(which ? tbrec : twrec)[tri_off(t, 8 * gp)]) = pk;
+    *reinterpret_cast<uint4*>(rec + (which ? Rec::TB : Rec::TW) + tri_frag_byte(t, 8 * gp)) = pk;
   }
 }
 
 // ============================================================ state kernel ==
 template <int D>
 struct __align__(16) StateStage {
-  uint16_t Q[kC * D];     // raw q rows (fp16), swz<D>
-  uint16_t Kt[D * kC];    // k^ transposed: row = key, token positions, swz<64>
-  uint16_t Vt[kCB * kC];  // v transposed: row = value column, token positions, swz<64>
-  uint16_t W[kC * D];     // W = T diag(beta e^G) K^ rows (fp16), swz<D>
-  uint16_t Tb[3 * 1024];  // record TB
-  uint16_t A[3 * 1024];   // record AQ
-  float vec[256];         // record VEC: cQ[64], cK[64], e^gamma
+  h16x8_t Kt[D / 32 * 4][64];  // K^T fragments [key tile * 4 + token step][lane]; rows in
+                                // position order (row p holds key qswap(p))
+  h16x8_t W[2 * (D / 16)][64];  // -W fragments [token tile * D/16 + key step][lane]
+  f32x4_t U[2][2][4][64];       // U = T'' V, fp32: [column tile][token tile][quad][lane]
+  float vec[256];               // record VEC: cQ[64], cK[64], e^gamma
+};
+
+// What the chain waves hand the output waves for one chunk: their fp16
+// operand fragments of S (before the chunk's update) and of Vn, in register
+// order.
+template <int D>
+struct __align__(16) StateXchg {
+  h16x8_t Sh[2][D / 16][64];
+  h16x8_t Vh[2][4][64];
 };
 
 template <int D>
 struct __align__(16) StateSmem {
   StateStage<D> st[2];
-  uint16_t out[2][kC * kCB];  // bf16 output tiles of the last two chunks, swz<64>
+  StateXchg<D> xc[2];
+  uint16_t ot[2][32 * kCB];  // each output wave's bf16 tile on its way out, swz<64>
 };
 
-constexpr int kChainWaves = 2;  // 32 state columns each
-constexpr int kProdWaves = 4;
+constexpr int kStateWaves = 8;
 
-// Producer roles.  Waves are placed on the SIMDs round-robin, so chain waves
-// 0 and 1 share their SIMDs with producer waves 4 and 5, while waves 2 and 3
-// have a SIMD each.  Waves 2 and 3 ("K waves", pw = 0, 1) take the MFMA
-// work: for their key tiles kt = pw, pw + 2 (D = 128) they transpose the K
-// rows into K^T and multiply them by T' into the matching columns of W, so
-// everything they read back from LDS they wrote themselves; they also store
-// the previous chunk's outputs.  Waves 4 and 5 (pw = 2, 3) stage V^T, the raw
-// Q rows and the record blocks the chain reads (13 blocks of 1 KiB: Tb and A
-// (12), vec (1)).
-constexpr int kRecBlocks = 13;
+// Wave roles of the state kernel (wave w; waves land on the SIMDs in the
+// order 0, 2, 1, 3, 0, 2, 1, 3 or a rotation of it, so each SIMD runs two
+// roles):
+//   w 0, 1  chain: the recurrence for state columns 32 w .. 32 w + 31 of the
+//           workgroup's 64 (Vn = U - W S, S <- e^gamma S + K^T diag(cK) Vn)
+//   w 2, 3  output: O^T = S^T Q'^T + Vn^T A^T of token tile w - 2 (both
+//           chains' columns), one chunk behind the chain
+//   w 4, 5  U: U = T'' V for value-column tile w - 4
+//   w 6, 7  K: K^T and -W = -T' K for key tiles w - 6 (+ 2), and the
+//           record's vec block, into the stage
+// Per chunk the chain, U, output and K roles issue 32, 10, 24 and 20
+// matrix-core products of 32x32x16.
 
 // Per-lane prefetch registers of one chunk, one struct per role.
 template <int D>
-struct KPrefetch {                    // K waves
-  static constexpr int NKT = D / 64;  // key tiles per K wave
-  s16x8_t k[NKT][2][2];               // K rows: key tile pw + 2u, token tile tt, key k-step h
-  s16x8_t tw[6];                      // T' fragments (fp16 bits): (nt 0, ks 0..1), (nt 1, ks 0..3)
+struct KPrefetch {
+  static constexpr int NKT = D / 64;  // key tiles per K wave: pk, pk + 2
+  s16x8_t k[NKT][2][2];               // raw K rows: key tile pk + 2u, token tile tt, 16-key step h
+  s16x8_t tw[6];                      // -T' fragments
+  s16x8_t vec;                        // the lane's 16 bytes of the record vec block
+};
+
+struct UPrefetch {
+  s16x8_t v[2][2];  // raw V rows: token tile tt, value k-step h
+  s16x8_t tb[6];    // T'' fragments
 };
 
 template <int D>
-struct VPrefetch {                    // V / Q / record waves
-  static constexpr int NQ = D / 16;   // Q granules per lane
-  static constexpr int NREC = 7;      // record blocks per wave (ceil(13 / 2))
-  s16x8_t v[2][2];                    // V rows of V^T task 2 (pw - 2) + u, k-step h
-  s16x8_t q[NQ];
-  s16x8_t rec[NREC];
+struct OPrefetch {
+  s16x8_t q[D / 16];  // Q' fragments of the wave's token tile, per key step
+  s16x8_t a[4];       // A fragments 2 nt .. 2 nt + 3: k-steps 0..1 of tile 0, 0..3 of tile 1
 };
 
-// byte offset in the record of the staged 1 KiB block b (Tb, A, vec)
-__device__ __forceinline__ int rec_block_src(int b) { return b < 12 ? Rec::TB + b * 1024 : Rec::VEC; }
-
-// Identity fragment (bf16 B operand) of k-step h of a 32-wide column tile:
-// lane (n, g) has a 1 at slot e iff 16 h + 8 g + e == n.
-__device__ __forceinline__ s16x8_t ident_frag(int h, int n, int g) {
-  s16x8_t f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) f[e] = (16 * h + 8 * g + e == n) ? static_cast<short>(0x3f80) : static_cast<short>(0);
-  return f;
+// Raw buffer access: a wave-uniform base in the descriptor, the per-lane
+// byte offset in a VGPR that stays fixed across chunks, and the per-load part
+// in the scalar offset, so the prefetches need no per-load address registers.
+// The range is left open (offsets are computed in bounds); the third word is
+// the gfx9 raw-dword format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ s16x8_t buf_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(s16x8_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-__device__ __forceinline__ f32x16_t mfma32_bf16(const s16x8_t& a, const s16x8_t& b, const f32x16_t& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gdn::bf16x8_t, a),
-                                                 __builtin_bit_cast(gdn::bf16x8_t, b), c, 0, 0, 0);
-}
-
-// The prefetches issue the global loads of chunk (tok0, len) for this lane.
-// The chunk bases are wave-uniform; lane offsets are 32-bit.  Nothing here
-// consumes a loaded value, so the loads stay in flight until staging.  Rows
-// past the sequence end re-read its last token: those tokens carry zero
-// weights in T', T'' and cK, and their outputs are not stored.
+// The prefetches issue the loads of one chunk for this lane.  Nothing here
+// consumes a loaded value, so the loads stay in flight until staging.
+// K rows past the sequence end re-read its last token: those tokens carry
+// zero weights in T' and cK.  Rows and the vec block, then the -T' fragments.
 template <int D>
-__device__ __forceinline__ void k_prefetch(KPrefetch<D>& p, const uint16_t* kh, int sk, const uint8_t* rec,
-                                           int64_t tok0, int len, int pw, int lane) {
+__device__ __forceinline__ void k_prefetch_rows(KPrefetch<D>& p, const uint16_t* kh, int sk, const uint8_t* rec,
+                                                int64_t tok0, int len, int pk, int lane) {
   const int li = lane & 31, g = lane >> 5;
-  const uint16_t* kc = kh + tok0 * sk;
+  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kh + tok0 * sk);
 #pragma unroll
-  for (int u = 0; u < KPrefetch<D>::NKT; ++u)
+  for (int tt = 0; tt < 2; ++tt) {
+    const int row = min(32 * tt + li, len - 1);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int off = min(32 * tt + li, len - 1) * sk + 32 * (pw + 2 * u) + 8 * g;
-      p.k[u][tt][0] = *reinterpret_cast<const s16x8_t*>(kc + off);
-      p.k[u][tt][1] = *reinterpret_cast<const s16x8_t*>(kc + off + 16);
-    }
-  const uint16_t* twr = reinterpret_cast<const uint16_t*>(rec + Rec::TW);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) p.tw[ks] = *reinterpret_cast<const s16x8_t*>(twr + tri_off(li, 16 * ks + 8 * g));
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    p.tw[2 + ks] = *reinterpret_cast<const s16x8_t*>(twr + tri_off(32 + li, 16 * ks + 8 * g));
-}
-
-template <int D>
-__device__ __forceinline__ void v_prefetch(VPrefetch<D>& p, const uint16_t* qh, int sq, const uint16_t* vh, int sv,
-                                           const uint8_t* rec, int64_t tok0, int len, int pv, int lane) {
-  const int li = lane & 31, g = lane >> 5;
-  const uint16_t* vc = vh + tok0 * sv;
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int task = 2 * pv + u;
-    const int tt = task & 1, vt = task >> 1;
-    const int off = min(32 * tt + li, len - 1) * sv + 32 * vt + 8 * g;
-    p.v[u][0] = *reinterpret_cast<const s16x8_t*>(vc + off);
-    p.v[u][1] = *reinterpret_cast<const s16x8_t*>(vc + off + 16);
-  }
-  const uint16_t* qc = qh + tok0 * sq;
-  const int plane = pv * 64 + lane;
-#pragma unroll
-  for (int u = 0; u < VPrefetch<D>::NQ; ++u) {
-    const int id = plane + 128 * u;
-    const int t = id / (D / 8), c8 = id % (D / 8);
-    p.q[u] = *reinterpret_cast<const s16x8_t*>(qc + min(t, len - 1) * sq + 8 * c8);
-  }
-#pragma unroll
-  for (int u = 0; u < VPrefetch<D>::NREC; ++u) {
-    const int b = min(pv + 2 * u, kRecBlocks - 1);  // past the end: a repeat, not staged
-    p.rec[u] = *reinterpret_cast<const s16x8_t*>(rec + rec_block_src(b) + 16 * lane);
-  }
-}
-
-// raw bf16 -> fp16 (exact within the fp16 range)
-__device__ __forceinline__ h16x8_t bf8_to_h8_raw(const s16x8_t& x) {
-  const u32x4_t u = __builtin_bit_cast(u32x4_t, x);
-  u32x4_t r;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) r[p] = f2h2(lo_half(u[p]), hi_half(u[p]));
-  return __builtin_bit_cast(h16x8_t, r);
-}
-
-// K waves: K^T of their key tiles by bf16 identity products (C = K I of a
-// 32-token tile gives lane (key n, g) the tokens 8i + 4g + r, which belong at
-// positions 8g + 0..7 and 16 + 8g + 0..7; exact), then W = T' K as
-// W^T = K^T T'^T: the A operand reads the K^T rows this wave just wrote, in
-// qswap order, so lane (token t, g) ends up with keys 32 kt + 8 g + 0..7 and
-// 32 kt + 16 + 8 g + 0..7, two plain 16-byte pieces of row t of W.  k stays
-// unnormalised (1/||k|| is folded into T' and cK).
-template <int D>
-__device__ __forceinline__ void k_stage(const KPrefetch<D>& p, StateStage<D>& S, int pw, int lane,
-                                        const s16x8_t& id0, const s16x8_t& id1) {
-  const int li = lane & 31, g = lane >> 5;
-#pragma unroll
-  for (int u = 0; u < KPrefetch<D>::NKT; ++u) {
-    const int kt = pw + 2 * u;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      f32x16_t c = zero16();
-      c = mfma32_bf16(p.k[u][tt][0], id0, c);
-      c = mfma32_bf16(p.k[u][tt][1], id1, c);
-      const int row = 32 * kt + li;
-      *reinterpret_cast<h16x8_t*>(&S.Kt[swz<kC>(row, 32 * tt + 8 * g)]) = pack_h8<0>(c);
-      *reinterpret_cast<h16x8_t*>(&S.Kt[swz<kC>(row, 32 * tt + 16 + 8 * g)]) = pack_h8<8>(c);
+    for (int u = 0; u < KPrefetch<D>::NKT; ++u) {
+      const int off = 2 * (row * sk + 32 * (pk + 2 * u) + 8 * g);
+      p.k[u][tt][0] = buf_ld(rk, off, 0);
+      p.k[u][tt][1] = buf_ld(rk, off, 32);
     }
   }
-  wave_sync();  // the K^T rows are read back by this wave only
-  h16x8_t tw[6];
-#pragma unroll
-  for (int j = 0; j < 6; ++j) tw[j] = __builtin_bit_cast(h16x8_t, p.tw[j]);
-#pragma unroll
-  for (int u = 0; u < KPrefetch<D>::NKT; ++u) {
-    const int kt = pw + 2 * u;
-    const int arow = qswap(32 * kt + li);
-    h16x8_t kf[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kf[ks] = ld_h8(S.Kt, swz<kC>(arow, 16 * ks + 8 * g));
-    f32x16_t c0 = zero16(), c1 = zero16();
-    c0 = mfma32(kf[0], tw[0], c0);
-    c1 = mfma32(kf[0], tw[2], c1);
-    c0 = mfma32(kf[1], tw[1], c0);
-    c1 = mfma32(kf[1], tw[3], c1);
-    c1 = mfma32(kf[2], tw[4], c1);
-    c1 = mfma32(kf[3], tw[5], c1);
-    *reinterpret_cast<h16x8_t*>(&S.W[swz<D>(li, 32 * kt + 8 * g)]) = pack_h8<0>(c0);
-    *reinterpret_cast<h16x8_t*>(&S.W[swz<D>(li, 32 * kt + 16 + 8 * g)]) = pack_h8<8>(c0);
-    *reinterpret_cast<h16x8_t*>(&S.W[swz<D>(32 + li, 32 * kt + 8 * g)]) = pack_h8<0>(c1);
-    *reinterpret_cast<h16x8_t*>(&S.W[swz<D>(32 + li, 32 * kt + 16 + 8 * g)]) = pack_h8<8>(c1);
-  }
+  p.vec = buf_ld(buf_rsrc(rec), 16 * lane, Rec::VEC);
 }
 
-// V / Q / record waves: record blocks (Tb, A, vec), V^T by identity
-// products, raw q rows as fp16 (1/||q|| is folded into cQ).
 template <int D>
-__device__ __forceinline__ void v_stage(const VPrefetch<D>& p, StateStage<D>& S, int pv, int lane,
-                                        const s16x8_t& id0, const s16x8_t& id1) {
+__device__ __forceinline__ void k_prefetch_tw(KPrefetch<D>& p, const uint8_t* rec, int lane) {
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
+#pragma unroll
+  for (int j = 0; j < 6; ++j) p.tw[j] = buf_ld(r, 16 * lane, Rec::TW + 1024 * j);
+}
+
+// V rows past the sequence end re-read its last token: those tokens carry
+// zero weights in T'', and their outputs are not stored.
+__device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int sv, const uint8_t* rec,
+                                           int64_t tok0, int len, int c, int lane) {
   const int li = lane & 31, g = lane >> 5;
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vh + tok0 * sv);
 #pragma unroll
-  for (int u = 0; u < VPrefetch<D>::NREC; ++u) {
-    const int b = pv + 2 * u;
-    if (b < kRecBlocks) {
-      uint8_t* dst = b < 12 ? reinterpret_cast<uint8_t*>(S.Tb) + b * 1024 : reinterpret_cast<uint8_t*>(S.vec);
-      *reinterpret_cast<s16x8_t*>(dst + 16 * lane) = p.rec[u];
-    }
+  for (int tt = 0; tt < 2; ++tt) {
+    const int off = 2 * (min(32 * tt + li, len - 1) * sv + 32 * c + 8 * g);
+    p.v[tt][0] = buf_ld(rv, off, 0);
+    p.v[tt][1] = buf_ld(rv, off, 32);
   }
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int task = 2 * pv + u;
-    const int tt = task & 1, vt = task >> 1;
-    f32x16_t c = zero16();
-    c = mfma32_bf16(p.v[u][0], id0, c);
-    c = mfma32_bf16(p.v[u][1], id1, c);
-    const int row = 32 * vt + li;
-    *reinterpret_cast<h16x8_t*>(&S.Vt[swz<kC>(row, 32 * tt + 8 * g)]) = pack_h8<0>(c);
-    *reinterpret_cast<h16x8_t*>(&S.Vt[swz<kC>(row, 32 * tt + 16 + 8 * g)]) = pack_h8<8>(c);
+  for (int j = 0; j < 6; ++j) p.tb[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * j);
+}
+
+template <int D>
+__device__ __forceinline__ void o_prefetch(OPrefetch<D>& p, const uint8_t* rec, int nt, int lane) {
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) p.q[s] = buf_ld(r, 16 * lane, Rec::QP + 1024 * (nt * (D / 16) + s));
+  // four fragments for either tile (tile 0 uses the first two), so every
+  // path issues the same loads
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) p.a[ks] = buf_ld(r, 16 * lane, Rec::AQ + 1024 * (2 * nt + ks));
+}
+
+// K waves: K^T and -W of key tiles pk (+ 2) into the stage, as fragments.
+//  * K^T of a key tile by a bf16 identity product C = K I with the identity's
+//    columns qswap-ordered: lane (position n, g) of C holds key
+//    qswap(32 kt + n) at tokens 8i + 4g + r, i.e. at token positions
+//    8g + 0..7 (elements 0..7) and 16 + 8g + 0..7 (elements 8..15); the
+//    product is exact.
+//  * -W^T = K^T (-T')^T from those registers (as fp16 A fragments): lane
+//    (token t, g) of its C tiles holds keys 32 kt + 8g + 0..7 and
+//    32 kt + 16 + 8g + 0..7, the -W fragments of key steps 2 kt, 2 kt + 1.
+//  * The fp16 K^T fragments are also the state update's A operand.
+template <int D>
+__device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int pk, int lane, const uint16_t* kh,
+                                        int sk, const uint8_t* next_rec, int64_t next_tok0, int next_len) {
+  constexpr int KS = D / 16;
+  constexpr int NKT = KPrefetch<D>::NKT;
+  const int li = lane & 31, g = lane >> 5;
+  *reinterpret_cast<s16x8_t*>(reinterpret_cast<uint8_t*>(S.vec) + 16 * lane) = p.vec;
+  // K^T of both key tiles first: four independent product chains
+  const s16x8_t iq0 = ident_frag(0, qswap(li), g), iq1 = ident_frag(1, qswap(li), g);
+  f32x16_t kc[NKT][2];
+#pragma unroll
+  for (int u = 0; u < NKT; ++u)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) kc[u][tt] = mfma32_bf16(p.k[u][tt][0], iq0, zero16());
+#pragma unroll
+  for (int u = 0; u < NKT; ++u)
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) kc[u][tt] = mfma32_bf16(p.k[u][tt][1], iq1, kc[u][tt]);
+  // The next chunk's K rows and vec block go out as soon as these are read,
+  // its -T' fragments once the products below have read them: a single set
+  // of registers then carries a whole iteration's worth of loads.
+  k_prefetch_rows<D>(p, kh, sk, next_rec, next_tok0, next_len, pk, lane);
+  gdn::keep_loads_here();
+  f32x16_t cw[NKT][2];
+#pragma unroll
+  for (int u = 0; u < NKT; ++u) {
+    h16x8_t ka[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ka[ks] = (ks & 1) ? pack_h8<8>(kc[u][ks >> 1]) : pack_h8<0>(kc[u][ks >> 1]);
+    // the same fragments are the state update's K^T (rows in position order)
+    const int kt = pk + 2 * u;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) S.Kt[kt * 4 + ks][lane] = ka[ks];
+    cw[u][0] = mfma32(ka[0], as_h8(p.tw[0]), zero16());
+    cw[u][1] = mfma32(ka[0], as_h8(p.tw[2]), zero16());
+    cw[u][0] = mfma32(ka[1], as_h8(p.tw[1]), cw[u][0]);
+    cw[u][1] = mfma32(ka[1], as_h8(p.tw[3]), cw[u][1]);
+    cw[u][1] = mfma32(ka[2], as_h8(p.tw[4]), cw[u][1]);
+    cw[u][1] = mfma32(ka[3], as_h8(p.tw[5]), cw[u][1]);
   }
-  const int plane = pv * 64 + lane;
+  k_prefetch_tw<D>(p, next_rec, lane);
+  gdn::keep_loads_here();
 #pragma unroll
-  for (int u = 0; u < VPrefetch<D>::NQ; ++u) {
-    const int id = plane + 128 * u;
-    const int t = id / (D / 8), c8 = id % (D / 8);
-    *reinterpret_cast<h16x8_t*>(&S.Q[swz<D>(t, 8 * c8)]) = bf8_to_h8_raw(p.q[u]);
+  for (int u = 0; u < NKT; ++u) {
+    const int kt = pk + 2 * u;
+    S.W[2 * kt][lane] = pack_h8<0>(cw[u][0]);
+    S.W[2 * kt + 1][lane] = pack_h8<8>(cw[u][0]);
+    S.W[KS + 2 * kt][lane] = pack_h8<0>(cw[u][1]);
+    S.W[KS + 2 * kt + 1][lane] = pack_h8<8>(cw[u][1]);
   }
 }
 
-// K waves: store one chunk's output tile (bf16 [64 tokens][64 columns] in
-// LDS, swz<64>) to o with 16-byte stores, 8 lanes per token row.
+// U waves: V^T of column tile c by the natural identity, then U = T'' V; U's
+// C tiles are stored lane-major for the chain wave that owns the columns.
 template <int D>
-__device__ __forceinline__ void store_out(const uint16_t* out, uint16_t* o, int64_t tok0, int len, int Hv, int h,
-                                          int cb, int pw, int lane) {
+__device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, int c, int lane) {
+  const int li = lane & 31, g = lane >> 5;
+  const s16x8_t in0 = ident_frag(0, li, g), in1 = ident_frag(1, li, g);
+  f32x16_t vt[2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    vt[tt] = mfma32_bf16(p.v[tt][0], in0, zero16());
+    vt[tt] = mfma32_bf16(p.v[tt][1], in1, vt[tt]);
+  }
+  h16x8_t vb[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) vb[ks] = (ks & 1) ? pack_h8<8>(vt[ks >> 1]) : pack_h8<0>(vt[ks >> 1]);
+  f32x16_t u0 = zero16(), u1 = zero16();
+  u0 = mfma32(as_h8(p.tb[0]), vb[0], u0);
+  u1 = mfma32(as_h8(p.tb[2]), vb[0], u1);
+  u0 = mfma32(as_h8(p.tb[1]), vb[1], u0);
+  u1 = mfma32(as_h8(p.tb[3]), vb[1], u1);
+  u1 = mfma32(as_h8(p.tb[4]), vb[2], u1);
+  u1 = mfma32(as_h8(p.tb[5]), vb[3], u1);
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    S.U[c][0][qd][lane] = f32x4_t{u0[4 * qd], u0[4 * qd + 1], u0[4 * qd + 2], u0[4 * qd + 3]};
+    S.U[c][1][qd][lane] = f32x4_t{u1[4 * qd], u1[4 * qd + 1], u1[4 * qd + 2], u1[4 * qd + 3]};
+  }
+}
+
+// Output waves: O^T = S^T Q'^T + Vn^T A^T for token tile nt and the 32
+// columns of each chain (two independent accumulation chains), stored straight
+// from the C tiles: lane (token t, g) holds value columns 8 i + 4 g + 0..3.
+template <int D>
+__device__ __forceinline__ void o_chunk(const OPrefetch<D>& p, const StateXchg<D>& X, uint16_t* ot, uint16_t* ob,
+                                        int len, int Hv, int nt, int lane) {
+  constexpr int KS = D / 16;
+  h16x8_t sh[2][KS], vh[2][4];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) sh[c][s] = X.Sh[c][s][lane];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) vh[c][s] = X.Vh[c][s][lane];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Tile 0 has no A entries at token steps 2 and 3; the fragments loaded there
+  // (tile 1's, so that both tiles issue the same loads) are masked to zero.
+  // Every product then runs on every path, and no loaded register is left
+  // unread.
+  const uint32_t keep_hi = nt ? 0xffffffffu : 0u;
+  h16x8_t af[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const u32x4_t x = __builtin_bit_cast(u32x4_t, p.a[s]);
+    af[s] = __builtin_bit_cast(h16x8_t, s < 2 ? x : (x & keep_hi));
+  }
+  f32x16_t acc[2] = {zero16(), zero16()};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    acc[0] = mfma32(sh[0][s], as_h8(p.q[s]), acc[0]);
+    acc[1] = mfma32(sh[1][s], as_h8(p.q[s]), acc[1]);
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    acc[0] = mfma32(vh[0][s], af[s], acc[0]);
+    acc[1] = mfma32(vh[1][s], af[s], acc[1]);
+  }
+  // The C tiles give each lane 4 columns of a row per store; rows go out
+  // whole instead (8 lanes per 128-byte row), through the wave's own LDS tile.
+  const int tl = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x2_t pk;
+      pk[0] = gdn::f2bf2(acc[c][4 * i], acc[c][4 * i + 1]);
+      pk[1] = gdn::f2bf2(acc[c][4 * i + 2], acc[c][4 * i + 3]);
+      *reinterpret_cast<u32x2_t*>(&ot[swz<kCB>(tl, 32 * c + 8 * i + 4 * g)]) = pk;
+    }
+  wave_sync();
+  // Raw buffer stores whose range ends at the chunk's last token: rows past
+  // the sequence end fall outside it and are dropped, so every path issues
+  // the same stores.
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(ob, static_cast<short>(0), len * Hv * D * 2, 0x00020000);
+  const int gr = lane & 7;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int id = pw * 64 + lane + 128 * u;
-    const int row = id >> 3, gr = id & 7;
-    if (row < len)
-      *reinterpret_cast<uint4*>(o + ((tok0 + row) * Hv + h) * D + cb * kCB + 8 * gr) =
-          *reinterpret_cast<const uint4*>(out + swz<kCB>(row, 8 * gr));
+    const int row = 8 * u + (lane >> 3);
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(&ot[swz<kCB>(row, 8 * gr)]);
+    __builtin_amdgcn_raw_buffer_store_b128(x, r, 2 * ((32 * nt + row) * Hv * D + 8 * gr), 0, 0);
   }
+  wave_sync();  // the tile is read before the next chunk's writes
 }
 
-// grid = 8 * ceil(n_seqs * Hv * NCB / 8), NCB = D / 64; block = 64 * 6.
-// Workgroup (sequence r, value head h, column block cb): waves 0, 1 own the
-// state columns cb*64 + 32 w .. + 32 (the chain); waves 2..5 stage chunks
-// and store outputs.  One workgroup barrier per chunk: the producer fills the
-// stage buffer the chain is not reading and stores the output tile the chain
-// wrote in the previous chunk; no producer wave reads what another one wrote.
+// grid = 8 * ceil(n_seqs * Hv * NCB / 8), NCB = D / 64; block = 64 * 8.
+// Workgroup (sequence r, value head h, column block cb) owns state columns
+// cb*64 .. cb*64 + 63.  One workgroup barrier per chunk j: before it the
+// chain consumes stage j % 2 and writes exchange j % 2, the K and U waves fill
+// stage (j + 1) % 2, and the output waves read exchange (j - 1) % 2.  No wave
+// reads what another wave wrote before the barrier that separates them.
 template <int D>
-__global__ __launch_bounds__(64 * (kChainWaves + kProdWaves)) void chunk_state_kernel(
-    const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
-    const uint16_t* __restrict__ v, int64_t sv, const uint8_t* __restrict__ ws, const float* h0, float* hT,
-    const int64_t* __restrict__ ids, int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hk,
-    int Hv, uint16_t* __restrict__ o) {
+__global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
+    const uint16_t* __restrict__ k, int64_t sk, const uint16_t* __restrict__ v, int64_t sv,
+    const uint8_t* __restrict__ ws, const float* h0, float* hT, const int64_t* __restrict__ ids, int64_t sstride,
+    const int64_t* __restrict__ cu, int n_seqs, int Hk, int Hv, uint16_t* __restrict__ o) {
   constexpr int NCB = D / kCB;
   constexpr int NR = D / 32;  // 32-row tiles of the state
   constexpr int KS = D / 16;  // k-steps over keys
@@ -770,61 +876,120 @@ __global__ __launch_bounds__(64 * (kChainWaves + kProdWaves)) void chunk_state_k
   }
   __syncthreads();
   const int64_t cbase = s_base;
-  const uint8_t* rec0 = ws + (cbase * Hv + h) * Rec::BYTES;
-  const int64_t rec_stride = static_cast<int64_t>(Hv) * Rec::BYTES;
+  const int64_t rec_stride = static_cast<int64_t>(Hv) * rec_bytes(D);
+  const uint8_t* rec0 = ws + cbase * rec_stride + static_cast<int64_t>(h) * rec_bytes(D);
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int li = lane & 31, g = lane >> 5;
 
-  if (wave >= kChainWaves) {
-    // ---------------------------------------------------------- producer --
-    const int pw = wave - kChainWaves;
-    const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
-    const uint16_t* khp = k + static_cast<int64_t>(kh) * D;
-    const uint16_t* vh = v + static_cast<int64_t>(h) * D + cb * kCB;
-    if (nch == 0) return;
-    const int sqi = static_cast<int>(sq), ski = static_cast<int>(sk), svi = static_cast<int>(sv);
-    const s16x8_t id0 = ident_frag(0, li, g), id1 = ident_frag(1, li, g);
-    // The prefetch of chunk j + 2 is issued as soon as chunk j + 1 has left
-    // the registers, so its loads have a whole chunk of chain work to land.
 #define GDN_LEN(j_) static_cast<int>(min<int64_t>(kC, seqlen - (j_) * kC))
-    if (pw < 2) {
-      KPrefetch<D> p;
-      k_prefetch<D>(p, khp, ski, rec0, bos, GDN_LEN(0), pw, lane);
-      k_stage<D>(p, sm.st[0], pw, lane, id0, id1);
-      if (nch > 1) k_prefetch<D>(p, khp, ski, rec0 + rec_stride, bos + kC, GDN_LEN(1), pw, lane);
+  if (wave >= 2) {
+    if (nch == 0) return;
+    if (wave < 4) {
+      // ------------------------------------------------------------ output --
+      // Chunk c's operands live in register set c % 2; its loads go out right
+      // after chunk c - 2 is done, about one and a half iterations before use.
+      // The compiler's load counters must stay exact for that, so no load may
+      // look younger than it is: every path issues the same loads (past the
+      // last chunk they repeat it), the sets go out oldest first, and the loop
+      // has a single exit (two chunks per trip, the odd one after it).
+      const int nt = wave - 2;
+      uint16_t* oh = o + (bos * Hv + h) * D + cb * kCB;
+      const int64_t ostride = static_cast<int64_t>(kC) * Hv * D;
+      OPrefetch<D> p0, p1;
+      o_prefetch<D>(p0, rec0, nt, lane);
+      gdn::keep_loads_here();  // the sets go out oldest first, as in the loop
+      o_prefetch<D>(p1, rec0 + min<int64_t>(1, nch - 1) * rec_stride, nt, lane);
+      gdn::keep_loads_here();
       gdn::lds_barrier();
-      for (int64_t j = 0; j < nch; ++j) {
-        if (j + 1 < nch) {
-          k_stage<D>(p, sm.st[(j + 1) & 1], pw, lane, id0, id1);
-          if (j + 2 < nch)
-            k_prefetch<D>(p, khp, ski, rec0 + (j + 2) * rec_stride, bos + (j + 2) * kC, GDN_LEN(j + 2), pw, lane);
-        }
-        if (j > 0) store_out<D>(sm.out[(j - 1) & 1], o, bos + (j - 1) * kC, kC, Hv, h, cb, pw, lane);
-        gdn::lds_barrier();
+      gdn::lds_barrier();  // iteration 0: no chunk finished yet
+#define GDN_OITER(jj, PC)                                                                     \
+  o_chunk<D>(PC, sm.xc[((jj) - 1) & 1], sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, nt, lane); \
+  __builtin_amdgcn_sched_barrier(0);                                                          \
+  o_prefetch<D>(PC, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);          \
+  gdn::keep_loads_here();                                                                     \
+  gdn::lds_barrier();
+      int64_t j = 1;
+      for (; j + 1 < nch; j += 2) {
+        GDN_OITER(j, p0)      // computes chunk j - 1 (even), loads chunk j + 1
+        GDN_OITER(j + 1, p1)  // computes chunk j (odd), loads chunk j + 2
       }
-      store_out<D>(sm.out[(nch - 1) & 1], o, bos + (nch - 1) * kC, GDN_LEN(nch - 1), Hv, h, cb, pw, lane);
+      if (j < nch) {
+        GDN_OITER(j, p0)
+      }
+#undef GDN_OITER
+      if ((nch - 1) & 1)
+        o_chunk<D>(p1, sm.xc[1], sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, nt, lane);
+      else
+        o_chunk<D>(p0, sm.xc[0], sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, nt, lane);
     } else {
-      const int pv = pw - 2;
-      VPrefetch<D> p;
-      v_prefetch<D>(p, qh, sqi, vh, svi, rec0, bos, GDN_LEN(0), pv, lane);
-      v_stage<D>(p, sm.st[0], pv, lane, id0, id1);
-      if (nch > 1) v_prefetch<D>(p, qh, sqi, vh, svi, rec0 + rec_stride, bos + kC, GDN_LEN(1), pv, lane);
-      gdn::lds_barrier();
-      for (int64_t j = 0; j < nch; ++j) {
-        if (j + 1 < nch) {
-          v_stage<D>(p, sm.st[(j + 1) & 1], pv, lane, id0, id1);
-          if (j + 2 < nch)
-            v_prefetch<D>(p, qh, sqi, vh, svi, rec0 + (j + 2) * rec_stride, bos + (j + 2) * kC, GDN_LEN(j + 2), pv,
-                          lane);
-        }
+      // --------------------------------------------------------- U and copy --
+      // Chunk c's inputs live in register set c % 3; the loads of chunk j + 3
+      // go out before chunk j + 1 is staged, two iterations ahead of their use.
+      // The loop runs three chunks per trip so each set stays a fixed set of
+      // registers; as for the output waves, every path issues the same loads,
+      // oldest set first, and the loop has a single exit.
+#define GDN_PITER(jj, LD, ST, PREFETCH, STAGE)               \
+  PREFETCH(LD, min<int64_t>((jj) + 3, nch - 1));             \
+  gdn::keep_loads_here();                                    \
+  if ((jj) + 1 < nch) STAGE(ST, ((jj) + 1) & 1);             \
+  gdn::lds_barrier();
+      if (wave < 6) {
+        const int c = wave - 4;
+        const uint16_t* vh = v + static_cast<int64_t>(h) * D + cb * kCB;
+        const int svi = static_cast<int>(sv);
+#define GDN_UPF(P, jc) u_prefetch(P, vh, svi, rec0 + (jc) * rec_stride, bos + (jc) * kC, GDN_LEN(jc), c, lane)
+#define GDN_UST(P, b) u_stage<D>(P, sm.st[b], c, lane)
+        UPrefetch p0, p1, p2;
+        GDN_UPF(p0, 0);
+        gdn::keep_loads_here();  // the sets go out oldest first, as in the loop
+        GDN_UPF(p1, min<int64_t>(1, nch - 1));
+        gdn::keep_loads_here();
+        GDN_UPF(p2, min<int64_t>(2, nch - 1));
+        gdn::keep_loads_here();
+        GDN_UST(p0, 0);
         gdn::lds_barrier();
+        int64_t j = 0;
+        for (; j + 2 < nch; j += 3) {
+          GDN_PITER(j, p0, p1, GDN_UPF, GDN_UST)
+          GDN_PITER(j + 1, p1, p2, GDN_UPF, GDN_UST)
+          GDN_PITER(j + 2, p2, p0, GDN_UPF, GDN_UST)
+        }
+        if (j < nch) {
+          GDN_PITER(j, p0, p1, GDN_UPF, GDN_UST)
+        }
+        if (j + 1 < nch) {
+          GDN_PITER(j + 1, p1, p2, GDN_UPF, GDN_UST)
+        }
+#undef GDN_UPF
+#undef GDN_UST
+      } else {
+        // One register set: each stage issues the next chunk's loads as soon
+        // as it has read the registers they land in.
+        const int pk = wave - 6;
+        const uint16_t* khp = k + static_cast<int64_t>(kh) * D;
+        const int ski = static_cast<int>(sk);
+#define GDN_KSTAGE(jc, jn)                                                                          \
+  k_stage<D>(p, sm.st[(jc) & 1], pk, lane, khp, ski, rec0 + (jn) * rec_stride, bos + (jn) * kC, GDN_LEN(jn))
+        KPrefetch<D> p;
+        k_prefetch_rows<D>(p, khp, ski, rec0, bos, GDN_LEN(0), pk, lane);
+        k_prefetch_tw<D>(p, rec0, lane);
+        gdn::keep_loads_here();
+        GDN_KSTAGE(0, min<int64_t>(1, nch - 1));
+        gdn::lds_barrier();
+        for (int64_t j = 0; j + 1 < nch; ++j) {  // an unconditional body keeps the load counters exact
+          GDN_KSTAGE(j + 1, min<int64_t>(j + 2, nch - 1));
+          gdn::lds_barrier();
+        }
+        gdn::lds_barrier();  // the last chunk: nothing left to stage
+#undef GDN_KSTAGE
       }
+#undef GDN_PITER
     }
-#undef GDN_LEN
     return;
   }
+#undef GDN_LEN
 
   // -------------------------------------------------------------- chain --
   const int64_t srow = ids ? ids[r] : r;
@@ -846,124 +1011,87 @@ __global__ __launch_bounds__(64 * (kChainWaves + kProdWaves)) void chunk_state_k
   if (nch > 0) gdn::lds_barrier();
   for (int64_t jc = 0; jc < nch; ++jc) {
     const StateStage<D>& B = sm.st[jc & 1];
+    StateXchg<D>& X = sm.xc[jc & 1];
     // Re-derive lane indices from an opaque copy each chunk so the compiler
     // does not keep every lane-dependent address live across the loop.
     int tid_l = static_cast<int>(threadIdx.x);
     asm volatile("" : "+v"(tid_l));
     const int ln = tid_l & 63;
-    const int m = ln & 31, lgp = ln >> 5;
 
     // Operand fragments of each product are read from LDS as one batch ahead
     // of its MFMAs, so the reads overlap each other instead of each MFMA
     // waiting out an LDS latency.
-    // U = T'' V (rows = tokens, cols = this wave's 32 value columns)
-    f32x16_t U[2];
-    {
-      h16x8_t vf[4], tf[6];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) vf[ks] = ld_h8(B.Vt, swz<kC>(32 * wave + m, 16 * ks + 8 * lgp));
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) tf[ks] = ld_h8(B.Tb, tri_off(m, 16 * ks + 8 * lgp));
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) tf[2 + ks] = ld_h8(B.Tb, tri_off(32 + m, 16 * ks + 8 * lgp));
-      __builtin_amdgcn_sched_barrier(0);  // keep the batch of reads ahead of the products
-      U[0] = mfma32(tf[0], vf[0], zero16());
-      U[1] = mfma32(tf[2], vf[0], zero16());
-      U[0] = mfma32(tf[1], vf[1], U[0]);
-      U[1] = mfma32(tf[3], vf[1], U[1]);
-      U[1] = mfma32(tf[4], vf[2], U[1]);
-      U[1] = mfma32(tf[5], vf[3], U[1]);
-    }
-    // S as fp16 fragments (B operand of W S, A operand of S^T Q^T)
+    // S as fp16 fragments: B operand of W S here, A operand of the output
+    // wave's S^T Q'^T
     h16x8_t Sh[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) Sh[s] = (s & 1) ? pack_h8<8>(S[s >> 1]) : pack_h8<0>(S[s >> 1]);
-    // Vn = U - W S, both 32-token tiles interleaved
+    // Vn = U + (-W) S, both 32-token tiles interleaved, accumulated onto U
+    f32x16_t U[2];
     {
       h16x8_t wf[2][KS];
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        wf[0][s] = ld_h8(B.W, swz<D>(m, 16 * s + 8 * lgp));
-        wf[1][s] = ld_h8(B.W, swz<D>(32 + m, 16 * s + 8 * lgp));
+        wf[0][s] = B.W[s][ln];
+        wf[1][s] = B.W[KS + s][ln];
       }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4_t u4 = B.U[wave][mt][qd][ln];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = u4[rr];
+        }
       __builtin_amdgcn_sched_barrier(0);
-      f32x16_t a0 = zero16(), a1 = zero16();
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        a0 = mfma32(wf[0][s], Sh[s], a0);
-        a1 = mfma32(wf[1][s], Sh[s], a1);
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        U[0][e] -= a0[e];
-        U[1][e] -= a1[e];
+        U[0] = mfma32(wf[0][s], Sh[s], U[0]);
+        U[1] = mfma32(wf[1][s], Sh[s], U[1]);
       }
     }
-    // Vn (for A Vn) and Vn' = diag(cK) Vn (for the state update) as fp16
-    h16x8_t Vh[4], Vk[4];
+    // the exchange copy of S, and the decay of the old state, while W S runs
 #pragma unroll
-    for (int s = 0; s < 4; ++s) Vh[s] = (s & 1) ? pack_h8<8>(U[s >> 1]) : pack_h8<0>(U[s >> 1]);
+    for (int s = 0; s < KS; ++s) X.Sh[wave][s][ln] = Sh[s];
+    const float eg = B.vec[2 * kC];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int rt = 0; rt < NR; ++rt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4_t ck = *reinterpret_cast<const f32x4_t*>(&B.vec[kC + 32 * mt + 8 * i + 4 * lgp]);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) U[mt][4 * i + rr] *= ck[rr];
-      }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) Vk[s] = (s & 1) ? pack_h8<8>(U[s >> 1]) : pack_h8<0>(U[s >> 1]);
-    // S <- e^gamma S + K^T Vn'  (the old S lives on in Sh for the outputs)
+      for (int e = 0; e < 16; ++e) S[rt][e] *= eg;
+    // S <- e^gamma S + K^T diag(cK) Vn
     {
       h16x8_t kf[NR][4];
 #pragma unroll
       for (int rt = 0; rt < NR; ++rt)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kf[rt][s] = ld_h8(B.Kt, swz<kC>(qswap(32 * rt + m), 16 * s + 8 * lgp));
-      const float eg = B.vec[2 * kC];
+        for (int s = 0; s < 4; ++s) kf[rt][s] = B.Kt[rt * 4 + s][ln];
+      // cK of the tokens 32 mt + 8 i + 4 lgp + r held by this lane's Vn elements
+      f32x4_t ck[2][4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          ck[mt][i] = *reinterpret_cast<const f32x4_t*>(&B.vec[kC + 32 * mt + 8 * i + 4 * (ln >> 5)]);
+      // Vn as fp16 (A operand of Vn^T A^T) and diag(cK) Vn as fp16 (B operand
+      // of the update)
+      h16x8_t Vh[4], Vk[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) Vh[s] = (s & 1) ? pack_h8<8>(U[s >> 1]) : pack_h8<0>(U[s >> 1]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) U[mt][4 * i + r] *= ck[mt][i][r];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) Vk[s] = (s & 1) ? pack_h8<8>(U[s >> 1]) : pack_h8<0>(U[s >> 1]);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int rt = 0; rt < NR; ++rt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) S[rt][e] *= eg;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int rt = 0; rt < NR; ++rt) S[rt] = mfma32(kf[rt][s], Vk[s], S[rt]);
-    }
-    // O^T = diag(cQ) S^T Q^T + Vn^T A^T, per 32-token tile; the k-steps of
-    // S^T Q^T alternate between two accumulators so the MFMAs do not wait on
-    // each other's results
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      h16x8_t qf[KS], af[4];
-#pragma unroll
-      for (int s = 0; s < KS; ++s) qf[s] = ld_h8(B.Q, swz<D>(32 * nt + m, 16 * s + 8 * lgp));
-#pragma unroll
-      for (int s = 0; s < 2 * nt + 2; ++s) af[s] = ld_h8(B.A, tri_off(32 * nt + m, 16 * s + 8 * lgp));
-      const float cq = B.vec[32 * nt + m];
-      __builtin_amdgcn_sched_barrier(0);
-      f32x16_t acc = zero16(), acc1 = zero16();
-#pragma unroll
-      for (int s = 0; s < KS; s += 2) {
-        acc = mfma32(Sh[s], qf[s], acc);
-        acc1 = mfma32(Sh[s + 1], qf[s + 1], acc1);
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] = (acc[e] + acc1[e]) * cq;
-#pragma unroll
-      for (int s = 0; s < 2 * nt + 2; ++s) acc = mfma32(Vh[s], af[s], acc);
-      // lane (token t, g) holds value columns 8 i + 4 g + 0..3 of its 32;
-      // the producer's K waves store the tile after the chunk barrier
-      uint16_t* ob = sm.out[jc & 1];
-      const int t = 32 * nt + m;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint2 pk;
-        pk.x = gdn::f2bf2(acc[4 * i], acc[4 * i + 1]);
-        pk.y = gdn::f2bf2(acc[4 * i + 2], acc[4 * i + 3]);
-        *reinterpret_cast<uint2*>(&ob[swz<kCB>(t, 32 * wave + 8 * i + 4 * lgp)]) = pk;
-      }
+      for (int s = 0; s < 4; ++s) X.Vh[wave][s][ln] = Vh[s];
     }
     gdn::lds_barrier();
   }
@@ -993,8 +1121,8 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   if (st != GDN_OK) return st;
   const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv * (D / kCB);
   const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * (kChainWaves + kProdWaves)), 0, stream>>>(
-      q, sq, k, sk, v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hk, Hv, o);
+  chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
+      k, sk, v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hk, Hv, o);
   return gdn_launch_status();
 }
 
@@ -1003,7 +1131,7 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
 extern "C" int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D) {
   if (N < 0 || n_seqs < 0 || Hv <= 0 || (D != 64 && D != 128)) return -1;
   const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
-  return nc_bound * Hv * Rec::BYTES;
+  return nc_bound * Hv * rec_bytes(D);
 }
 
 extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k,
@@ -1028,7 +1156,7 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
       ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
     return GDN_ERR_INVALID_ARG;
   const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
-  if (workspace_bytes < nc_bound * Hv * Rec::BYTES) return GDN_ERR_INVALID_ARG;
+  if (workspace_bytes < nc_bound * Hv * rec_bytes(D)) return GDN_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   if (D == 128)

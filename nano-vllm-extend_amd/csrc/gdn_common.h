@@ -71,10 +71,18 @@ __device__ __forceinline__ float wave_sum(float v) {
 // each barrier.  This barrier orders LDS accesses only (lgkmcnt(0)); global
 // loads stay in flight across it.  Global memory written by one wave and read
 // by another still needs __syncthreads().
+// Compiler-level fence for memory operations (emits no instruction): loads
+// issued before it stay before it, so a prefetch is not sunk next to its use.
+__device__ __forceinline__ void keep_loads_here() { asm volatile("" ::: "memory"); }
+
 __device__ __forceinline__ void lds_barrier() {
+  // No instruction is scheduled across the barrier: work moved ahead of it
+  // would wait there on loads that are meant to stay in flight.
+  __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // ---- XCD-aware block remap ----
