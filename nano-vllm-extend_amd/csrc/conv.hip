@@ -31,14 +31,25 @@ __device__ __forceinline__ Vec8 load8(const uint16_t* p) {
 
 __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
   uint4 u;
-  uint16_t* s = reinterpret_cast<uint16_t*>(&u);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) s[i] = gdn::f2bf(v[i]);
+  u.x = gdn::f2bf2(v[0], v[1]);
+  u.y = gdn::f2bf2(v[2], v[3]);
+  u.z = gdn::f2bf2(v[4], v[5]);
+  u.w = gdn::f2bf2(v[6], v[7]);
   *reinterpret_cast<uint4*>(p) = u;
 }
 
-// y = acc * sigmoid(acc), as the reference epilogue computes it.
-__device__ __forceinline__ float silu_mul(float acc) { return acc * (1.0f / (1.0f + expf(-acc))); }
+// y = acc * sigmoid(acc), the reference epilogue's form: the library expf,
+// and 1 / (1 + e) as the hardware reciprocal refined by one Newton step
+// (within an ulp of the divide, a fraction of the divide's instructions).
+// The exponent is capped at 88 so 1 + e stays finite (the Newton step would
+// turn an infinite e into NaN); below acc = -88 y is then ~ -5e-37 where the
+// divide gives -0, both far under any bf16 output step of interest.
+__device__ __forceinline__ float silu_mul(float acc) {
+  const float d = 1.0f + expf(fminf(-acc, 88.0f));
+  float r = __builtin_amdgcn_rcpf(d);
+  r = fmaf(r, fmaf(-d, r, 1.0f), r);
+  return acc * r;
+}
 
 // The reference writes the rolled state as (x + s) with the other operand
 // masked to zero, which maps -0.0 to +0.0 and is otherwise a bit copy.
