@@ -127,6 +127,8 @@ __device__ __forceinline__ void wave_sync() {
 //                      cK[64] = e^{gamma - G_t} / ||k_t|| (0 past the sequence end),
 //                      e^gamma
 //   QP  [2][D/16]      Q' = diag(cQ) q: [token tile][key step]
+//   KT  [D/32][4]      K^T, rows in position order (row p holds key qswap(p)):
+//                      [key tile][token step]
 struct Rec {
   static constexpr int TW = 0;
   static constexpr int TB = 6144;
@@ -134,8 +136,9 @@ struct Rec {
   static constexpr int VEC = 18432;
   static constexpr int QP = 19456;
 };
+__host__ __device__ constexpr int64_t rec_kt(int D) { return Rec::QP + 128LL * D; }
 // bytes of one record (a multiple of 256)
-__host__ __device__ constexpr int64_t rec_bytes(int D) { return Rec::QP + 128LL * D; }
+__host__ __device__ constexpr int64_t rec_bytes(int D) { return Rec::QP + 256LL * D; }
 
 // byte offset of fragment f, lane l
 __device__ __forceinline__ int frag_byte(int f, int l) { return (f * 64 + l) * 16; }
@@ -265,7 +268,7 @@ __device__ __forceinline__ int quad_of_pos(int P) { return qswap(4 * P) >> 2; }
 // grid = 8 * ceil(nc_bound * Hv / 8); block = 256.  One workgroup per
 // (chunk, value head); writes the chunk's record.
 template <int D>
-__global__ __launch_bounds__(256) void chunk_prep_kernel(
+__global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
     const float* __restrict__ g, const uint16_t* __restrict__ beta, const int64_t* __restrict__ cu,
     int n_seqs, int64_t nc_bound, int Hk, int Hv, float scale, int l2norm, uint8_t* __restrict__ ws) {
@@ -297,52 +300,46 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   const int lg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // Waves 1..3 form the A blocks b = wave - 1 and wave + 2 later on; their q
-  // rows (B operands) are loaded now so the loads overlap the whole first half.
-  s16x8_t qpre[2][KTD];
-  if (wave > 0) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int b = wave - 1 + 3 * u;
-      const int mt = b < 2 ? b : 2 + ((b - 2) >> 1);
-      const uint16_t* qr = qh + (tok0 + min(16 * mt + lr, len - 1)) * sq + 8 * lg;
-#pragma unroll
-      for (int kk = 0; kk < KTD; ++kk) qpre[u][kk] = *reinterpret_cast<const s16x8_t*>(qr + 32 * kk);
-    }
-  }
-
   // ---- phase 1: K rows, row norms of K and Q, gates ----
-  s16x8_t qraw[NSEG1];  // this thread's q segments, scaled into Q' once cQ is known
+  // q is read once, straight into the layout in which it serves as the A
+  // blocks' B operand: wave w holds query rows 16 w + lr, keys 32 kk + 8 lg.
+  // The same registers become Q' once cQ is known.
+  s16x8_t qv[KTD];
+  {
+    const int t = 16 * wave + lr;
+    const uint16_t* qr = qh + (tok0 + min(t, len - 1)) * sq + 8 * lg;
+    float qs = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KTD; ++kk) {
+      qv[kk] = *reinterpret_cast<const s16x8_t*>(qr + 32 * kk);
+      if (t >= len) qv[kk] = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float qf = gdn::bf2f(static_cast<uint16_t>(qv[kk][i]));
+        qs += qf * qf;
+      }
+    }
+    qs += __shfl_xor(qs, 16, 64);
+    qs += __shfl_xor(qs, 32, 64);
+    if (lg == 0) sm.ssq[t] = qs;
+  }
 #pragma unroll
   for (int j = 0; j < NSEG1; ++j) {
     const int e = tid + NT * j;
     const int t = e / SEG, c8 = e % SEG;
     const int64_t row = tok0 + min(t, len - 1);
     s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + row * sk + c8 * 8);
-    s16x8_t qv8 = *reinterpret_cast<const s16x8_t*>(qh + row * sq + c8 * 8);
-    if (t >= len) {
-      kv8 = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      qv8 = kv8;
-    }
-    qraw[j] = qv8;
+    if (t >= len) kv8 = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
     *reinterpret_cast<s16x8_t*>(&sm.Kr[t][c8 * 8]) = kv8;
-    float ks = 0.f, qs = 0.f;
+    float ks = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
-      const float qf = gdn::bf2f(static_cast<uint16_t>(qv8[i]));
       ks += kf * kf;
-      qs += qf * qf;
     }
 #pragma unroll
-    for (int m = SEG / 2; m >= 1; m >>= 1) {
-      ks += __shfl_xor(ks, m, 64);
-      qs += __shfl_xor(qs, m, 64);
-    }
-    if (c8 == 0) {
-      sm.ssk[t] = ks;
-      sm.ssq[t] = qs;
-    }
+    for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
+    if (c8 == 0) sm.ssk[t] = ks;
   }
   if (wave == 0) {
     float gv = 0.f, bv = 0.f;
@@ -360,6 +357,28 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     sm.bt[lane] = bv;
   }
   __syncthreads();
+
+  // ---- K^T (as soon as the K rows are in LDS, so its stores retire during
+  //      the solve), key tile kt = wave, by a bf16 identity product C = K I
+  //      with the identity's columns qswap-ordered: lane (position n, g) of C holds
+  //      key qswap(32 kt + n) at tokens 8i + 4g + r, i.e. at token positions
+  //      8g + 0..7 (elements 0..7) and 16 + 8g + 0..7 (elements 8..15); the
+  //      product is exact, the fp16 packing rounds K once. ----
+  if (wave < D / 32) {
+    const int kt = wave;
+    const int li = lane & 31, g = lane >> 5;
+    const s16x8_t iq0 = ident_frag(0, qswap(li), g), iq1 = ident_frag(1, qswap(li), g);
+    uint8_t* kp = rec + rec_kt(D);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const s16x8_t* kr = reinterpret_cast<const s16x8_t*>(&sm.Kr[32 * tt + li][32 * kt + 8 * g]);
+      f32x16_t kc = mfma32_bf16(kr[0], iq0, zero16());
+      kc = mfma32_bf16(kr[2], iq1, kc);
+      *reinterpret_cast<h16x8_t*>(kp + frag_byte(kt * 4 + 2 * tt, lane)) = pack_h8<0>(kc);
+      *reinterpret_cast<h16x8_t*>(kp + frag_byte(kt * 4 + 2 * tt + 1, lane)) = pack_h8<8>(kc);
+    }
+  }
+
   if (tid < kC) {
     const int t = tid;
     // rk = 0 past the sequence end: cK and T' then clear those key tokens
@@ -379,21 +398,21 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   }
   __syncthreads();
 
-  // ---- Q' = diag(cQ) q as fp16, in B-fragment order ----
+  // ---- Q' = diag(cQ) q as fp16, in B-fragment order: this lane's keys
+  //      32 kk + 8 lg of token t are fragment (t / 32, 2 kk + lg / 2), lane
+  //      t % 32 + 32 (lg % 2) ----
   {
     uint8_t* qrec = rec + Rec::QP;
+    const int t = 16 * wave + lr;
+    const float cqv = sm.cq[t];
 #pragma unroll
-    for (int j = 0; j < NSEG1; ++j) {
-      const int e = tid + NT * j;
-      const int t = e / SEG, c8 = e % SEG;
-      const float cqv = sm.cq[t];
-      const u32x4_t x = __builtin_bit_cast(u32x4_t, qraw[j]);
+    for (int kk = 0; kk < KTD; ++kk) {
+      const u32x4_t x = __builtin_bit_cast(u32x4_t, qv[kk]);
       u32x4_t y;
 #pragma unroll
       for (int i = 0; i < 4; ++i) y[i] = f2h2(lo_half(x[i]) * cqv, hi_half(x[i]) * cqv);
-      const int frag = (t >> 5) * (D / 16) + (c8 >> 1);
-      const int ln = (t & 31) + 32 * (c8 & 1);
-      *reinterpret_cast<u32x4_t*>(qrec + (frag * 64 + ln) * 16) = y;
+      const int frag = (t >> 5) * (D / 16) + 2 * kk + (lg >> 1);
+      *reinterpret_cast<u32x4_t*>(qrec + frag_byte(frag, (t & 31) + 32 * (lg & 1))) = y;
     }
   }
 
@@ -419,8 +438,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
   }
   __syncthreads();
 
-  // ---- phase 2b: wave 0 inverts the diagonal blocks; the other waves form
-  //      A = lower_incl(scale q^.k^ e^{G_t - G_s}) and write it to the record ----
+  // ---- phase 2b: wave 0 inverts the diagonal blocks; every wave w forms the
+  //      rows 16 w .. 16 w + 15 of A = lower_incl(scale q^.k^ e^{G_t - G_s})
+  //      from the q rows it holds, and writes them to the record ----
   if (wave == 0) {
     const int bb = lane >> 4, c = lane & 15;
     const int dt = tix(bb, bb);
@@ -441,43 +461,37 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(
     }
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) sm.Tp[dt][rr][c] = x[rr];
-  } else {
-    // blocks (mt, kt): query rows 16 mt.., key tokens 32 kt.. with 32 kt <= 16 mt + 15
+  }
+  {
+    // key-token tiles ns of the 32-wide column blocks the rows touch; tiles
+    // above the diagonal are written as zeros
     uint8_t* arec = rec + Rec::AQ;
-    static_assert(NW == 4, "waves 1..3 take two A blocks each");
+    const int mt = wave;
+    const int t = 16 * mt + lr;  // the lane's query token (C column)
+    const float qscale = sm.rq[t] * scale;
+    const float Gt = sm.G[t];
+#pragma unroll 1
+    for (int ns = 0; ns <= (mt | 1); ++ns) {  // wave-uniform trip count
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      if (ns <= mt) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int b = wave - 1 + 3 * u;
-      const int mt = b < 2 ? b : 2 + ((b - 2) >> 1);
-      const int kt = b < 2 ? 0 : ((b - 2) & 1);
-      const int t = 16 * mt + lr;  // the lane's query token (C column)
-      const s16x8_t* qb = qpre[u];
-      const float qscale = sm.rq[t] * scale;
-      const float Gt = sm.G[t];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int ns = 2 * kt + half;  // key-token tile
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        if (ns <= mt) {
-#pragma unroll
-          for (int kk = 0; kk < KTD; ++kk) {
-            const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Kr[16 * ns + lr][32 * kk + 8 * lg]);
-            acc = gdn::mfma16x16x32(a8, qb[kk], acc);
-          }
+        for (int kk = 0; kk < KTD; ++kk) {
+          const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Kr[16 * ns + lr][32 * kk + 8 * lg]);
+          acc = gdn::mfma16x16x32(a8, qv[kk], acc);
         }
-        float a[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int s = 16 * ns + 4 * lg + i;
-          a[i] = (s <= t && t < len) ? acc[i] * qscale * sm.rk[s] * __expf(Gt - sm.G[s]) : 0.f;
-        }
-        // tokens 16 ns + 4 lg .. + 3 sit at the positions of quad qswap
-        const int pos = qswap(16 * ns + 4 * lg);
-        uint2 pk;
-        pk.x = f2h2(a[0], a[1]);
-        pk.y = f2h2(a[2], a[3]);
-        *reinterpret_cast<uint2*>(arec + tri_frag_byte(t, pos)) = pk;
       }
+      float a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int s = 16 * ns + 4 * lg + i;
+        a[i] = (s <= t && t < len) ? acc[i] * qscale * sm.rk[s] * __expf(Gt - sm.G[s]) : 0.f;
+      }
+      // tokens 16 ns + 4 lg .. + 3 sit at the positions of quad qswap
+      const int pos = qswap(16 * ns + 4 * lg);
+      uint2 pk;
+      pk.x = f2h2(a[0], a[1]);
+      pk.y = f2h2(a[2], a[3]);
+      *reinterpret_cast<uint2*>(arec + tri_frag_byte(t, pos)) = pk;
     }
   }
   __syncthreads();
@@ -588,16 +602,16 @@ constexpr int kStateWaves = 8;
 //   w 2, 3  output: O^T = S^T Q'^T + Vn^T A^T of token tile w - 2 (both
 //           chains' columns), one chunk behind the chain
 //   w 4, 5  U: U = T'' V for value-column tile w - 4
-//   w 6, 7  K: K^T and -W = -T' K for key tiles w - 6 (+ 2), and the
-//           record's vec block, into the stage
-// Per chunk the chain, U, output and K roles issue 32, 10, 24 and 20
+//   w 6, 7  K: the record's K^T and -W = -T' K for key tiles w - 6 (+ 2), and
+//           the record's vec block, into the stage
+// Per chunk the chain, U, output and K roles issue 32, 10, 24 and 12
 // matrix-core products of 32x32x16.
 
 // Per-lane prefetch registers of one chunk, one struct per role.
 template <int D>
 struct KPrefetch {
   static constexpr int NKT = D / 64;  // key tiles per K wave: pk, pk + 2
-  s16x8_t k[NKT][2][2];               // raw K rows: key tile pk + 2u, token tile tt, 16-key step h
+  s16x8_t k[NKT][4];                  // K^T fragments: key tile pk + 2u, token step
   s16x8_t tw[6];                      // -T' fragments
   s16x8_t vec;                        // the lane's 16 bytes of the record vec block
 };
@@ -627,24 +641,16 @@ __device__ __forceinline__ s16x8_t buf_ld(__amdgpu_buffer_rsrc_t r, int voff, in
 
 // The prefetches issue the loads of one chunk for this lane.  Nothing here
 // consumes a loaded value, so the loads stay in flight until staging.
-// K rows past the sequence end re-read its last token: those tokens carry
-// zero weights in T' and cK.  Rows and the vec block, then the -T' fragments.
+// K^T fragments and the vec block, then the -T' fragments.
 template <int D>
-__device__ __forceinline__ void k_prefetch_rows(KPrefetch<D>& p, const uint16_t* kh, int sk, const uint8_t* rec,
-                                                int64_t tok0, int len, int pk, int lane) {
-  const int li = lane & 31, g = lane >> 5;
-  const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kh + tok0 * sk);
+__device__ __forceinline__ void k_prefetch_kt(KPrefetch<D>& p, const uint8_t* rec, int pk, int lane) {
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
+  const int kt0 = static_cast<int>(rec_kt(D));
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int row = min(32 * tt + li, len - 1);
+  for (int u = 0; u < KPrefetch<D>::NKT; ++u)
 #pragma unroll
-    for (int u = 0; u < KPrefetch<D>::NKT; ++u) {
-      const int off = 2 * (row * sk + 32 * (pk + 2 * u) + 8 * g);
-      p.k[u][tt][0] = buf_ld(rk, off, 0);
-      p.k[u][tt][1] = buf_ld(rk, off, 32);
-    }
-  }
-  p.vec = buf_ld(buf_rsrc(rec), 16 * lane, Rec::VEC);
+    for (int ks = 0; ks < 4; ++ks) p.k[u][ks] = buf_ld(r, 16 * lane, kt0 + 1024 * ((pk + 2 * u) * 4 + ks));
+  p.vec = buf_ld(r, 16 * lane, Rec::VEC);
 }
 
 template <int D>
@@ -683,55 +689,32 @@ __device__ __forceinline__ void o_prefetch(OPrefetch<D>& p, const uint8_t* rec, 
 }
 
 // K waves: K^T and -W of key tiles pk (+ 2) into the stage, as fragments.
-//  * K^T of a key tile by a bf16 identity product C = K I with the identity's
-//    columns qswap-ordered: lane (position n, g) of C holds key
-//    qswap(32 kt + n) at tokens 8i + 4g + r, i.e. at token positions
-//    8g + 0..7 (elements 0..7) and 16 + 8g + 0..7 (elements 8..15); the
-//    product is exact.
-//  * -W^T = K^T (-T')^T from those registers (as fp16 A fragments): lane
-//    (token t, g) of its C tiles holds keys 32 kt + 8g + 0..7 and
-//    32 kt + 16 + 8g + 0..7, the -W fragments of key steps 2 kt, 2 kt + 1.
-//  * The fp16 K^T fragments are also the state update's A operand.
+// -W^T = K^T (-T')^T with the record's fp16 K^T fragments as A operands: lane
+// (token t, g) of its C tiles holds keys 32 kt + 8g + 0..7 and
+// 32 kt + 16 + 8g + 0..7, the -W fragments of key steps 2 kt, 2 kt + 1.  The
+// K^T fragments themselves are the state update's A operands.
 template <int D>
-__device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int pk, int lane, const uint16_t* kh,
-                                        int sk, const uint8_t* next_rec, int64_t next_tok0, int next_len) {
+__device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int pk, int lane,
+                                        const uint8_t* next_rec) {
   constexpr int KS = D / 16;
   constexpr int NKT = KPrefetch<D>::NKT;
-  const int li = lane & 31, g = lane >> 5;
   *reinterpret_cast<s16x8_t*>(reinterpret_cast<uint8_t*>(S.vec) + 16 * lane) = p.vec;
-  // K^T of both key tiles first: four independent product chains
-  const s16x8_t iq0 = ident_frag(0, qswap(li), g), iq1 = ident_frag(1, qswap(li), g);
-  f32x16_t kc[NKT][2];
-#pragma unroll
-  for (int u = 0; u < NKT; ++u)
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) kc[u][tt] = mfma32_bf16(p.k[u][tt][0], iq0, zero16());
-#pragma unroll
-  for (int u = 0; u < NKT; ++u)
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) kc[u][tt] = mfma32_bf16(p.k[u][tt][1], iq1, kc[u][tt]);
-  // The next chunk's K rows and vec block go out as soon as these are read,
-  // its -T' fragments once the products below have read them: a single set
-  // of registers then carries a whole iteration's worth of loads.
-  k_prefetch_rows<D>(p, kh, sk, next_rec, next_tok0, next_len, pk, lane);
-  gdn::keep_loads_here();
   f32x16_t cw[NKT][2];
 #pragma unroll
   for (int u = 0; u < NKT; ++u) {
-    h16x8_t ka[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) ka[ks] = (ks & 1) ? pack_h8<8>(kc[u][ks >> 1]) : pack_h8<0>(kc[u][ks >> 1]);
-    // the same fragments are the state update's K^T (rows in position order)
     const int kt = pk + 2 * u;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) S.Kt[kt * 4 + ks][lane] = ka[ks];
-    cw[u][0] = mfma32(ka[0], as_h8(p.tw[0]), zero16());
-    cw[u][1] = mfma32(ka[0], as_h8(p.tw[2]), zero16());
-    cw[u][0] = mfma32(ka[1], as_h8(p.tw[1]), cw[u][0]);
-    cw[u][1] = mfma32(ka[1], as_h8(p.tw[3]), cw[u][1]);
-    cw[u][1] = mfma32(ka[2], as_h8(p.tw[4]), cw[u][1]);
-    cw[u][1] = mfma32(ka[3], as_h8(p.tw[5]), cw[u][1]);
+    for (int ks = 0; ks < 4; ++ks) S.Kt[kt * 4 + ks][lane] = as_h8(p.k[u][ks]);
+    cw[u][0] = mfma32(as_h8(p.k[u][0]), as_h8(p.tw[0]), zero16());
+    cw[u][1] = mfma32(as_h8(p.k[u][0]), as_h8(p.tw[2]), zero16());
+    cw[u][0] = mfma32(as_h8(p.k[u][1]), as_h8(p.tw[1]), cw[u][0]);
+    cw[u][1] = mfma32(as_h8(p.k[u][1]), as_h8(p.tw[3]), cw[u][1]);
+    cw[u][1] = mfma32(as_h8(p.k[u][2]), as_h8(p.tw[4]), cw[u][1]);
+    cw[u][1] = mfma32(as_h8(p.k[u][3]), as_h8(p.tw[5]), cw[u][1]);
   }
+  // The next chunk's loads go out as soon as these registers are read: a
+  // single set of registers then carries a whole iteration's worth of loads.
+  k_prefetch_kt<D>(p, next_rec, pk, lane);
   k_prefetch_tw<D>(p, next_rec, lane);
   gdn::keep_loads_here();
 #pragma unroll
@@ -847,9 +830,9 @@ __device__ __forceinline__ void o_chunk(const OPrefetch<D>& p, const StateXchg<D
 // reads what another wave wrote before the barrier that separates them.
 template <int D>
 __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
-    const uint16_t* __restrict__ k, int64_t sk, const uint16_t* __restrict__ v, int64_t sv,
-    const uint8_t* __restrict__ ws, const float* h0, float* hT, const int64_t* __restrict__ ids, int64_t sstride,
-    const int64_t* __restrict__ cu, int n_seqs, int Hk, int Hv, uint16_t* __restrict__ o) {
+    const uint16_t* __restrict__ v, int64_t sv, const uint8_t* __restrict__ ws, const float* h0, float* hT,
+    const int64_t* __restrict__ ids, int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hv,
+    uint16_t* __restrict__ o) {
   constexpr int NCB = D / kCB;
   constexpr int NR = D / 32;  // 32-row tiles of the state
   constexpr int KS = D / 16;  // k-steps over keys
@@ -864,7 +847,6 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   const int64_t bos = cu[r];
   const int64_t seqlen = cu[r + 1] - bos;
   const int64_t nch = chunks_of(seqlen);
-  const int kh = h / (Hv / Hk);
 
   // first workspace chunk of this sequence: sum of earlier sequences' chunks
   if (threadIdx.x < 64) {
@@ -968,12 +950,9 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
         // One register set: each stage issues the next chunk's loads as soon
         // as it has read the registers they land in.
         const int pk = wave - 6;
-        const uint16_t* khp = k + static_cast<int64_t>(kh) * D;
-        const int ski = static_cast<int>(sk);
-#define GDN_KSTAGE(jc, jn)                                                                          \
-  k_stage<D>(p, sm.st[(jc) & 1], pk, lane, khp, ski, rec0 + (jn) * rec_stride, bos + (jn) * kC, GDN_LEN(jn))
+#define GDN_KSTAGE(jc, jn) k_stage<D>(p, sm.st[(jc) & 1], pk, lane, rec0 + (jn) * rec_stride)
         KPrefetch<D> p;
-        k_prefetch_rows<D>(p, khp, ski, rec0, bos, GDN_LEN(0), pk, lane);
+        k_prefetch_kt<D>(p, rec0, pk, lane);
         k_prefetch_tw<D>(p, rec0, lane);
         gdn::keep_loads_here();
         GDN_KSTAGE(0, min<int64_t>(1, nch - 1));
@@ -1122,7 +1101,7 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv * (D / kCB);
   const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
   chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
-      k, sk, v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hk, Hv, o);
+      v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o);
   return gdn_launch_status();
 }
 
