@@ -114,12 +114,13 @@ int gdn_conv_padded(const uint16_t* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
  *   l2norm != 0: q, k rows are L2-normalised in fp32 (eps 1e-6) first.
  *   workspace: device buffer of at least gdn_chunk_prefill_workspace_size()
  *         bytes, 256-byte aligned, owned by the caller.  It receives one
- *         19 KiB record per (chunk, value head) from the first launch;
- *         contents need no initialisation and are dead after the call.
+ *         record of 19 KiB + 256 D bytes per (chunk, value head) from the
+ *         first launch; contents need no initialisation and are dead after
+ *         the call.
  * D must be 64 or 128.  Two launches on `stream`: a prep kernel over all
- * chunks in parallel (row norms, K K^T, Q K^T, the triangular inverse), then
- * a state kernel per (sequence, value head, 64 value columns) that walks the
- * chunks in order with its state slice in registers (fp16 matrix-core
+ * chunks in parallel (row norms, K^T, K K^T, Q K^T, the triangular inverse),
+ * then a state kernel per (sequence, value head, 64 value columns) that walks
+ * the chunks in order with its state slice in registers (fp16 matrix-core
  * operands, fp32 accumulation and state).
  */
 int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k, int64_t sk_tok,
