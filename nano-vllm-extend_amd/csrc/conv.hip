@@ -38,14 +38,14 @@ __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
   *reinterpret_cast<uint4*>(p) = u;
 }
 
-// y = acc * sigmoid(acc), the reference epilogue's form: the library expf,
-// and 1 / (1 + e) as the hardware reciprocal refined by one Newton step
-// (within an ulp of the divide, a fraction of the divide's instructions).
-// The exponent is capped at 88 so 1 + e stays finite (the Newton step would
-// turn an infinite e into NaN); below acc = -88 y is then ~ -5e-37 where the
-// divide gives -0, both far under any bf16 output step of interest.
+// y = acc * sigmoid(acc), the reference epilogue's form: e^-acc within a few
+// ulp (exp_acc), and 1 / (1 + e) as the hardware reciprocal refined by one
+// Newton step (within an ulp of the divide, a fraction of the divide's
+// instructions).  The exponent is capped at 88 so 1 + e stays finite (the
+// Newton step would turn an infinite e into NaN); below acc = -88 y is then
+// ~ -5e-37 where the divide gives -0, both far under any bf16 output step.
 __device__ __forceinline__ float silu_mul(float acc) {
-  const float d = 1.0f + expf(fminf(-acc, 88.0f));
+  const float d = 1.0f + gdn::exp_acc(fminf(-acc, 88.0f));
   float r = __builtin_amdgcn_rcpf(d);
   r = fmaf(r, fmaf(-d, r, 1.0f), r);
   return acc * r;
