@@ -138,7 +138,6 @@ __global__ __launch_bounds__(256) void conv_varlen_kernel(
 
   // window: win[0..2] = inputs at t-3, t-2, t-1
   float win[3][8];
-  uint16_t old_state[8][kK - 1];
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
     const int64_t p = t_beg - 3 + j;
@@ -153,12 +152,6 @@ __global__ __launch_bounds__(256) void conv_varlen_kernel(
         win[j][i] = gdn::bf2f(b);
       }
     }
-  }
-  if (owns_state) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < kK - 1; ++j) old_state[i][j] = st[static_cast<int64_t>(i) * ss_ch + j];
   }
 
   const int part = c0 < key_dim ? 0 : (c0 < 2 * key_dim ? 1 : 2);
@@ -196,7 +189,7 @@ __global__ __launch_bounds__(256) void conv_varlen_kernel(
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          st[static_cast<int64_t>(i) * ss_ch + j] = roll_value(old_state[i][p + (kK - 1)]);
+          st[static_cast<int64_t>(i) * ss_ch + j] = roll_value(st[static_cast<int64_t>(i) * ss_ch + p + (kK - 1)]);
       }
     }
   }
