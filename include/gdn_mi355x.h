@@ -135,6 +135,39 @@ int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k, int6
 int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
 
 /*
+ * Fused varlen prefill of the layer core's first three steps: gates, causal
+ * conv1d + SiLU with the conv-state roll, and the chunked gated delta rule.
+ * Replaces the sequence fused_g_beta (nanovllm/models/qwen3_5.py:934) ->
+ * causal_conv_silu_varlen (:942-947) -> chunk_gated_delta_rule (:956-961) of
+ * _gdn_prefill_varlen (:922-965), with the same results as the three entry
+ * points above called in that order (gdn_g_beta, gdn_conv_varlen with
+ * key_dim = Hk*D, gdn_chunk_prefill with l2norm), bit for bit.
+ *   x      [N, C] bf16 raw q | k | v rows, C = 2*Hk*D + Hv*D, row stride
+ *          sx_row (a multiple of 8), channel stride 1, 16-byte aligned
+ *   conv_state, ss_seq, ss_ch, conv_w: as gdn_conv_varlen with K = 4; the
+ *          pool row of sequence r is state_ids[r] (r if NULL), the same row
+ *          as the recurrent state's
+ *   b, a   [N, Hv] bf16 contiguous; A_log, dt_bias [Hv] (param_is_fp32 as
+ *          gdn_g_beta; no padding mask)
+ *   h0, hT, state_ids, state_stride, cu_seqlens, scale, l2norm, o: as
+ *          gdn_chunk_prefill
+ *   workspace: at least gdn_conv_chunk_prefill_workspace_size() bytes,
+ *          256-byte aligned (the chunk records, then the conv's v rows)
+ * Two launches, as gdn_chunk_prefill: the prep kernel also runs the conv and
+ * the gates of its chunk; the state kernel also rolls the conv states.
+ */
+int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_state, int64_t ss_seq,
+                           int64_t ss_ch, const uint16_t* conv_w, const uint16_t* b, const uint16_t* a,
+                           const void* A_log, const void* dt_bias, int param_is_fp32, const float* h0,
+                           float* hT, const int64_t* state_ids, int64_t state_stride,
+                           const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv, int D,
+                           float scale, int l2norm, uint16_t* o, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of gdn_conv_chunk_prefill; -1 on bad args. */
+int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
+
+/*
  * Recurrent gated delta rule for decode: T >= 1 tokens per sequence, state
  * read once and written once.  Replaces recurrent_gdn_inplace /
  * _recurrent_inplace_kernel (nanovllm/models/qwen3_5.py:561-613, T = 1, in

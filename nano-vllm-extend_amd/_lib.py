@@ -44,6 +44,9 @@ SIGNATURES: dict[str, list] = {
     "gdn_chunk_prefill": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _p, _i32, _i64,
                           _i32, _i32, _i32, _f32, _i32, _p, _p, _i64, _p],
     "gdn_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],
+    "gdn_conv_chunk_prefill": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i64, _p,
+                               _i32, _i64, _i32, _i32, _i32, _f32, _i32, _p, _p, _i64, _p],
+    "gdn_conv_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],
     "gdn_recurrent": [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
                       _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     "gdn_state_commit": [_p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _p],
@@ -51,7 +54,8 @@ SIGNATURES: dict[str, list] = {
 }
 
 # entry points whose return type is not int (status)
-RESTYPES = {"gdn_chunk_prefill_workspace_size": ctypes.c_int64}
+RESTYPES = {"gdn_chunk_prefill_workspace_size": ctypes.c_int64,
+            "gdn_conv_chunk_prefill_workspace_size": ctypes.c_int64}
 
 _LIB: ctypes.CDLL | None = None
 

@@ -265,13 +265,119 @@ __device__ __forceinline__ float4 t_quad(const float (*Tp)[16][kTileLd], const f
 // quad index (4 tokens) of the tokens at positions [4P, 4P + 4)
 __device__ __forceinline__ int quad_of_pos(int P) { return qswap(4 * P) >> 2; }
 
+// Inputs of the fused variant (conv1d + SiLU and the gates computed in the
+// prep kernel from the layer's raw inputs).
+struct ConvIn {
+  const uint16_t* x;       // [N, C] raw q | k | v rows, row stride sx; C = 2 key_dim + Hv D
+  int64_t sx;
+  const uint16_t* cstate;  // conv state pool: row `slot`, channel c, tap j at
+  int64_t ss_seq, ss_ch;   //   cstate + slot*ss_seq + c*ss_ch + j (read here only)
+  const int64_t* ids;      // pool rows per sequence (NULL: the sequence index)
+  const uint16_t* w;       // [C, 4] conv taps
+  int key_dim;             // Hk * D
+  uint16_t* vout;          // [N, Hv, D] conv output of the v channels
+  const uint16_t* a;       // [N, Hv] gate inputs
+  const uint16_t* b;
+  const void* A_log;       // [Hv], bf16 or fp32 (param_f32)
+  const void* dt_bias;
+  int param_f32;
+};
+
+// Fused variant, phase 1: causal conv (width 4) + SiLU of the chunk's q, k and
+// v rows.  Each output row needs the 3 raw rows before it: inside the chunk
+// and the previous chunk they are rows of x, before a sequence's first token
+// they are the conv state's taps.  Thread (16-byte channel segment c8, rows
+// t0 .. t0 + RPT - 1) loads its RPT + 3 raw rows once per part and writes
+// q -> Qc and k -> Kr (bf16 rows in LDS, zero past the sequence end), the k
+// rows' sums of squares -> ssk (in the plain path's summation order), and
+// v -> vout (rows of this sequence only).
+template <int D>
+__device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)[D + 8], uint16_t (*Kr)[D + 8],
+                                                float* ssk, int64_t tok0, int len, bool first, int r, int kh,
+                                                int h, int Hv, int tid) {
+  constexpr int SEG = D / 8;
+  constexpr int RPT = kC * SEG / 256;  // rows per thread
+  const int c8 = tid % SEG, t0 = RPT * (tid / SEG);
+  const int64_t slot = cv.ids ? cv.ids[r] : r;
+#pragma unroll
+  for (int part = 0; part < 3; ++part) {
+    const int ch = (part == 0 ? kh * D : part == 1 ? cv.key_dim + kh * D : 2 * cv.key_dim + h * D) + 8 * c8;
+    float wk[8][4];
+    {
+      const uint4* wp = reinterpret_cast<const uint4*>(cv.w + static_cast<int64_t>(ch) * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 u = wp[j];
+        const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          wk[2 * j + e / 2][2 * (e & 1)] = lo_half(uu[e]);
+          wk[2 * j + e / 2][2 * (e & 1) + 1] = hi_half(uu[e]);
+        }
+      }
+    }
+    float xw[RPT + 3][8];
+#pragma unroll
+    for (int i = 0; i < RPT + 3; ++i) {
+      const int t = t0 - 3 + i;
+      if (t >= 0 || !first) {
+        // rows past the sequence end re-read its last row (outputs dropped)
+        const uint4 u = *reinterpret_cast<const uint4*>(cv.x + (tok0 + min(t, len - 1)) * cv.sx + ch);
+        const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xw[i][2 * e] = lo_half(uu[e]);
+          xw[i][2 * e + 1] = hi_half(uu[e]);
+        }
+      } else {
+        const uint16_t* sp = cv.cstate + slot * cv.ss_seq + static_cast<int64_t>(ch) * cv.ss_ch + (t + 3);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xw[i][e] = gdn::bf2f(sp[static_cast<int64_t>(e) * cv.ss_ch]);
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPT; ++rr) {
+      const int t = t0 + rr;
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = gdn::conv4_silu(xw[rr][e], xw[rr + 1][e], xw[rr + 2][e], xw[rr + 3][e], wk[e]);
+      u32x4_t out;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] = gdn::f2bf2(y[2 * e], y[2 * e + 1]);
+      if (part == 2) {
+        if (t < len) *reinterpret_cast<u32x4_t*>(cv.vout + ((tok0 + t) * Hv + h) * D + 8 * c8) = out;
+        continue;
+      }
+      if (t >= len) out = u32x4_t{0u, 0u, 0u, 0u};
+      if (part == 0) {
+        *reinterpret_cast<u32x4_t*>(&Qc[t][8 * c8]) = out;
+      } else {
+        *reinterpret_cast<u32x4_t*>(&Kr[t][8 * c8]) = out;
+        const s16x8_t kv8 = __builtin_bit_cast(s16x8_t, out);
+        float ks = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
+          ks += kf * kf;
+        }
+#pragma unroll
+        for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
+        if (c8 == 0) ssk[t] = ks;
+      }
+    }
+  }
+}
+
 // grid = 8 * ceil(nc_bound * Hv / 8); block = 256.  One workgroup per
 // (chunk, value head); writes the chunk's record.
-template <int D>
+// kConv: q, k, v are the conv1d + SiLU of cv.x and g, beta the gates of
+// cv.a, cv.b, all computed here (q, k, g, beta unused); v goes to cv.vout.
+template <int D, bool kConv>
 __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
     const float* __restrict__ g, const uint16_t* __restrict__ beta, const int64_t* __restrict__ cu,
-    int n_seqs, int64_t nc_bound, int Hk, int Hv, float scale, int l2norm, uint8_t* __restrict__ ws) {
+    int n_seqs, int64_t nc_bound, int Hk, int Hv, float scale, int l2norm, uint8_t* __restrict__ ws,
+    ConvIn cv) {
   constexpr int NW = 4;
   constexpr int NT = 64 * NW;
   constexpr int KTD = D / 32;
@@ -301,18 +407,24 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // ---- phase 1: K rows, row norms of K and Q, gates ----
-  // q is read once, straight into the layout in which it serves as the A
-  // blocks' B operand: wave w holds query rows 16 w + lr, keys 32 kk + 8 lg.
-  // The same registers become Q' once cQ is known.
+  // q is held straight in the layout in which it serves as the A blocks' B
+  // operand: wave w holds query rows 16 w + lr, keys 32 kk + 8 lg.  The same
+  // registers become Q' once cQ is known.  The fused variant first runs the
+  // conv into LDS (q rows in the L / T tiles' space, free until phase 2a).
+  uint16_t (*Qc)[D + 8] = reinterpret_cast<uint16_t (*)[D + 8]>(&sm.Lp[0][0][0]);
+  static_assert(sizeof(sm.Lp) + sizeof(sm.Tp) >= sizeof(uint16_t) * kC * (D + 8), "conv q rows fit L and T");
   s16x8_t qv[KTD];
-  {
+  auto q_rows = [&]() {
     const int t = 16 * wave + lr;
-    const uint16_t* qr = qh + (tok0 + min(t, len - 1)) * sq + 8 * lg;
     float qs = 0.f;
 #pragma unroll
     for (int kk = 0; kk < KTD; ++kk) {
-      qv[kk] = *reinterpret_cast<const s16x8_t*>(qr + 32 * kk);
-      if (t >= len) qv[kk] = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      if constexpr (kConv) {
+        qv[kk] = *reinterpret_cast<const s16x8_t*>(&Qc[t][32 * kk + 8 * lg]);
+      } else {
+        qv[kk] = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, len - 1)) * sq + 8 * lg + 32 * kk);
+        if (t >= len) qv[kk] = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float qf = gdn::bf2f(static_cast<uint16_t>(qv[kk][i]));
@@ -322,31 +434,42 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     qs += __shfl_xor(qs, 16, 64);
     qs += __shfl_xor(qs, 32, 64);
     if (lg == 0) sm.ssq[t] = qs;
-  }
+  };
+  if constexpr (!kConv) q_rows();
+  if constexpr (kConv) {
+    conv_chunk_rows<D>(cv, Qc, sm.Kr, sm.ssk, tok0, len, jc == 0, r, kh, h, Hv, tid);
+  } else {
 #pragma unroll
-  for (int j = 0; j < NSEG1; ++j) {
-    const int e = tid + NT * j;
-    const int t = e / SEG, c8 = e % SEG;
-    const int64_t row = tok0 + min(t, len - 1);
-    s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + row * sk + c8 * 8);
-    if (t >= len) kv8 = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-    *reinterpret_cast<s16x8_t*>(&sm.Kr[t][c8 * 8]) = kv8;
-    float ks = 0.f;
+    for (int j = 0; j < NSEG1; ++j) {
+      const int e = tid + NT * j;
+      const int t = e / SEG, c8 = e % SEG;
+      const int64_t row = tok0 + min(t, len - 1);
+      s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + row * sk + c8 * 8);
+      if (t >= len) kv8 = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      *reinterpret_cast<s16x8_t*>(&sm.Kr[t][c8 * 8]) = kv8;
+      float ks = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
-      ks += kf * kf;
+      for (int i = 0; i < 8; ++i) {
+        const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
+        ks += kf * kf;
+      }
+#pragma unroll
+      for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
+      if (c8 == 0) sm.ssk[t] = ks;
     }
-#pragma unroll
-    for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
-    if (c8 == 0) sm.ssk[t] = ks;
   }
   if (wave == 0) {
     float gv = 0.f, bv = 0.f;
     if (lane < len) {
       const int64_t gi = (tok0 + lane) * Hv + h;
-      gv = g[gi];
-      bv = gdn::bf2f(beta[gi]);
+      if constexpr (kConv) {
+        gv = gdn::gate_g(gdn::bf2f(cv.a[gi]), gdn::load_param(cv.A_log, h, cv.param_f32),
+                         gdn::load_param(cv.dt_bias, h, cv.param_f32));
+        bv = gdn::bf2f(gdn::gate_beta(gdn::bf2f(cv.b[gi])));
+      } else {
+        gv = g[gi];
+        bv = gdn::bf2f(beta[gi]);
+      }
     }
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -355,6 +478,10 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     }
     sm.G[lane] = gv;
     sm.bt[lane] = bv;
+  }
+  if constexpr (kConv) {
+    __syncthreads();  // the conv's q rows are in LDS
+    q_rows();
   }
   __syncthreads();
 
@@ -822,6 +949,45 @@ __device__ __forceinline__ void o_chunk(const OPrefetch<D>& p, const StateXchg<D
   wave_sync();  // the tile is read before the next chunk's writes
 }
 
+// Conv-state roll of the fused variant, done here because the prep kernel
+// reads the old state from every chunk-0 workgroup of a sequence (the value
+// heads that share a key head included), and this kernel runs after all of
+// them.  Workgroup (sequence r, value head h, column block cb) rolls its 64 v
+// channels, and the q and k channels of its columns when h is the first value
+// head of its key head: state taps j = 0..2 <- the raw inputs at positions
+// T - 3 + j (old taps T + j where that is negative), as the standalone conv
+// kernel does.
+struct ConvRoll {
+  const uint16_t* x;  // [N, C] raw rows, row stride sx (NULL: not fused, no roll)
+  int64_t sx;
+  uint16_t* cstate;
+  int64_t ss_seq, ss_ch;
+  int key_dim;
+  int ratio;  // Hv / Hk
+};
+
+template <int D>
+__device__ __forceinline__ void conv_roll(const ConvRoll& cr, int64_t slot, int64_t bos, int64_t T, int h, int cb,
+                                          int i0, int nthreads) {
+  const bool qk = h % cr.ratio == 0;
+  const int kh = h / cr.ratio;
+  const int ntask = (qk ? 3 : 1) * kCB;
+  for (int task = i0; task < ntask; task += nthreads) {
+    const int part = qk ? task / kCB : 2;
+    const int ch = (part == 0 ? kh * D : part == 1 ? cr.key_dim + kh * D : 2 * cr.key_dim + h * D) + cb * kCB +
+                   task % kCB;
+    uint16_t* st = cr.cstate + slot * cr.ss_seq + static_cast<int64_t>(ch) * cr.ss_ch;
+    uint16_t val[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int64_t p = T - 3 + j;
+      val[j] = p >= 0 ? cr.x[(bos + p) * cr.sx + ch] : st[p + 3];
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) st[j] = gdn::roll_value(val[j]);
+  }
+}
+
 // grid = 8 * ceil(n_seqs * Hv * NCB / 8), NCB = D / 64; block = 64 * 8.
 // Workgroup (sequence r, value head h, column block cb) owns state columns
 // cb*64 .. cb*64 + 63.  One workgroup barrier per chunk j: before it the
@@ -832,7 +998,7 @@ template <int D>
 __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     const uint16_t* __restrict__ v, int64_t sv, const uint8_t* __restrict__ ws, const float* h0, float* hT,
     const int64_t* __restrict__ ids, int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hv,
-    uint16_t* __restrict__ o) {
+    uint16_t* __restrict__ o, ConvRoll cr) {
   constexpr int NCB = D / kCB;
   constexpr int NR = D / 32;  // 32-row tiles of the state
   constexpr int KS = D / 16;  // k-steps over keys
@@ -867,6 +1033,8 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 
 #define GDN_LEN(j_) static_cast<int>(min<int64_t>(kC, seqlen - (j_) * kC))
   if (wave >= 2) {
+    // the output waves have two chunk steps before their first product
+    if (cr.x && wave < 4) conv_roll<D>(cr, ids ? ids[r] : r, bos, seqlen, h, cb, threadIdx.x - 128, 128);
     if (nch == 0) return;
     if (wave < 4) {
       // ------------------------------------------------------------ output --
@@ -1091,17 +1259,25 @@ template <int D>
 int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, const uint16_t* v,
                  int64_t sv, const float* g, const uint16_t* beta, const float* h0, float* hT,
                  const int64_t* ids, int64_t sstride, const int64_t* cu, int n_seqs, int64_t nc_bound,
-                 int Hk, int Hv, float scale, int l2norm, uint16_t* o, uint8_t* ws, hipStream_t stream) {
+                 int Hk, int Hv, float scale, int l2norm, uint16_t* o, uint8_t* ws, const ConvIn* cv,
+                 hipStream_t stream) {
   const int64_t lwork = nc_bound * Hv;
   const int64_t lgrid = gdn::kNumXcd * ((lwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  chunk_prep_kernel<D><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
-      q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws);
+  ConvRoll cr{};
+  if (cv) {
+    chunk_prep_kernel<D, true><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
+        q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, *cv);
+    cr = ConvRoll{cv->x, cv->sx, const_cast<uint16_t*>(cv->cstate), cv->ss_seq, cv->ss_ch, cv->key_dim, Hv / Hk};
+  } else {
+    chunk_prep_kernel<D, false><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
+        q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, ConvIn{});
+  }
   const int st = gdn_launch_status();
   if (st != GDN_OK) return st;
   const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv * (D / kCB);
   const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
   chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
-      v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o);
+      v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr);
   return gdn_launch_status();
 }
 
@@ -1140,7 +1316,51 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   if (D == 128)
     return launch_chunk<128>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
-                             cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, s);
+                             cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, nullptr, s);
   return launch_chunk<64>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
-                          cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, s);
+                          cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, nullptr, s);
+}
+
+// workspace of the fused entry point: the records, then the conv's v rows
+static int64_t fused_v_offset(int64_t nc_bound, int Hv, int D) { return nc_bound * Hv * rec_bytes(D); }
+
+extern "C" int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D) {
+  if (N < 0 || n_seqs < 0 || Hv <= 0 || (D != 64 && D != 128)) return -1;
+  const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
+  return fused_v_offset(nc_bound, Hv, D) + ((N * Hv * D * 2 + 255) / 256) * 256;
+}
+
+extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_state,
+                                      int64_t ss_seq, int64_t ss_ch, const uint16_t* conv_w,
+                                      const uint16_t* b, const uint16_t* a, const void* A_log,
+                                      const void* dt_bias, int param_is_fp32, const float* h0, float* hT,
+                                      const int64_t* state_ids, int64_t state_stride,
+                                      const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv,
+                                      int D, float scale, int l2norm, uint16_t* o, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (n_seqs < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
+  if (n_seqs == 0) return GDN_OK;
+  if (!x || !conv_state || !conv_w || !a || !b || !A_log || !dt_bias || !cu_seqlens || !o || !workspace)
+    return GDN_ERR_INVALID_ARG;
+  const int64_t C = 2LL * Hk * D + static_cast<int64_t>(Hv) * D;
+  // 16-byte row segments of x, 8-byte output pieces, 256-byte workspace records
+  if (sx_row % 8 || sx_row < C || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(conv_w) % 16 || reinterpret_cast<uintptr_t>(o) % 8 ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 || ss_ch < 3 || ss_seq < C * ss_ch ||
+      ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
+    return GDN_ERR_INVALID_ARG;
+  const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
+  if (workspace_bytes < gdn_conv_chunk_prefill_workspace_size(N, n_seqs, Hv, D)) return GDN_ERR_INVALID_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint16_t* vws = reinterpret_cast<uint16_t*>(ws + fused_v_offset(nc_bound, Hv, D));
+  const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, conv_w, Hk * D, vws, a, b, A_log, dt_bias,
+                  param_is_fp32 ? 1 : 0};
+  const int64_t sv = static_cast<int64_t>(Hv) * D;
+  if (D == 128)
+    return launch_chunk<128>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
+                             cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, &cv, s);
+  return launch_chunk<64>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
+                          cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, &cv, s);
 }

@@ -38,24 +38,8 @@ __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
   *reinterpret_cast<uint4*>(p) = u;
 }
 
-// y = acc * sigmoid(acc), the reference epilogue's form: e^-acc within a few
-// ulp (exp_acc), and 1 / (1 + e) as the hardware reciprocal refined by one
-// Newton step (within an ulp of the divide, a fraction of the divide's
-// instructions).  The exponent is capped at 88 so 1 + e stays finite (the
-// Newton step would turn an infinite e into NaN); below acc = -88 y is then
-// ~ -5e-37 where the divide gives -0, both far under any bf16 output step.
-__device__ __forceinline__ float silu_mul(float acc) {
-  const float d = 1.0f + gdn::exp_acc(fminf(-acc, 88.0f));
-  float r = __builtin_amdgcn_rcpf(d);
-  r = fmaf(r, fmaf(-d, r, 1.0f), r);
-  return acc * r;
-}
-
-// The reference writes the rolled state as (x + s) with the other operand
-// masked to zero, which maps -0.0 to +0.0 and is otherwise a bit copy.
-__device__ __forceinline__ uint16_t roll_value(uint16_t bits) {
-  return bits == 0x8000u ? static_cast<uint16_t>(0) : bits;
-}
+using gdn::roll_value;
+using gdn::silu_acc;
 
 // Finds the (sequence, tile) of flat tile index `tile` given per-sequence
 // token counts.  Every sequence owns max(1, ceil(len/64)) tiles (a sequence
@@ -164,11 +148,7 @@ __global__ __launch_bounds__(256) void conv_varlen_kernel(
     float out[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float acc = win[0][i] * wk[i][0];
-      acc += win[1][i] * wk[i][1];
-      acc += win[2][i] * wk[i][2];
-      acc += cur.v[i] * wk[i][3];
-      out[i] = silu_mul(acc);
+      out[i] = gdn::conv4_silu(win[0][i], win[1][i], win[2][i], cur.v[i], wk[i]);
       win[0][i] = win[1][i];
       win[1][i] = win[2][i];
       win[2][i] = cur.v[i];
@@ -243,7 +223,7 @@ __global__ __launch_bounds__(256) void conv_decode_kernel(
     float acc = gdn::bf2f(xs[i]) * gdn::bf2f(wr[i * kK + 3]);
 #pragma unroll
     for (int j = 0; j < 3; ++j) acc += gdn::bf2f(s[i][j]) * gdn::bf2f(wr[i * kK + j]);
-    ys[i] = gdn::f2bf(silu_mul(acc));
+    ys[i] = gdn::f2bf(silu_acc(acc));
   }
   *reinterpret_cast<uint4*>(y + b * sy_row + c0) = yu;
   // roll: s0 <- s1, s1 <- s2, s2 <- x (bit copies)
@@ -308,7 +288,7 @@ __global__ __launch_bounds__(256) void conv_padded_kernel(
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < kK; ++i) acc += tile[c][tl + i] * gdn::bf2f(wp[i]);
-    y[(static_cast<int64_t>(n) * C + cc) * T + t] = gdn::f2bf(silu_mul(acc));
+    y[(static_cast<int64_t>(n) * C + cc) * T + t] = gdn::f2bf(silu_acc(acc));
   }
   // state writeback by the first token tile (the only reader of the old state)
   if (blockIdx.x == 0) {

@@ -29,14 +29,12 @@ __global__ __launch_bounds__(256) void g_beta_kernel(const uint16_t* __restrict_
   const float bv = gdn::bf2f(b[i]);
   const float al = load_param<kParamF32>(A_log, h);
   const float dt = load_param<kParamF32>(dt_bias, h);
-  const float z = av + dt;
-  const float sp = z > 20.0f ? z : logf(1.0f + expf(z));
-  float gv = -expf(al) * sp;
+  float gv = gdn::gate_g(av, al, dt);
   if constexpr (kHasMask) {
     if (mask[i / Hv] == 0) gv = 0.0f;
   }
   g[i] = gv;
-  beta[i] = gdn::f2bf(1.0f / (1.0f + expf(-bv)));
+  beta[i] = gdn::gate_beta(bv);
 }
 
 }  // namespace

@@ -57,6 +57,52 @@ __device__ __forceinline__ float exp_acc(float y) {
 }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// y = acc * sigmoid(acc), the reference conv epilogue's form: e^-acc within a
+// few ulp (exp_acc), and 1 / (1 + e) as the hardware reciprocal refined by one
+// Newton step (within an ulp of the divide, a fraction of the divide's
+// instructions).  The exponent is capped at 88 so 1 + e stays finite (the
+// Newton step would turn an infinite e into NaN); below acc = -88 y is then
+// ~ -5e-37 where the divide gives -0, both far under any bf16 output step.
+__device__ __forceinline__ float silu_acc(float acc) {
+  const float d = 1.0f + exp_acc(fminf(-acc, 88.0f));
+  float r = __builtin_amdgcn_rcpf(d);
+  r = fmaf(r, fmaf(-d, r, 1.0f), r);
+  return acc * r;
+}
+
+// Causal depthwise conv of width 4 at one channel (x0 the oldest input, x3 the
+// current one; w the channel's 4 taps) followed by SiLU, in one fixed operation
+// order: every varlen conv path (the standalone conv kernel and the conv fused
+// into the chunk prep kernel) goes through this, so they agree bit for bit.
+__device__ __forceinline__ float conv4_silu(float x0, float x1, float x2, float x3, const float* w) {
+  float acc = x0 * w[0];
+  acc = fmaf(x1, w[1], acc);
+  acc = fmaf(x2, w[2], acc);
+  acc = fmaf(x3, w[3], acc);
+  return silu_acc(acc);
+}
+
+// The reference writes the rolled conv state as (x + s) with the other operand
+// masked to zero, which maps -0.0 to +0.0 and is otherwise a bit copy.
+__device__ __forceinline__ uint16_t roll_value(uint16_t bits) {
+  return bits == 0x8000u ? static_cast<uint16_t>(0) : bits;
+}
+
+// Gates of one (token, value head): g = -exp(A_log) * softplus(a + dt_bias)
+// (softplus threshold 20) and beta = sigmoid(b) rounded to bf16, with libm's
+// expf / logf.  Shared by the gate kernel and the fused chunk prep kernel.
+__device__ __forceinline__ float gate_g(float a, float A_log, float dt_bias) {
+  const float z = a + dt_bias;
+  const float sp = z > 20.0f ? z : logf(1.0f + expf(z));
+  return -expf(A_log) * sp;
+}
+__device__ __forceinline__ uint16_t gate_beta(float b) { return f2bf(1.0f / (1.0f + expf(-b))); }
+
+// A per-head parameter stored as bf16 (is_f32 = 0) or fp32.
+__device__ __forceinline__ float load_param(const void* p, int h, int is_f32) {
+  return is_f32 ? static_cast<const float*>(p)[h] : bf2f(static_cast<const uint16_t*>(p)[h]);
+}
+
 // ---- MFMA fragment types (v_mfma_f32_16x16x32_bf16) ----
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x8_t __attribute__((ext_vector_type(8)));

@@ -38,6 +38,7 @@ class Switches:
     varlen: bool = True
     fla_chunk: bool = True
     fla_recurrent: bool = True
+    fused_prefill: bool = True
 
     @classmethod
     def from_env(cls) -> "Switches":
@@ -47,7 +48,8 @@ class Switches:
                    inplace=e("NANOVLLM_GDN_INPLACE", "1") == "1",
                    varlen=e("NANOVLLM_GDN_VARLEN", "1") == "1",
                    fla_chunk=e("FLA_CHUNK", "1") == "1",
-                   fla_recurrent=e("FLA_RECURRENT", "1") == "1")
+                   fla_recurrent=e("FLA_RECURRENT", "1") == "1",
+                   fused_prefill=e("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1")
 
 
 class GatedDeltaNetCore:
@@ -150,6 +152,14 @@ class GatedDeltaNetCore:
         self._to(mixed.device)
         N = mixed.shape[0]
         Hk, Hv, D = self.Hk, self.Hv, self.D
+        if self.sw.fused_prefill and self.sw.gbeta and self.sw.conv_kernel and self.K == 4:
+            # gates + conv + chunk rule in one call (the same results as the
+            # three calls below)
+            cu64_gpu = varlen_meta(lens_q, mixed.device)[3]
+            with self._timed("conv_chunk_prefill"):
+                o = ops.conv_chunk_prefill_varlen(mixed, conv_cache, self.conv_w, b, a, self.A_log, self.dt_bias,
+                                                  cu64_gpu, s_cache, ids, Hk, Hv, D)
+            return self._norm(o, z.view(N, Hv, D))
         g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
         cu_gpu, lens_gpu, _, cu64_gpu = varlen_meta(lens_q, mixed.device)
         if self.sw.conv_kernel:

@@ -247,6 +247,67 @@ def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     return o, hT
 
 
+def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, conv_weight: torch.Tensor,
+                              b: torch.Tensor, a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
+                              cu_seqlens: torch.Tensor, state: torch.Tensor, state_ids: torch.Tensor | None,
+                              num_k_heads: int, num_v_heads: int, head_dim: int,
+                              scale: float | None = None) -> torch.Tensor:
+    """Gates, varlen causal conv1d + SiLU and the chunked gated delta rule in
+    one call (two kernels), the prefill sequence of _gdn_prefill_varlen
+    (nanovllm/models/qwen3_5.py:934-961): the same results as fused_g_beta ->
+    causal_conv_silu_varlen_parts -> chunk_gated_delta_rule_varlen (q/k L2
+    norm on), bit for bit.
+
+    mixed [N, C] bf16 raw q|k|v rows (C = 2*Hk*D + Hv*D, channel stride 1);
+    conv_state [slots, C, 3] bf16 and state [slots, Hv, D, D] fp32 slot pools,
+    both read and updated in place at rows state_ids (the sequence index if
+    None); conv_weight [C, 4] (or [C, 1, 4]); b, a [N, Hv] bf16; a_log,
+    dt_bias [Hv]; cu_seqlens [n+1] (device).  Returns o [N, Hv, D] bf16."""
+    dev = _check_cuda(mixed, conv_state, conv_weight, b, a, a_log, dt_bias, cu_seqlens, state, state_ids)
+    _bf16(mixed, "mixed")
+    _bf16(conv_state, "conv_state")
+    _bf16(a, "a")
+    _bf16(b, "b")
+    Hk, Hv, D = num_k_heads, num_v_heads, head_dim
+    N, C = mixed.shape
+    assert C == 2 * Hk * D + Hv * D and Hv % Hk == 0
+    w = conv_weight.reshape(C, -1)
+    _bf16(w, "conv_weight")
+    assert w.shape[1] == 4, "the fused path is built for conv width 4"
+    w = w.contiguous()
+    if mixed.stride(1) != 1 or mixed.stride(0) % 8 or mixed.data_ptr() % 16:
+        mixed = mixed.contiguous()
+    assert conv_state.stride(2) == 1 and tuple(conv_state.shape[1:]) == (C, 3)
+    a = a.contiguous()
+    b = b.contiguous()
+    assert a.shape == (N, Hv) and b.shape == (N, Hv)
+    if a_log.dtype != dt_bias.dtype or a_log.dtype not in (torch.bfloat16, torch.float32):
+        a_log = a_log.float()
+        dt_bias = dt_bias.float()
+    a_log = a_log.contiguous()
+    dt_bias = dt_bias.contiguous()
+    assert _state_view_ok(state, Hv, D), "state must be an fp32 [slots, Hv, D, D] view"
+    cu = cu_seqlens.to(torch.int64).contiguous()
+    n = cu.shape[0] - 1
+    ids = None
+    if state_ids is not None:
+        ids = state_ids.to(torch.int64).contiguous()
+        assert ids.shape[0] == n
+    if scale is None:
+        scale = D ** -0.5
+    o = torch.empty(N, Hv, D, dtype=torch.bfloat16, device=mixed.device)
+    ws_bytes = _lib.load().gdn_conv_chunk_prefill_workspace_size(N, n, Hv, D)
+    if ws_bytes < 0:
+        raise ValueError(f"unsupported chunk shape N={N} n_seqs={n} Hv={Hv} D={D}")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=mixed.device)
+    _lib.call("gdn_conv_chunk_prefill", _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_state),
+              conv_state.stride(0), conv_state.stride(1), _lib.ptr(w), _lib.ptr(b), _lib.ptr(a),
+              _lib.ptr(a_log), _lib.ptr(dt_bias), int(a_log.dtype == torch.float32), _lib.ptr(state),
+              _lib.ptr(state), _lib.ptr(ids), state.stride(0), _lib.ptr(cu), n, N, Hk, Hv, D, float(scale), 1,
+              _lib.ptr(o), _lib.ptr(ws), ws_bytes, _stream(dev))
+    return o
+
+
 def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False,
                            cu_seqlens=None, cu_seqlens_cpu=None, chunk_size=64, **kwargs):

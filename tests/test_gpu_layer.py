@@ -40,6 +40,7 @@ SWITCH_SETS = [
     {"conv_kernel": False},
     {"inplace": False},
     {"varlen": False},
+    {"fused_prefill": False},
 ]
 
 
