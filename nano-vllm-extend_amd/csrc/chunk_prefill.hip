@@ -287,85 +287,155 @@ struct ConvIn {
 // v rows.  Each output row needs the 3 raw rows before it: inside the chunk
 // and the previous chunk they are rows of x, before a sequence's first token
 // they are the conv state's taps.  Thread (16-byte channel segment c8, rows
-// t0 .. t0 + RPT - 1) loads its RPT + 3 raw rows once per part and writes
-// q -> Qc and k -> Kr (bf16 rows in LDS, zero past the sequence end), the k
-// rows' sums of squares -> ssk (in the plain path's summation order), and
-// v -> vout (rows of this sequence only).
+// t0 .. t0 + RPT - 1) loads its RPT + 3 raw rows of a part (q, k or v) and the
+// part's taps, and writes q -> Qc and k -> Kr (bf16 rows in LDS, zero past the
+// sequence end), the k rows' sums of squares -> ssk (in the plain path's
+// summation order), and v -> vout (rows of this sequence only).
+// The loads of a part are unconditional (rows clamped into x) so that the
+// three parts' loads can be in flight together; the few lanes whose window
+// starts before the sequence replace those rows with the conv state after the
+// loads have landed.
+template <int D>
+struct ConvRaw {
+  static constexpr int RPT = kC * (D / 8) / 256;  // rows per thread
+  uint4 x[RPT + 3];                               // raw rows t0 - 3 .. t0 + RPT - 1
+  uint4 w[4];                                     // taps of the 8 channels
+};
+
+// A per-head parameter stored as bf16 or fp32 (is_f32), read with two 16-bit
+// loads whose addresses do not depend on a branch.
+__device__ __forceinline__ float param_bits(const void* p, int h, int is_f32) {
+  const uint16_t* q = static_cast<const uint16_t*>(p);
+  const uint32_t hi = q[is_f32 ? 2 * h + 1 : h];
+  const uint32_t lo = q[is_f32 ? 2 * h : h];
+  return __uint_as_float((hi << 16) | (is_f32 ? lo : 0u));
+}
+
+__device__ __forceinline__ int conv_part_channel(const ConvIn& cv, int part, int kh, int h, int D) {
+  return part == 0 ? kh * D : part == 1 ? cv.key_dim + kh * D : 2 * cv.key_dim + h * D;
+}
+
+template <int D>
+__device__ __forceinline__ void conv_load(ConvRaw<D>& R, const ConvIn& cv, int part, int64_t tok0, int len, int kh,
+                                          int h, int tid) {
+  constexpr int SEG = D / 8;
+  const int c8 = tid % SEG, t0 = ConvRaw<D>::RPT * (tid / SEG);
+  const int ch = conv_part_channel(cv, part, kh, h, D) + 8 * c8;
+  const uint4* wp = reinterpret_cast<const uint4*>(cv.w + static_cast<int64_t>(ch) * 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) R.w[j] = wp[j];
+#pragma unroll
+  for (int i = 0; i < ConvRaw<D>::RPT + 3; ++i) {
+    // rows past the sequence end re-read its last row (outputs dropped); rows
+    // before the first chunk's start are replaced by the state
+    const int t = t0 - 3 + i;
+    const int64_t row = max<int64_t>(tok0 + min(t, len - 1), 0);
+    R.x[i] = *reinterpret_cast<const uint4*>(cv.x + row * cv.sx + ch);
+  }
+}
+
+// Rows before the sequence's first token (row t0 - 3 + i < 0 of the first
+// chunk): the conv state's tap t0 + i.
+template <int D>
+__device__ __forceinline__ void conv_state_halo(ConvRaw<D>& R, const ConvIn& cv, int part, bool first, int r,
+                                                int kh, int h, int tid) {
+  constexpr int SEG = D / 8;
+  const int c8 = tid % SEG, t0 = ConvRaw<D>::RPT * (tid / SEG);
+  if (first && t0 < 3) {
+    const int64_t slot = cv.ids ? cv.ids[r] : r;
+    const int ch = conv_part_channel(cv, part, kh, h, D) + 8 * c8;
+    const uint16_t* sp = cv.cstate + slot * cv.ss_seq + static_cast<int64_t>(ch) * cv.ss_ch + t0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (t0 + i >= 3) break;
+      uint32_t u[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        u[e] = static_cast<uint32_t>(sp[static_cast<int64_t>(2 * e) * cv.ss_ch + i]) |
+               (static_cast<uint32_t>(sp[static_cast<int64_t>(2 * e + 1) * cv.ss_ch + i]) << 16);
+      R.x[i] = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+  }
+}
+
+__device__ __forceinline__ float bf_elem(const uint4& u, int e) {
+  const uint32_t w = e < 2 ? u.x : e < 4 ? u.y : e < 6 ? u.z : u.w;
+  return (e & 1) ? hi_half(w) : lo_half(w);
+}
+
+template <int D>
+__device__ __forceinline__ void conv_compute(const ConvRaw<D>& R, const ConvIn& cv, int part, uint16_t (*Qc)[D + 8],
+                                             uint16_t (*Kr)[D + 8], float* ssk, int64_t tok0, int len, int h,
+                                             int Hv, int tid) {
+  constexpr int SEG = D / 8;
+  constexpr int RPT = ConvRaw<D>::RPT;
+  const int c8 = tid % SEG, t0 = RPT * (tid / SEG);
+  // two channels at a time keep the unpacked window small
+  uint32_t yp[RPT][4];
+#pragma unroll
+  for (int e2 = 0; e2 < 4; ++e2) {
+    float y[2][RPT];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int e = 2 * e2 + c;
+      float wk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wk[j] = bf_elem(R.w[(4 * e + j) / 8], (4 * e + j) % 8);
+      float xe[RPT + 3];
+#pragma unroll
+      for (int i = 0; i < RPT + 3; ++i) xe[i] = bf_elem(R.x[i], e);
+#pragma unroll
+      for (int rr = 0; rr < RPT; ++rr) y[c][rr] = gdn::conv4_silu(xe[rr], xe[rr + 1], xe[rr + 2], xe[rr + 3], wk);
+    }
+#pragma unroll
+    for (int rr = 0; rr < RPT; ++rr) yp[rr][e2] = gdn::f2bf2(y[0][rr], y[1][rr]);
+  }
+#pragma unroll
+  for (int rr = 0; rr < RPT; ++rr) {
+    const int t = t0 + rr;
+    u32x4_t out = {yp[rr][0], yp[rr][1], yp[rr][2], yp[rr][3]};
+    if (part == 2) {
+      if (t < len) *reinterpret_cast<u32x4_t*>(cv.vout + ((tok0 + t) * Hv + h) * D + 8 * c8) = out;
+      continue;
+    }
+    if (t >= len) out = u32x4_t{0u, 0u, 0u, 0u};
+    if (part == 0) {
+      *reinterpret_cast<u32x4_t*>(&Qc[t][8 * c8]) = out;
+    } else {
+      *reinterpret_cast<u32x4_t*>(&Kr[t][8 * c8]) = out;
+      const s16x8_t kv8 = __builtin_bit_cast(s16x8_t, out);
+      float ks = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
+        ks += kf * kf;
+      }
+#pragma unroll
+      for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
+      if (c8 == 0) ssk[t] = ks;
+    }
+  }
+}
+
+// The three parts with two register sets: q and k in flight together, v's
+// loads issued once q's registers are free.
 template <int D>
 __device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)[D + 8], uint16_t (*Kr)[D + 8],
                                                 float* ssk, int64_t tok0, int len, bool first, int r, int kh,
                                                 int h, int Hv, int tid) {
-  constexpr int SEG = D / 8;
-  constexpr int RPT = kC * SEG / 256;  // rows per thread
-  const int c8 = tid % SEG, t0 = RPT * (tid / SEG);
-  const int64_t slot = cv.ids ? cv.ids[r] : r;
-#pragma unroll
-  for (int part = 0; part < 3; ++part) {
-    const int ch = (part == 0 ? kh * D : part == 1 ? cv.key_dim + kh * D : 2 * cv.key_dim + h * D) + 8 * c8;
-    float wk[8][4];
-    {
-      const uint4* wp = reinterpret_cast<const uint4*>(cv.w + static_cast<int64_t>(ch) * 4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint4 u = wp[j];
-        const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          wk[2 * j + e / 2][2 * (e & 1)] = lo_half(uu[e]);
-          wk[2 * j + e / 2][2 * (e & 1) + 1] = hi_half(uu[e]);
-        }
-      }
-    }
-    float xw[RPT + 3][8];
-#pragma unroll
-    for (int i = 0; i < RPT + 3; ++i) {
-      const int t = t0 - 3 + i;
-      if (t >= 0 || !first) {
-        // rows past the sequence end re-read its last row (outputs dropped)
-        const uint4 u = *reinterpret_cast<const uint4*>(cv.x + (tok0 + min(t, len - 1)) * cv.sx + ch);
-        const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          xw[i][2 * e] = lo_half(uu[e]);
-          xw[i][2 * e + 1] = hi_half(uu[e]);
-        }
-      } else {
-        const uint16_t* sp = cv.cstate + slot * cv.ss_seq + static_cast<int64_t>(ch) * cv.ss_ch + (t + 3);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xw[i][e] = gdn::bf2f(sp[static_cast<int64_t>(e) * cv.ss_ch]);
-      }
-    }
-#pragma unroll
-    for (int rr = 0; rr < RPT; ++rr) {
-      const int t = t0 + rr;
-      float y[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = gdn::conv4_silu(xw[rr][e], xw[rr + 1][e], xw[rr + 2][e], xw[rr + 3][e], wk[e]);
-      u32x4_t out;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) out[e] = gdn::f2bf2(y[2 * e], y[2 * e + 1]);
-      if (part == 2) {
-        if (t < len) *reinterpret_cast<u32x4_t*>(cv.vout + ((tok0 + t) * Hv + h) * D + 8 * c8) = out;
-        continue;
-      }
-      if (t >= len) out = u32x4_t{0u, 0u, 0u, 0u};
-      if (part == 0) {
-        *reinterpret_cast<u32x4_t*>(&Qc[t][8 * c8]) = out;
-      } else {
-        *reinterpret_cast<u32x4_t*>(&Kr[t][8 * c8]) = out;
-        const s16x8_t kv8 = __builtin_bit_cast(s16x8_t, out);
-        float ks = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
-          ks += kf * kf;
-        }
-#pragma unroll
-        for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
-        if (c8 == 0) ssk[t] = ks;
-      }
-    }
-  }
+  ConvRaw<D> R0, R1;
+  conv_load<D>(R0, cv, 0, tok0, len, kh, h, tid);
+  gdn::keep_loads_here();
+  conv_load<D>(R1, cv, 1, tok0, len, kh, h, tid);
+  gdn::keep_loads_here();
+  conv_state_halo<D>(R0, cv, 0, first, r, kh, h, tid);
+  conv_compute<D>(R0, cv, 0, Qc, Kr, ssk, tok0, len, h, Hv, tid);
+  conv_load<D>(R0, cv, 2, tok0, len, kh, h, tid);
+  gdn::keep_loads_here();
+  conv_state_halo<D>(R1, cv, 1, first, r, kh, h, tid);
+  conv_compute<D>(R1, cv, 1, Qc, Kr, ssk, tok0, len, h, Hv, tid);
+  conv_state_halo<D>(R0, cv, 2, first, r, kh, h, tid);
+  conv_compute<D>(R0, cv, 2, Qc, Kr, ssk, tok0, len, h, Hv, tid);
 }
 
 // grid = 8 * ceil(nc_bound * Hv / 8); block = 256.  One workgroup per
@@ -436,6 +506,22 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     if (lg == 0) sm.ssq[t] = qs;
   };
   if constexpr (!kConv) q_rows();
+  // gate inputs of token tok0 + lane (used by wave 0), loaded ahead of the
+  // rows by every wave with in-range addresses, so no load waits on a branch
+  float gin, bin, al = 0.f, dtb = 0.f;
+  {
+    const int64_t gi = (tok0 + min(lane, len - 1)) * Hv + h;
+    if constexpr (kConv) {
+      gin = gdn::bf2f(cv.a[gi]);
+      bin = gdn::bf2f(cv.b[gi]);
+      al = param_bits(cv.A_log, h, cv.param_f32);
+      dtb = param_bits(cv.dt_bias, h, cv.param_f32);
+    } else {
+      gin = g[gi];
+      bin = gdn::bf2f(beta[gi]);
+    }
+  }
+  gdn::keep_loads_here();
   if constexpr (kConv) {
     conv_chunk_rows<D>(cv, Qc, sm.Kr, sm.ssk, tok0, len, jc == 0, r, kh, h, Hv, tid);
   } else {
@@ -461,14 +547,12 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
   if (wave == 0) {
     float gv = 0.f, bv = 0.f;
     if (lane < len) {
-      const int64_t gi = (tok0 + lane) * Hv + h;
       if constexpr (kConv) {
-        gv = gdn::gate_g(gdn::bf2f(cv.a[gi]), gdn::load_param(cv.A_log, h, cv.param_f32),
-                         gdn::load_param(cv.dt_bias, h, cv.param_f32));
-        bv = gdn::bf2f(gdn::gate_beta(gdn::bf2f(cv.b[gi])));
+        gv = gdn::gate_g(gin, al, dtb);
+        bv = gdn::bf2f(gdn::gate_beta(bin));
       } else {
-        gv = g[gi];
-        bv = gdn::bf2f(beta[gi]);
+        gv = gin;
+        bv = bin;
       }
     }
 #pragma unroll
