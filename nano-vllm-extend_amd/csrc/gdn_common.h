@@ -57,17 +57,16 @@ __device__ __forceinline__ float exp_acc(float y) {
 }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-// y = acc * sigmoid(acc), the reference conv epilogue's form: e^-acc within a
-// few ulp (exp_acc), and 1 / (1 + e) as the hardware reciprocal refined by one
-// Newton step (within an ulp of the divide, a fraction of the divide's
-// instructions).  The exponent is capped at 88 so 1 + e stays finite (the
-// Newton step would turn an infinite e into NaN); below acc = -88 y is then
-// ~ -5e-37 where the divide gives -0, both far under any bf16 output step.
+// y = acc * sigmoid(acc), the reference conv epilogue's form (acc *
+// tl.sigmoid(acc), which lowers to an exp2 of the scaled argument and a
+// reciprocal): e^-acc as the hardware exp2 of -acc log2(e), then the hardware
+// reciprocal of 1 + e^-acc.  Relative error <= ~1e-7 (|acc| + 2) -- the
+// argument's rounding times log2(e) ln 2 plus an ulp each for exp2 and rcp --
+// far below the bf16 output step (3.9e-3).  For acc < -88.7 e^-acc is +inf,
+// its reciprocal 0 and y = -0, as the divide gives.
 __device__ __forceinline__ float silu_acc(float acc) {
-  const float d = 1.0f + exp_acc(fminf(-acc, 88.0f));
-  float r = __builtin_amdgcn_rcpf(d);
-  r = fmaf(r, fmaf(-d, r, 1.0f), r);
-  return acc * r;
+  const float e = __builtin_amdgcn_exp2f(acc * -1.44269504088896340736f);
+  return acc * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // Causal depthwise conv of width 4 at one channel (x0 the oldest input, x3 the
