@@ -133,18 +133,25 @@ def _profiled_traffic(name: str):
 # ------------------------------------------------------------------ timing --
 class EventTimer:
     """HIP events around named kernels on torch's current stream (the stream
-    the kernels are launched on)."""
+    the kernels are launched on).  `only`: record just these names (each
+    event pair costs the stream a few microseconds, so the timed steps carry
+    events around the measured kernel only)."""
 
-    def __init__(self):
+    def __init__(self, only=None):
         self.open: dict[str, torch.cuda.Event] = {}
         self.pairs: dict[str, list] = {}
+        self.only = only
 
     def start(self, name):
+        if self.only is not None and name not in self.only:
+            return
         e = torch.cuda.Event(enable_timing=True)
         e.record()
         self.open[name] = e
 
     def stop(self, name):
+        if self.only is not None and name not in self.only:
+            return
         e = torch.cuda.Event(enable_timing=True)
         e.record()
         self.pairs.setdefault(name, []).append((self.open.pop(name), e))
@@ -182,11 +189,20 @@ def prefill_bench(pkg, cfg, dev, K, W):
 
     for _ in range(W):
         step()
-    timer = EventTimer()
+    # timed steps: events around the dominant kernel only
+    timer = EventTimer(only={"conv_chunk_prefill", "chunk_prefill"})
     core.timer = timer
     t = timed_steps(step, K)
+    # per-kernel breakdown of the other kernels: a few more steps with events on every kernel
+    rest = EventTimer()
+    core.timer = rest
+    for _ in range(min(K, 20)):
+        step()
+    torch.cuda.synchronize()
     core.timer = None
-    return t / K, timer.avg_us()
+    us = rest.avg_us()
+    us.update(timer.avg_us())
+    return t / K, us
 
 
 def decode_bench(pkg, cfg, dev, K, W):
@@ -282,8 +298,8 @@ def cpu_baseline(cfg, n_seq: int, threads: int):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="1,2,3,4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",

@@ -19,6 +19,13 @@ layer code:
 and sets the feature flags the layer reads (_HAS_FLA, _USE_FLA_CHUNK,
 _USE_FLA_RECURRENT, _USE_GDN_VARLEN) from the same environment switches
 (FLA_CHUNK, FLA_RECURRENT, NANOVLLM_GDN_VARLEN) the reference reads.
+
+With NANOVLLM_GDN_FUSED_PREFILL=1 (the default; it also needs the gate and
+conv kernels on and a conv width of 4) it further replaces the method
+Qwen3_5GatedDeltaNet._gdn_prefill_varlen (qwen3_5.py:922-965) with one whose
+gates, conv and chunk rule are the single fused call
+ops.conv_chunk_prefill_varlen (the same results as the three calls the
+method makes, bit for bit), on the layer's own pools and slot ids.
 """
 from __future__ import annotations
 
@@ -36,6 +43,35 @@ PATCHED_NAMES = (
 def _recurrent_ref_api(query, key, value, g, beta, initial_state=None):
     return ops.recurrent_gated_delta_rule(query, key, value, g=g, beta=beta, initial_state=initial_state,
                                           output_final_state=True, use_qk_l2norm_in_kernel=True)
+
+
+def _fused_prefill_method(mod, orig):
+    def _gdn_prefill_varlen(self, hidden, lens_q, ids):
+        """Fused form of Qwen3_5GatedDeltaNet._gdn_prefill_varlen
+        (nanovllm/models/qwen3_5.py:922-965); other conv widths keep the
+        original method."""
+        if self.conv_kernel != 4:
+            return orig(self, hidden, lens_q, ids)
+        b = self.in_proj_b(hidden)
+        a = self.in_proj_a(hidden)
+        A_log = self.A_log[self._v_head_slice]
+        dt_bias = self.dt_bias[self._v_head_slice]
+        z = self.in_proj_z(hidden)
+        mixed = self.in_proj_qkv(hidden)
+        cu64_gpu = mod._varlen_meta(lens_q)[3]
+        core = ops.conv_chunk_prefill_varlen(
+            mixed, self.conv_cache, self.conv1d.weight.view(self.conv_dim, self.conv_kernel), b, a, A_log, dt_bias,
+            cu64_gpu, self.s_cache, ids, self.num_k_heads, self.num_v_heads, self.head_k_dim)
+        core = self.norm(core, z.view(-1, self.num_v_heads, self.head_v_dim))
+        return self.out_proj(core.reshape(-1, self.value_dim))
+
+    return _gdn_prefill_varlen
+
+
+def _fused_prefill_enabled() -> bool:
+    e = os.environ.get
+    return (e("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1" and e("NANOVLLM_GDN_GBETA", "1") == "1"
+            and e("NANOVLLM_CONV_TRITON", "1") == "1")
 
 
 def install(mod) -> dict:
@@ -58,9 +94,20 @@ def install(mod) -> dict:
     mod._USE_FLA_CHUNK = os.environ.get("FLA_CHUNK", "1") == "1"
     mod._USE_FLA_RECURRENT = os.environ.get("FLA_RECURRENT", "1") == "1"
     mod._USE_GDN_VARLEN = mod._USE_FLA_CHUNK and os.environ.get("NANOVLLM_GDN_VARLEN", "1") == "1"
+    cls = getattr(mod, "Qwen3_5GatedDeltaNet", None)
+    if cls is not None and _fused_prefill_enabled():
+        prev["Qwen3_5GatedDeltaNet._gdn_prefill_varlen"] = cls.__dict__.get("_gdn_prefill_varlen")
+        cls._gdn_prefill_varlen = _fused_prefill_method(mod, cls._gdn_prefill_varlen)
     return prev
 
 
 def uninstall(mod, prev: dict) -> None:
     for name, val in prev.items():
+        if name == "Qwen3_5GatedDeltaNet._gdn_prefill_varlen":
+            cls = mod.Qwen3_5GatedDeltaNet
+            if val is None:
+                del cls._gdn_prefill_varlen
+            else:
+                cls._gdn_prefill_varlen = val
+            continue
         setattr(mod, name, val)

@@ -281,3 +281,59 @@ def test_config4_spec_verify_full(pkg, dev):
     for i in range(B):
         acc = int(c["accepted"][i])
         assert torch.equal(poolc[ids[i]], interc[i, acc - 1]), "rollback restores the accepted prefix state"
+
+
+def test_installed_prefill_method_equals_layer_core(pkg, dev):
+    """integration.install's fused _gdn_prefill_varlen on a stand-in layer with
+    the reference's attribute names gives the layer core's prefill bit for bit
+    and updates the same pools."""
+    import types
+
+    gen = torch.Generator().manual_seed(35)
+    Hk, Hv, D = 2, 4, 128
+    C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
+    lens = [70, 3, 130]
+    N = sum(lens)
+    mixed, z, b, a = (t.to(dev) for t in _rows(gen, N, C, Hv, D))
+    slots = 6
+    conv0 = torch.randn(slots, C, 3, generator=gen).to(BF16).to(dev)
+    s0 = (torch.randn(slots, Hv, D, D, generator=gen) * 0.1).to(dev)
+    ids = torch.tensor([4, 0, 2], device=dev)
+
+    core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w)
+    cp1, sp1 = conv0.clone(), s0.clone()
+    ref = core.prefill_varlen(mixed, z, b, a, lens, ids, cp1, sp1).reshape(N, Hv * D)
+
+    mod = types.ModuleType("qwen3_5_stub")
+
+    def _varlen_meta(lens_q):
+        cu = torch.tensor([0] + torch.tensor(lens_q).cumsum(0).tolist(), dtype=torch.int64, device=dev)
+        return cu.int(), torch.tensor(lens_q, dtype=torch.int32, device=dev), cu.cpu(), cu
+
+    class Qwen3_5GatedDeltaNet:
+        def _gdn_prefill_varlen(self, hidden, lens_q, ids):
+            raise AssertionError("the original method must not run")
+
+    mod._varlen_meta = _varlen_meta
+    mod.Qwen3_5GatedDeltaNet = Qwen3_5GatedDeltaNet
+    prev = pkg.integration.install(mod)
+    try:
+        layer = Qwen3_5GatedDeltaNet()
+        layer.num_k_heads, layer.num_v_heads, layer.head_k_dim, layer.head_v_dim = Hk, Hv, D, D
+        layer.value_dim, layer.conv_dim, layer.conv_kernel = Hv * D, C, 4
+        layer.in_proj_b, layer.in_proj_a = (lambda h: b), (lambda h: a)
+        layer.in_proj_z, layer.in_proj_qkv = (lambda h: z), (lambda h: mixed)
+        layer.A_log, layer.dt_bias, layer._v_head_slice = A_log.to(dev), dt_bias.to(dev), slice(0, Hv)
+        layer.conv1d = types.SimpleNamespace(weight=conv_w.to(dev).view(C, 1, 4))
+        norm = pkg.ops.Qwen3_5RMSNormGated(D)
+        norm.weight.data = norm_w.to(dev)
+        layer.norm = norm
+        layer.out_proj = lambda x: x
+        layer.conv_cache, layer.s_cache = conv0.clone(), s0.clone()
+        out = layer._gdn_prefill_varlen(None, lens, ids)
+    finally:
+        pkg.integration.uninstall(mod, prev)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(layer.s_cache, sp1)
+    assert torch.equal(layer.conv_cache.view(torch.int16), cp1.view(torch.int16))

@@ -72,6 +72,28 @@ def test_install_rebinds_reference_call_sites(pkg):
     assert mod._HAS_FLA is False
 
 
+def test_install_replaces_varlen_prefill_method(pkg, monkeypatch):
+    mod = types.ModuleType("qwen3_5_stub")
+
+    class Qwen3_5GatedDeltaNet:
+        def _gdn_prefill_varlen(self, hidden, lens_q, ids):
+            return "original"
+
+    mod.Qwen3_5GatedDeltaNet = Qwen3_5GatedDeltaNet
+    orig = Qwen3_5GatedDeltaNet.__dict__["_gdn_prefill_varlen"]
+    prev = pkg.integration.install(mod)
+    assert Qwen3_5GatedDeltaNet.__dict__["_gdn_prefill_varlen"] is not orig
+    layer = Qwen3_5GatedDeltaNet()
+    layer.conv_kernel = 3                     # other widths keep the original method
+    assert layer._gdn_prefill_varlen(None, [1], None) == "original"
+    pkg.integration.uninstall(mod, prev)
+    assert Qwen3_5GatedDeltaNet.__dict__["_gdn_prefill_varlen"] is orig
+    monkeypatch.setenv("NANOVLLM_GDN_FUSED_PREFILL", "0")
+    prev = pkg.integration.install(mod)
+    assert Qwen3_5GatedDeltaNet.__dict__["_gdn_prefill_varlen"] is orig
+    pkg.integration.uninstall(mod, prev)
+
+
 def test_ops_have_no_cpu_path(pkg):
     a = torch.zeros(4, 2, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU only"):
