@@ -244,20 +244,36 @@ __device__ __forceinline__ void tri_tile(int j, int& mt, int& nt) {
 }
 __device__ __forceinline__ int tix(int mt, int nt) { return (mt * (mt + 1)) / 2 + nt; }
 
+// LDS of the prep kernel: 37 KiB at D = 128, four workgroups per CU.
 template <int D>
 struct __align__(16) PrepSmem {
-  uint16_t Kr[kC][D + 8];         // raw bf16 K rows
+  // The bf16 K rows are last read by the A rows (phase 2b); after that
+  // barrier the same bytes hold the off-diagonal tiles of T and the solve's
+  // per-wave scratch.
+  union {
+    uint16_t Kr[kC][D + 8];
+    struct {
+      float To[6][16][kTileLd];   // T tiles (mt, nt < mt) at mt (mt - 1) / 2 + nt
+      float scr[4][16][kTileLd];
+    } s;
+  } u;
   float Lp[10][16][kTileLd];      // lower tiles of L
-  float Tp[10][16][kTileLd];      // lower tiles of T = (I + L)^-1
-  float scr[4][16][kTileLd];      // per-wave scratch of the solve
+  float Td[4][16][kTileLd];       // diagonal tiles of T = (I + L)^-1
   float G[kC], bt[kC], rk[kC], rq[kC], ssk[kC], ssq[kC], cw[kC], cq[kC];
 };
 
+// 16x16 tile (mt, nt) of T, nt <= mt
+template <int D>
+__device__ __forceinline__ float* t_tile(PrepSmem<D>& sm, int mt, int nt) {
+  return mt == nt ? &sm.Td[mt][0][0] : &sm.u.s.To[(mt * (mt - 1)) / 2 + nt][0][0];
+}
+
 // Row t, token quad Q (tokens 4Q..4Q+3) of T, times c[s]: 4 floats.
-__device__ __forceinline__ float4 t_quad(const float (*Tp)[16][kTileLd], const float* c, int t, int Q) {
+template <int D>
+__device__ __forceinline__ float4 t_quad(PrepSmem<D>& sm, const float* c, int t, int Q) {
   const int mt = t >> 4, st = Q >> 2;
   if (st > mt) return make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4 r = *reinterpret_cast<const float4*>(&Tp[tix(mt, st)][t & 15][(Q & 3) * 4]);
+  const float4 r = *reinterpret_cast<const float4*>(t_tile(sm, mt, st) + (t & 15) * kTileLd + (Q & 3) * 4);
   const float4 cc = *reinterpret_cast<const float4*>(&c[4 * Q]);
   return make_float4(r.x * cc.x, r.y * cc.y, r.z * cc.z, r.w * cc.w);
 }
@@ -299,7 +315,6 @@ template <int D>
 struct ConvRaw {
   static constexpr int RPT = kC * (D / 8) / 256;  // rows per thread
   uint4 x[RPT + 3];                               // raw rows t0 - 3 .. t0 + RPT - 1
-  uint4 w[4];                                     // taps of the 8 channels
 };
 
 // A per-head parameter stored as bf16 or fp32 (is_f32), read with two 16-bit
@@ -321,9 +336,6 @@ __device__ __forceinline__ void conv_load(ConvRaw<D>& R, const ConvIn& cv, int p
   constexpr int SEG = D / 8;
   const int c8 = tid % SEG, t0 = ConvRaw<D>::RPT * (tid / SEG);
   const int ch = conv_part_channel(cv, part, kh, h, D) + 8 * c8;
-  const uint4* wp = reinterpret_cast<const uint4*>(cv.w + static_cast<int64_t>(ch) * 4);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) R.w[j] = wp[j];
 #pragma unroll
   for (int i = 0; i < ConvRaw<D>::RPT + 3; ++i) {
     // rows past the sequence end re-read its last row (outputs dropped); rows
@@ -365,11 +377,20 @@ __device__ __forceinline__ float bf_elem(const uint4& u, int e) {
 
 template <int D>
 __device__ __forceinline__ void conv_compute(const ConvRaw<D>& R, const ConvIn& cv, int part, uint16_t (*Qc)[D + 8],
-                                             uint16_t (*Kr)[D + 8], float* ssk, int64_t tok0, int len, int h,
-                                             int Hv, int tid) {
+                                             uint16_t (*Kr)[D + 8], float* ssk, int64_t tok0, int len, int kh,
+                                             int h, int Hv, int tid) {
   constexpr int SEG = D / 8;
   constexpr int RPT = ConvRaw<D>::RPT;
   const int c8 = tid % SEG, t0 = RPT * (tid / SEG);
+  // the part's taps (8 channels x 4), read here rather than with the rows:
+  // every workgroup reads the same few KiB, so they come from cache
+  uint4 wt[4];
+  {
+    const uint4* wp =
+        reinterpret_cast<const uint4*>(cv.w + static_cast<int64_t>(conv_part_channel(cv, part, kh, h, D) + 8 * c8) * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wt[j] = wp[j];
+  }
   // two channels at a time keep the unpacked window small
   uint32_t yp[RPT][4];
 #pragma unroll
@@ -380,7 +401,7 @@ __device__ __forceinline__ void conv_compute(const ConvRaw<D>& R, const ConvIn& 
       const int e = 2 * e2 + c;
       float wk[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wk[j] = bf_elem(R.w[(4 * e + j) / 8], (4 * e + j) % 8);
+      for (int j = 0; j < 4; ++j) wk[j] = bf_elem(wt[(4 * e + j) / 8], (4 * e + j) % 8);
       float xe[RPT + 3];
 #pragma unroll
       for (int i = 0; i < RPT + 3; ++i) xe[i] = bf_elem(R.x[i], e);
@@ -429,13 +450,13 @@ __device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)
   conv_load<D>(R1, cv, 1, tok0, len, kh, h, tid);
   gdn::keep_loads_here();
   conv_state_halo<D>(R0, cv, 0, first, r, kh, h, tid);
-  conv_compute<D>(R0, cv, 0, Qc, Kr, ssk, tok0, len, h, Hv, tid);
+  conv_compute<D>(R0, cv, 0, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
+  conv_state_halo<D>(R1, cv, 1, first, r, kh, h, tid);
+  conv_compute<D>(R1, cv, 1, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
   conv_load<D>(R0, cv, 2, tok0, len, kh, h, tid);
   gdn::keep_loads_here();
-  conv_state_halo<D>(R1, cv, 1, first, r, kh, h, tid);
-  conv_compute<D>(R1, cv, 1, Qc, Kr, ssk, tok0, len, h, Hv, tid);
   conv_state_halo<D>(R0, cv, 2, first, r, kh, h, tid);
-  conv_compute<D>(R0, cv, 2, Qc, Kr, ssk, tok0, len, h, Hv, tid);
+  conv_compute<D>(R0, cv, 2, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
 }
 
 // grid = 8 * ceil(nc_bound * Hv / 8); block = 256.  One workgroup per
@@ -443,7 +464,7 @@ __device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)
 // kConv: q, k, v are the conv1d + SiLU of cv.x and g, beta the gates of
 // cv.a, cv.b, all computed here (q, k, g, beta unused); v goes to cv.vout.
 template <int D, bool kConv>
-__global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
+__global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
     const float* __restrict__ g, const uint16_t* __restrict__ beta, const int64_t* __restrict__ cu,
     int n_seqs, int64_t nc_bound, int Hk, int Hv, float scale, int l2norm, uint8_t* __restrict__ ws,
@@ -482,7 +503,7 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
   // registers become Q' once cQ is known.  The fused variant first runs the
   // conv into LDS (q rows in the L / T tiles' space, free until phase 2a).
   uint16_t (*Qc)[D + 8] = reinterpret_cast<uint16_t (*)[D + 8]>(&sm.Lp[0][0][0]);
-  static_assert(sizeof(sm.Lp) + sizeof(sm.Tp) >= sizeof(uint16_t) * kC * (D + 8), "conv q rows fit L and T");
+  static_assert(sizeof(sm.Lp) + sizeof(sm.Td) >= sizeof(uint16_t) * kC * (D + 8), "conv q rows fit L and T");
   s16x8_t qv[KTD];
   auto q_rows = [&]() {
     const int t = 16 * wave + lr;
@@ -523,7 +544,7 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
   }
   gdn::keep_loads_here();
   if constexpr (kConv) {
-    conv_chunk_rows<D>(cv, Qc, sm.Kr, sm.ssk, tok0, len, jc == 0, r, kh, h, Hv, tid);
+    conv_chunk_rows<D>(cv, Qc, sm.u.Kr, sm.ssk, tok0, len, jc == 0, r, kh, h, Hv, tid);
   } else {
 #pragma unroll
     for (int j = 0; j < NSEG1; ++j) {
@@ -532,7 +553,7 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
       const int64_t row = tok0 + min(t, len - 1);
       s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + row * sk + c8 * 8);
       if (t >= len) kv8 = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      *reinterpret_cast<s16x8_t*>(&sm.Kr[t][c8 * 8]) = kv8;
+      *reinterpret_cast<s16x8_t*>(&sm.u.Kr[t][c8 * 8]) = kv8;
       float ks = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -582,7 +603,7 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     uint8_t* kp = rec + rec_kt(D);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const s16x8_t* kr = reinterpret_cast<const s16x8_t*>(&sm.Kr[32 * tt + li][32 * kt + 8 * g]);
+      const s16x8_t* kr = reinterpret_cast<const s16x8_t*>(&sm.u.Kr[32 * tt + li][32 * kt + 8 * g]);
       f32x16_t kc = mfma32_bf16(kr[0], iq0, zero16());
       kc = mfma32_bf16(kr[2], iq1, kc);
       *reinterpret_cast<h16x8_t*>(kp + frag_byte(kt * 4 + 2 * tt, lane)) = pack_h8<0>(kc);
@@ -634,8 +655,8 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KTD; ++kk) {
-      const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Kr[16 * mt + lr][32 * kk + 8 * lg]);
-      const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.Kr[16 * nt + lr][32 * kk + 8 * lg]);
+      const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.u.Kr[16 * mt + lr][32 * kk + 8 * lg]);
+      const s16x8_t b8 = *reinterpret_cast<const s16x8_t*>(&sm.u.Kr[16 * nt + lr][32 * kk + 8 * lg]);
       acc = gdn::mfma16x16x32(a8, b8, acc);
     }
     const int s = 16 * nt + lr;
@@ -671,7 +692,7 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
       x[rr] = acc;
     }
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) sm.Tp[dt][rr][c] = x[rr];
+    for (int rr = 0; rr < 16; ++rr) sm.Td[bb][rr][c] = x[rr];
   }
   {
     // key-token tiles ns of the 32-wide column blocks the rows touch; tiles
@@ -687,7 +708,7 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
       if (ns <= mt) {
 #pragma unroll
         for (int kk = 0; kk < KTD; ++kk) {
-          const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.Kr[16 * ns + lr][32 * kk + 8 * lg]);
+          const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.u.Kr[16 * ns + lr][32 * kk + 8 * lg]);
           acc = gdn::mfma16x16x32(a8, qv[kk], acc);
         }
       }
@@ -710,52 +731,52 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
   if (wave < 3) {
     const int j = wave, i = j + 1;
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lp[tix(i, j)][0][0], kTileLd, &sm.Tp[tix(j, j)][0][0], kTileLd, lane);
-    st16_f32(&sm.scr[wave][0][0], p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(i, j)][0][0], kTileLd, t_tile(sm, j, j), kTileLd, lane);
+    st16_f32(&sm.u.s.scr[wave][0][0], p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tp[tix(i, i)][0][0], kTileLd, &sm.scr[wave][0][0], kTileLd, lane);
-    st16_f32(&sm.Tp[tix(i, j)][0][0], t2, -1.f, lane);
+    t2 = mm16_f32(t2, t_tile(sm, i, i), kTileLd, &sm.u.s.scr[wave][0][0], kTileLd, lane);
+    st16_f32(t_tile(sm, i, j), t2, -1.f, lane);
   } else {
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lp[tix(3, 0)][0][0], kTileLd, &sm.Tp[tix(0, 0)][0][0], kTileLd, lane);  // L30 T00
-    st16_f32(&sm.scr[3][0][0], p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 0)][0][0], kTileLd, t_tile(sm, 0, 0), kTileLd, lane);  // L30 T00
+    st16_f32(&sm.u.s.scr[3][0][0], p, 1.f, lane);
   }
   __syncthreads();
   // second sub-diagonal: T20, T31; partial sum for T30
   if (wave == 0) {
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lp[tix(2, 0)][0][0], kTileLd, &sm.Tp[tix(0, 0)][0][0], kTileLd, lane);  // L20 T00
-    p = mm16_f32(p, &sm.Lp[tix(2, 1)][0][0], kTileLd, &sm.Tp[tix(1, 0)][0][0], kTileLd, lane);  // L21 T10
-    st16_f32(&sm.scr[0][0][0], p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(2, 0)][0][0], kTileLd, t_tile(sm, 0, 0), kTileLd, lane);  // L20 T00
+    p = mm16_f32(p, &sm.Lp[tix(2, 1)][0][0], kTileLd, t_tile(sm, 1, 0), kTileLd, lane);  // L21 T10
+    st16_f32(&sm.u.s.scr[0][0][0], p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tp[tix(2, 2)][0][0], kTileLd, &sm.scr[0][0][0], kTileLd, lane);
-    st16_f32(&sm.Tp[tix(2, 0)][0][0], t2, -1.f, lane);
+    t2 = mm16_f32(t2, t_tile(sm, 2, 2), kTileLd, &sm.u.s.scr[0][0][0], kTileLd, lane);
+    st16_f32(t_tile(sm, 2, 0), t2, -1.f, lane);
   } else if (wave == 1) {
     f32x4_t p = {0.f, 0.f, 0.f, 0.f};
-    p = mm16_f32(p, &sm.Lp[tix(3, 1)][0][0], kTileLd, &sm.Tp[tix(1, 1)][0][0], kTileLd, lane);  // L31 T11
-    p = mm16_f32(p, &sm.Lp[tix(3, 2)][0][0], kTileLd, &sm.Tp[tix(2, 1)][0][0], kTileLd, lane);  // L32 T21
-    st16_f32(&sm.scr[1][0][0], p, 1.f, lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 1)][0][0], kTileLd, t_tile(sm, 1, 1), kTileLd, lane);  // L31 T11
+    p = mm16_f32(p, &sm.Lp[tix(3, 2)][0][0], kTileLd, t_tile(sm, 2, 1), kTileLd, lane);  // L32 T21
+    st16_f32(&sm.u.s.scr[1][0][0], p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tp[tix(3, 3)][0][0], kTileLd, &sm.scr[1][0][0], kTileLd, lane);
-    st16_f32(&sm.Tp[tix(3, 1)][0][0], t2, -1.f, lane);
+    t2 = mm16_f32(t2, t_tile(sm, 3, 3), kTileLd, &sm.u.s.scr[1][0][0], kTileLd, lane);
+    st16_f32(t_tile(sm, 3, 1), t2, -1.f, lane);
   } else if (wave == 3) {
-    f32x4_t p = ld16_f32(&sm.scr[3][0][0], lane);
-    p = mm16_f32(p, &sm.Lp[tix(3, 1)][0][0], kTileLd, &sm.Tp[tix(1, 0)][0][0], kTileLd, lane);  // + L31 T10
-    st16_f32(&sm.scr[3][0][0], p, 1.f, lane);
+    f32x4_t p = ld16_f32(&sm.u.s.scr[3][0][0], lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 1)][0][0], kTileLd, t_tile(sm, 1, 0), kTileLd, lane);  // + L31 T10
+    st16_f32(&sm.u.s.scr[3][0][0], p, 1.f, lane);
   }
   __syncthreads();
   // third sub-diagonal: T30
   if (wave == 3) {
-    f32x4_t p = ld16_f32(&sm.scr[3][0][0], lane);
-    p = mm16_f32(p, &sm.Lp[tix(3, 2)][0][0], kTileLd, &sm.Tp[tix(2, 0)][0][0], kTileLd, lane);  // + L32 T20
-    st16_f32(&sm.scr[3][0][0], p, 1.f, lane);
+    f32x4_t p = ld16_f32(&sm.u.s.scr[3][0][0], lane);
+    p = mm16_f32(p, &sm.Lp[tix(3, 2)][0][0], kTileLd, t_tile(sm, 2, 0), kTileLd, lane);  // + L32 T20
+    st16_f32(&sm.u.s.scr[3][0][0], p, 1.f, lane);
     wave_sync();
     f32x4_t t2 = {0.f, 0.f, 0.f, 0.f};
-    t2 = mm16_f32(t2, &sm.Tp[tix(3, 3)][0][0], kTileLd, &sm.scr[3][0][0], kTileLd, lane);
-    st16_f32(&sm.Tp[tix(3, 0)][0][0], t2, -1.f, lane);
+    t2 = mm16_f32(t2, t_tile(sm, 3, 3), kTileLd, &sm.u.s.scr[3][0][0], kTileLd, lane);
+    st16_f32(t_tile(sm, 3, 0), t2, -1.f, lane);
   }
   __syncthreads();
 
@@ -766,8 +787,8 @@ __global__ __launch_bounds__(256, 3) void chunk_prep_kernel(
     const int t = (e >> 3) & 63, gp = e & 7;
     if ((gp >> 2) > (t >> 5)) continue;  // above the diagonal blocks: not stored
     const float* c = which ? sm.bt : sm.cw;
-    const float4 a = t_quad(sm.Tp, c, t, quad_of_pos(2 * gp));
-    const float4 b = t_quad(sm.Tp, c, t, quad_of_pos(2 * gp + 1));
+    const float4 a = t_quad(sm, c, t, quad_of_pos(2 * gp));
+    const float4 b = t_quad(sm, c, t, quad_of_pos(2 * gp + 1));
     uint4 pk;
     pk.x = f2h2(a.x, a.y);
     pk.y = f2h2(a.z, a.w);
