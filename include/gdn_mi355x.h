@@ -151,6 +151,10 @@ int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
  *          gdn_g_beta; no padding mask)
  *   h0, hT, state_ids, state_stride, cu_seqlens, scale, l2norm, o: as
  *          gdn_chunk_prefill
+ *   fresh  uint8 [n_seqs] or NULL: fresh[r] != 0 runs sequence r from zero
+ *          recurrent and conv states without reading its pool rows (the
+ *          reference zeroes a fresh prefill's slot first, model_runner.py:305-322;
+ *          this folds that into the call).  Its final states are written.
  *   workspace: at least gdn_conv_chunk_prefill_workspace_size() bytes,
  *          256-byte aligned (the chunk records, then the conv's v rows)
  * Two launches, as gdn_chunk_prefill: the prep kernel also runs the conv and
@@ -159,7 +163,7 @@ int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
 int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_state, int64_t ss_seq,
                            int64_t ss_ch, const uint16_t* conv_w, const uint16_t* b, const uint16_t* a,
                            const void* A_log, const void* dt_bias, int param_is_fp32, const float* h0,
-                           float* hT, const int64_t* state_ids, int64_t state_stride,
+                           float* hT, const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
                            const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv, int D,
                            float scale, int l2norm, uint16_t* o, void* workspace,
                            int64_t workspace_bytes, void* stream);

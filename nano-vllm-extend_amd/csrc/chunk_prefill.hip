@@ -289,6 +289,7 @@ struct ConvIn {
   const uint16_t* cstate;  // conv state pool: row `slot`, channel c, tap j at
   int64_t ss_seq, ss_ch;   //   cstate + slot*ss_seq + c*ss_ch + j (read here only)
   const int64_t* ids;      // pool rows per sequence (NULL: the sequence index)
+  const uint8_t* fresh;    // per sequence, nonzero: zero initial states, pools not read (NULL: none)
   const uint16_t* w;       // [C, 4] conv taps
   int key_dim;             // Hk * D
   uint16_t* vout;          // [N, Hv, D] conv output of the v channels
@@ -354,6 +355,12 @@ __device__ __forceinline__ void conv_state_halo(ConvRaw<D>& R, const ConvIn& cv,
   constexpr int SEG = D / 8;
   const int c8 = tid % SEG, t0 = ConvRaw<D>::RPT * (tid / SEG);
   if (first && t0 < 3) {
+    if (cv.fresh && cv.fresh[r]) {  // a fresh sequence: zero state
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+        if (t0 + i < 3) R.x[i] = make_uint4(0u, 0u, 0u, 0u);
+      return;
+    }
     const int64_t slot = cv.ids ? cv.ids[r] : r;
     const int ch = conv_part_channel(cv, part, kh, h, D) + 8 * c8;
     const uint16_t* sp = cv.cstate + slot * cv.ss_seq + static_cast<int64_t>(ch) * cv.ss_ch + t0;
@@ -1071,9 +1078,11 @@ struct ConvRoll {
   int ratio;  // Hv / Hk
 };
 
+// (a fresh sequence rolls from a zero state: its old taps are not read)
+
 template <int D>
-__device__ __forceinline__ void conv_roll(const ConvRoll& cr, int64_t slot, int64_t bos, int64_t T, int h, int cb,
-                                          int i0, int nthreads) {
+__device__ __forceinline__ void conv_roll(const ConvRoll& cr, int64_t slot, bool fresh, int64_t bos, int64_t T, int h,
+                                          int cb, int i0, int nthreads) {
   const bool qk = h % cr.ratio == 0;
   const int kh = h / cr.ratio;
   const int ntask = (qk ? 3 : 1) * kCB;
@@ -1086,7 +1095,7 @@ __device__ __forceinline__ void conv_roll(const ConvRoll& cr, int64_t slot, int6
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       const int64_t p = T - 3 + j;
-      val[j] = p >= 0 ? cr.x[(bos + p) * cr.sx + ch] : st[p + 3];
+      val[j] = p >= 0 ? cr.x[(bos + p) * cr.sx + ch] : (fresh ? static_cast<uint16_t>(0) : st[p + 3]);
     }
 #pragma unroll
     for (int j = 0; j < 3; ++j) st[j] = gdn::roll_value(val[j]);
@@ -1103,7 +1112,7 @@ template <int D>
 __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     const uint16_t* __restrict__ v, int64_t sv, const uint8_t* __restrict__ ws, const float* h0, float* hT,
     const int64_t* __restrict__ ids, int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hv,
-    uint16_t* __restrict__ o, ConvRoll cr) {
+    uint16_t* __restrict__ o, ConvRoll cr, const uint8_t* __restrict__ fresh) {
   constexpr int NCB = D / kCB;
   constexpr int NR = D / 32;  // 32-row tiles of the state
   constexpr int KS = D / 16;  // k-steps over keys
@@ -1139,7 +1148,8 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #define GDN_LEN(j_) static_cast<int>(min<int64_t>(kC, seqlen - (j_) * kC))
   if (wave >= 2) {
     // the output waves have two chunk steps before their first product
-    if (cr.x && wave < 4) conv_roll<D>(cr, ids ? ids[r] : r, bos, seqlen, h, cb, threadIdx.x - 128, 128);
+    if (cr.x && wave < 4)
+      conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], bos, seqlen, h, cb, threadIdx.x - 128, 128);
     if (nch == 0) return;
     if (wave < 4) {
       // ------------------------------------------------------------ output --
@@ -1247,7 +1257,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   const int64_t srow = ids ? ids[r] : r;
   const int vc0 = cb * kCB + 32 * wave;  // first state column of this wave
   f32x16_t S[NR];
-  if (h0) {
+  if (h0 && !(fresh && fresh[r])) {
     const float* hp = h0 + srow * sstride + static_cast<int64_t>(h) * D * D + vc0 + li;
 #pragma unroll
     for (int rt = 0; rt < NR; ++rt)
@@ -1382,7 +1392,7 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv * (D / kCB);
   const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
   chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
-      v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr);
+      v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, cv ? cv->fresh : nullptr);
   return gdn_launch_status();
 }
 
@@ -1439,7 +1449,7 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
                                       int64_t ss_seq, int64_t ss_ch, const uint16_t* conv_w,
                                       const uint16_t* b, const uint16_t* a, const void* A_log,
                                       const void* dt_bias, int param_is_fp32, const float* h0, float* hT,
-                                      const int64_t* state_ids, int64_t state_stride,
+                                      const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
                                       const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv,
                                       int D, float scale, int l2norm, uint16_t* o, void* workspace,
                                       int64_t workspace_bytes, void* stream) {
@@ -1460,7 +1470,7 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint16_t* vws = reinterpret_cast<uint16_t*>(ws + fused_v_offset(nc_bound, Hv, D));
-  const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, conv_w, Hk * D, vws, a, b, A_log, dt_bias,
+  const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, fresh, conv_w, Hk * D, vws, a, b, A_log, dt_bias,
                   param_is_fp32 ? 1 : 0};
   const int64_t sv = static_cast<int64_t>(Hv) * D;
   if (D == 128)

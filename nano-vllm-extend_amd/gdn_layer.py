@@ -145,10 +145,12 @@ class GatedDeltaNetCore:
         return self._norm(out.view(B, Hv, D), z.view(B, Hv, D))
 
     # ------------------------------------------------------- varlen prefill --
-    def prefill_varlen(self, mixed, z, b, a, lens_q, ids, conv_cache, s_cache):
+    def prefill_varlen(self, mixed, z, b, a, lens_q, ids, conv_cache, s_cache, fresh=None):
         """Varlen prefill group (_gdn_prefill_varlen, qwen3_5.py:922-965) with the
         conv and recurrent states read / written in the pools at `ids`.
-        mixed [N, C], z [N, Hv*D], b/a [N, Hv].  Returns core [N, Hv, D] bf16."""
+        mixed [N, C], z [N, Hv*D], b/a [N, Hv].  fresh: optional bool [n],
+        sequences that start from zero states (their slots need no zeroing
+        beforehand, model_runner.py:305-322).  Returns core [N, Hv, D] bf16."""
         self._to(mixed.device)
         N = mixed.shape[0]
         Hk, Hv, D = self.Hk, self.Hv, self.D
@@ -158,8 +160,12 @@ class GatedDeltaNetCore:
             cu64_gpu = varlen_meta(lens_q, mixed.device)[3]
             with self._timed("conv_chunk_prefill"):
                 o = ops.conv_chunk_prefill_varlen(mixed, conv_cache, self.conv_w, b, a, self.A_log, self.dt_bias,
-                                                  cu64_gpu, s_cache, ids, Hk, Hv, D)
+                                                  cu64_gpu, s_cache, ids, Hk, Hv, D, fresh=fresh)
             return self._norm(o, z.view(N, Hv, D))
+        if fresh is not None:
+            zero = ids[fresh.to(device=ids.device, dtype=torch.bool)]
+            conv_cache[zero] = 0
+            s_cache[zero] = 0
         g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
         cu_gpu, lens_gpu, _, cu64_gpu = varlen_meta(lens_q, mixed.device)
         if self.sw.conv_kernel:

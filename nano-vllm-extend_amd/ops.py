@@ -251,7 +251,7 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
                               b: torch.Tensor, a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
                               cu_seqlens: torch.Tensor, state: torch.Tensor, state_ids: torch.Tensor | None,
                               num_k_heads: int, num_v_heads: int, head_dim: int,
-                              scale: float | None = None) -> torch.Tensor:
+                              scale: float | None = None, fresh: torch.Tensor | None = None) -> torch.Tensor:
     """Gates, varlen causal conv1d + SiLU and the chunked gated delta rule in
     one call (two kernels), the prefill sequence of _gdn_prefill_varlen
     (nanovllm/models/qwen3_5.py:934-961): the same results as fused_g_beta ->
@@ -262,7 +262,10 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     conv_state [slots, C, 3] bf16 and state [slots, Hv, D, D] fp32 slot pools,
     both read and updated in place at rows state_ids (the sequence index if
     None); conv_weight [C, 4] (or [C, 1, 4]); b, a [N, Hv] bf16; a_log,
-    dt_bias [Hv]; cu_seqlens [n+1] (device).  Returns o [N, Hv, D] bf16."""
+    dt_bias [Hv]; cu_seqlens [n+1] (device).  fresh: optional bool/uint8 [n]:
+    those sequences start from zero recurrent and conv states and their pool
+    rows are not read (the slot zeroing of a fresh prefill,
+    model_runner.py:305-322, folded into the call).  Returns o [N, Hv, D] bf16."""
     dev = _check_cuda(mixed, conv_state, conv_weight, b, a, a_log, dt_bias, cu_seqlens, state, state_ids)
     _bf16(mixed, "mixed")
     _bf16(conv_state, "conv_state")
@@ -293,6 +296,10 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     if state_ids is not None:
         ids = state_ids.to(torch.int64).contiguous()
         assert ids.shape[0] == n
+    fr = None
+    if fresh is not None:
+        fr = fresh.to(device=mixed.device, dtype=torch.uint8).contiguous()
+        assert fr.shape == (n,)
     if scale is None:
         scale = D ** -0.5
     o = torch.empty(N, Hv, D, dtype=torch.bfloat16, device=mixed.device)
@@ -303,7 +310,8 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     _lib.call("gdn_conv_chunk_prefill", _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_state),
               conv_state.stride(0), conv_state.stride(1), _lib.ptr(w), _lib.ptr(b), _lib.ptr(a),
               _lib.ptr(a_log), _lib.ptr(dt_bias), int(a_log.dtype == torch.float32), _lib.ptr(state),
-              _lib.ptr(state), _lib.ptr(ids), state.stride(0), _lib.ptr(cu), n, N, Hk, Hv, D, float(scale), 1,
+              _lib.ptr(state), _lib.ptr(ids), _lib.ptr(fr), state.stride(0), _lib.ptr(cu), n, N, Hk, Hv, D,
+              float(scale), 1,
               _lib.ptr(o), _lib.ptr(ws), ws_bytes, _stream(dev))
     return o
 

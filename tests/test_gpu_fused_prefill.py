@@ -99,3 +99,27 @@ def test_fused_against_oracle(pkg, dev):
     assert_out(o.cpu(), ro.to(BF16), "fused prefill output", ulps=4)
     assert_state(sp.cpu()[ids], rs, "fused prefill state")
     assert torch.equal(cp.cpu()[ids].view(torch.int16), new_conv.view(torch.int16)), "conv pool"
+
+
+@pytest.mark.parametrize("Hk,Hv,D,lens", [(4, 4, 128, [1, 2, 70, 3, 0, 129]), (2, 4, 64, [66, 2, 130])],
+                         ids=lambda c: str(c))
+def test_fresh_flags_equal_zeroed_slots(pkg, dev, Hk, Hv, D, lens):
+    """Sequences flagged fresh start from zero states without reading their
+    pool rows: the same results, bit for bit, as zeroing those slots first."""
+    slots = len(lens) + 2
+    C, mixed, conv_w, A_log, dt_bias, a, b, conv_pool, s_pool, ids = _case(43, Hk, Hv, D, lens, slots)
+    fresh = torch.tensor([i % 2 == 0 for i in range(len(lens))])
+    mixed, conv_w, A_log, dt_bias, a, b, ids = (t.to(dev) for t in (mixed, conv_w, A_log, dt_bias, a, b, ids))
+    cp_f, sp_f = conv_pool.to(dev), s_pool.to(dev)               # stale contents in the fresh slots
+    o_f = pkg.ops.conv_chunk_prefill_varlen(mixed, cp_f, conv_w, b, a, A_log, dt_bias, _cu(lens, dev), sp_f,
+                                            ids, Hk, Hv, D, fresh=fresh)
+    cp_z, sp_z = conv_pool.to(dev), s_pool.to(dev)
+    zero = ids[fresh.to(dev)]
+    cp_z[zero] = 0
+    sp_z[zero] = 0
+    o_z = pkg.ops.conv_chunk_prefill_varlen(mixed, cp_z, conv_w, b, a, A_log, dt_bias, _cu(lens, dev), sp_z,
+                                            ids, Hk, Hv, D)
+    torch.cuda.synchronize()
+    assert torch.equal(o_f.view(torch.int16), o_z.view(torch.int16)), "outputs differ"
+    assert torch.equal(sp_f, sp_z), "state pool differs"
+    assert torch.equal(cp_f.view(torch.int16), cp_z.view(torch.int16)), "conv pool differs"
