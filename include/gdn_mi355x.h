@@ -105,6 +105,15 @@ int gdn_conv_padded(const uint16_t* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
  *   g     [N, Hv] fp32 contiguous; beta [N, Hv] bf16 contiguous
  *   value head h reads key head h / (Hv / Hk)   (grouped-value layout)
  *   cu_seqlens int64 [n_seqs + 1] (device)
+ *   cu_seqlens_host  the same offsets in host memory, or NULL.  With them,
+ *         when few workgroups would otherwise run (n_seqs * Hv * D/64 < 128),
+ *         long sequences are cut into segments that run in parallel: the
+ *         first segment from h0; each middle one as its zero-start result R
+ *         and its transition P (the recurrence on the identity's columns);
+ *         a scan S_{s+1} = P_s S_s + R_s (fp32); then the later segments
+ *         again with outputs.  Same results up to rounding.
+ *   max_segments  0 = automatic (segments of >= 16 chunks), 1 = never split,
+ *         k >= 2 = up to k (at most 12) segments per sequence
  *   h0    initial state of sequence r at h0 + row(r)*state_stride, [Hv, D, D]
  *         fp32 dense; NULL = zero state.  hT likewise receives the final
  *         state (NULL = not written); row(r) = state_ids ? state_ids[r] : r.
@@ -115,9 +124,9 @@ int gdn_conv_padded(const uint16_t* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
  *   workspace: device buffer of at least gdn_chunk_prefill_workspace_size()
  *         bytes, 256-byte aligned, owned by the caller.  It receives one
  *         record of 19 KiB + 256 D bytes per (chunk, value head) from the
- *         first launch; contents need no initialisation and are dead after
- *         the call.
- * D must be 64 or 128.  Two launches on `stream`: a prep kernel over all
+ *         first launch, then (segmented calls) the segment states; contents
+ *         need no initialisation and are dead after the call.
+ * D must be 64 or 128.  Two launches on `stream` (four when segmented): a prep kernel over all
  * chunks in parallel (row norms, K^T, K K^T, Q K^T, the triangular inverse),
  * then a state kernel per (sequence, value head, 64 value columns) that walks
  * the chunks in order with its state slice in registers (fp16 matrix-core
@@ -126,7 +135,8 @@ int gdn_conv_padded(const uint16_t* x, int64_t sx_n, int64_t sx_c, int64_t sx_t,
 int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k, int64_t sk_tok,
                       const uint16_t* v, int64_t sv_tok, const float* g, const uint16_t* beta,
                       const float* h0, float* hT, const int64_t* state_ids, int64_t state_stride,
-                      const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv, int D,
+                      const int64_t* cu_seqlens, const int64_t* cu_seqlens_host, int max_segments,
+                      int n_seqs, int64_t N, int Hk, int Hv, int D,
                       float scale, int l2norm, uint16_t* o, void* workspace,
                       int64_t workspace_bytes, void* stream);
 
@@ -149,8 +159,8 @@ int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
  *          as the recurrent state's
  *   b, a   [N, Hv] bf16 contiguous; A_log, dt_bias [Hv] (param_is_fp32 as
  *          gdn_g_beta; no padding mask)
- *   h0, hT, state_ids, state_stride, cu_seqlens, scale, l2norm, o: as
- *          gdn_chunk_prefill
+ *   h0, hT, state_ids, state_stride, cu_seqlens, cu_seqlens_host, max_segments,
+ *          scale, l2norm, o: as gdn_chunk_prefill
  *   fresh  uint8 [n_seqs] or NULL: fresh[r] != 0 runs sequence r from zero
  *          recurrent and conv states without reading its pool rows (the
  *          reference zeroes a fresh prefill's slot first, model_runner.py:305-322;
@@ -164,7 +174,8 @@ int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_sta
                            int64_t ss_ch, const uint16_t* conv_w, const uint16_t* b, const uint16_t* a,
                            const void* A_log, const void* dt_bias, int param_is_fp32, const float* h0,
                            float* hT, const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
-                           const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv, int D,
+                           const int64_t* cu_seqlens, const int64_t* cu_seqlens_host, int max_segments,
+                           int n_seqs, int64_t N, int Hk, int Hv, int D,
                            float scale, int l2norm, uint16_t* o, void* workspace,
                            int64_t workspace_bytes, void* stream);
 

@@ -49,6 +49,8 @@
 // fp16 tiles in LDS and in the record are row-major with 16-byte granules
 // XOR-swizzled by row (swz), so 16 lanes reading one granule column of 16
 // rows hit 16 distinct bank groups.
+#include <algorithm>
+
 #include "gdn_common.h"
 
 namespace {
@@ -1102,8 +1104,33 @@ __device__ __forceinline__ void conv_roll(const ConvRoll& cr, int64_t slot, bool
   }
 }
 
-// grid = 8 * ceil(n_seqs * Hv * NCB / 8), NCB = D / 64; block = 64 * 8.
-// Workgroup (sequence r, value head h, column block cb) owns state columns
+// Segments of long sequences.  The state after chunk j is linear in the
+// state before it: S' = A_j S + B_j with A_j = e^gamma I - K^T diag(cK) W and
+// B_j = K^T diag(cK) U.  Over chunks [c0, c1) that gives S_c1 = P S_c0 + R,
+// where R is the recurrence run from S = 0 and P the recurrence run on the
+// identity's columns with U = 0.  A long sequence is cut into segments: the
+// first runs as usual (outputs, from h0) and ends in the second's initial
+// state; each middle segment runs twice, as R and as P, in parallel with the
+// first; a scan S_{s+1} = P_s S_s + R_s gives every later segment its initial
+// state; then those segments run again with outputs, all in parallel.
+constexpr int kSegOut = 0;         // outputs; state from h0 (NULL: zero), final to hT
+constexpr int kSegState = 1;       // no outputs; state from h0 (NULL: zero), final to hT
+constexpr int kSegTransition = 2;  // no outputs, U = 0, state from the identity's columns
+constexpr int kMaxSegItems = 64;
+
+struct SegItem {
+  int r, c0, c1, mode;  // sequence r, its chunks [c0, c1)
+  int pool_h0, pool_hT; // nonzero: the state at the sequence's pool row (kernel arguments h0 / hT)
+  const float* h0;      // else [Hv, D, D] initial state of the item (NULL: zero)
+  float* hT;            // else [Hv, D, D] final state (NULL: not stored)
+};
+struct SegList {
+  int n;  // 0: one item per sequence, states at the pool rows (the plain launch)
+  SegItem it[kMaxSegItems];
+};
+
+// grid = 8 * ceil(n_items * Hv * NCB / 8), NCB = D / 64; block = 64 * 8.
+// Workgroup (item: sequence r or a segment of it, value head h, column block cb) owns state columns
 // cb*64 .. cb*64 + 63.  One workgroup barrier per chunk j: before it the
 // chain consumes stage j % 2 and writes exchange j % 2, the K and U waves fill
 // stage (j + 1) % 2, and the output waves read exchange (j - 1) % 2.  No wave
@@ -1112,21 +1139,51 @@ template <int D>
 __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     const uint16_t* __restrict__ v, int64_t sv, const uint8_t* __restrict__ ws, const float* h0, float* hT,
     const int64_t* __restrict__ ids, int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hv,
-    uint16_t* __restrict__ o, ConvRoll cr, const uint8_t* __restrict__ fresh) {
+    uint16_t* __restrict__ o, ConvRoll cr, const uint8_t* __restrict__ fresh, SegList segs) {
   constexpr int NCB = D / kCB;
   constexpr int NR = D / 32;  // 32-row tiles of the state
   constexpr int KS = D / 16;  // k-steps over keys
   __shared__ StateSmem<D> sm;
   __shared__ long long s_base;
 
-  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(n_seqs) * Hv * NCB);
+  const int64_t n_items = segs.n ? segs.n : n_seqs;
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, n_items * Hv * NCB);
   if (wi < 0) return;
   const int cb = static_cast<int>(wi % NCB);
   const int h = static_cast<int>((wi / NCB) % Hv);
-  const int r = static_cast<int>(wi / (static_cast<int64_t>(NCB) * Hv));
-  const int64_t bos = cu[r];
-  const int64_t seqlen = cu[r + 1] - bos;
-  const int64_t nch = chunks_of(seqlen);
+  const int item = static_cast<int>(wi / (static_cast<int64_t>(NCB) * Hv));
+  int r, mode;
+  int64_t c0;
+  int64_t nch;  // chunks of the item
+  const float* ih0;
+  float* ihT;
+  const int64_t seq_bos = segs.n ? cu[segs.it[item].r] : cu[item];
+  const int64_t seq_len = (segs.n ? cu[segs.it[item].r + 1] : cu[item + 1]) - seq_bos;
+  {
+    int pool_h0 = 1, pool_hT = 1;
+    if (segs.n) {
+      const SegItem& it = segs.it[item];
+      r = it.r;
+      c0 = it.c0;
+      nch = it.c1 - it.c0;
+      mode = it.mode;
+      pool_h0 = it.pool_h0;
+      pool_hT = it.pool_hT;
+      ih0 = it.h0;
+      ihT = it.hT;
+    } else {
+      r = item;
+      c0 = 0;
+      nch = chunks_of(seq_len);
+      mode = kSegOut;
+    }
+    const int64_t srow = ids ? ids[r] : r;
+    if (pool_h0) ih0 = h0 && !(fresh && fresh[r]) ? h0 + srow * sstride : nullptr;
+    if (pool_hT) ihT = hT ? hT + srow * sstride : nullptr;
+  }
+  // the item's tokens
+  const int64_t bos = seq_bos + c0 * kC;
+  const int64_t seqlen = min<int64_t>(seq_len - c0 * kC, nch * kC);
 
   // first workspace chunk of this sequence: sum of earlier sequences' chunks
   if (threadIdx.x < 64) {
@@ -1137,7 +1194,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     if (threadIdx.x == 0) s_base = part;
   }
   __syncthreads();
-  const int64_t cbase = s_base;
+  const int64_t cbase = s_base + c0;
   const int64_t rec_stride = static_cast<int64_t>(Hv) * rec_bytes(D);
   const uint8_t* rec0 = ws + cbase * rec_stride + static_cast<int64_t>(h) * rec_bytes(D);
 
@@ -1147,10 +1204,17 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 
 #define GDN_LEN(j_) static_cast<int>(min<int64_t>(kC, seqlen - (j_) * kC))
   if (wave >= 2) {
-    // the output waves have two chunk steps before their first product
-    if (cr.x && wave < 4)
-      conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], bos, seqlen, h, cb, threadIdx.x - 128, 128);
+    // the output waves have two chunk steps before their first product; one
+    // item per sequence (its first chunk, with outputs) rolls the conv state
+    if (cr.x && wave < 4 && c0 == 0 && mode == kSegOut)
+      conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], seq_bos, seq_len, h, cb, threadIdx.x - 128, 128);
     if (nch == 0) return;
+    // roles with nothing to do for this item keep the chain's barrier count
+    // (one before the first chunk, one per chunk)
+    if ((wave < 4 && mode != kSegOut) || (wave >= 4 && wave < 6 && mode == kSegTransition)) {
+      for (int64_t i = 0; i <= nch; ++i) gdn::lds_barrier();
+      return;
+    }
     if (wave < 4) {
       // ------------------------------------------------------------ output --
       // Chunk c's operands live in register set c % 2; its loads go out right
@@ -1254,11 +1318,19 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #undef GDN_LEN
 
   // -------------------------------------------------------------- chain --
-  const int64_t srow = ids ? ids[r] : r;
   const int vc0 = cb * kCB + 32 * wave;  // first state column of this wave
   f32x16_t S[NR];
-  if (h0 && !(fresh && fresh[r])) {
-    const float* hp = h0 + srow * sstride + static_cast<int64_t>(h) * D * D + vc0 + li;
+  if (mode == kSegTransition) {
+    // the identity's columns vc0 + li (row position p holds key qswap(p))
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          S[rt][4 * i + rr] = qswap(32 * rt + 8 * i + 4 * g + rr) == vc0 + li ? 1.f : 0.f;
+  } else if (ih0) {
+    const float* hp = ih0 + static_cast<int64_t>(h) * D * D + vc0 + li;
 #pragma unroll
     for (int rt = 0; rt < NR; ++rt)
 #pragma unroll
@@ -1303,7 +1375,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
         for (int qd = 0; qd < 4; ++qd) {
           const f32x4_t u4 = B.U[wave][mt][qd][ln];
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = u4[rr];
+          for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = mode == kSegTransition ? 0.f : u4[rr];
         }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1358,8 +1430,8 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     gdn::lds_barrier();
   }
 
-  if (hT) {
-    float* hp = hT + srow * sstride + static_cast<int64_t>(h) * D * D + vc0 + li;
+  if (ihT) {
+    float* hp = ihT + static_cast<int64_t>(h) * D * D + vc0 + li;
 #pragma unroll
     for (int rt = 0; rt < NR; ++rt)
 #pragma unroll
@@ -1370,12 +1442,129 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   }
 }
 
+// ---- segment scan ----
+// For each split sequence: S_1 = the first segment's final state, then
+// S_{s+1} = P_s S_s + R_s for its middle segments s = 1 .. m, in fp32 (the
+// sum over keys in order).  States are [Hv, D, D] (row = key).
+constexpr int kMaxSeg = 12;     // segments per sequence
+constexpr int kMaxChains = 16;  // split sequences per call
+struct ScanChain {
+  float* S;        // [m + 1][Hv, D, D]: S_1 (read), S_2 .. S_{m+1} (written)
+  const float* P;  // [m][Hv, D, D]: P_1 .. P_m
+  const float* R;  // [m][Hv, D, D]: R_1 .. R_m
+  int m;
+};
+struct ScanList {
+  int n;
+  ScanChain c[kMaxChains];
+};
+
+// grid = n_chains * Hv * D / 16, block = 256: workgroup (chain, head, 16 state
+// columns); thread = one key row, OPT consecutive columns.
+template <int D>
+__global__ __launch_bounds__(256) void seg_scan_kernel(ScanList sl, int Hv) {
+  constexpr int CB = 16;
+  constexpr int NB = D / CB;
+  constexpr int OPT = D * CB / 256;  // outputs per thread: 8 or 4
+  constexpr int TPR = CB / OPT;      // threads per row
+  __shared__ __align__(16) float Ss[D][CB];
+  const int blk = blockIdx.x % NB;
+  const int h = (blockIdx.x / NB) % Hv;
+  const int ci = blockIdx.x / (NB * Hv);
+  if (ci >= sl.n) return;
+  const ScanChain& c = sl.c[ci];
+  const int64_t hs = static_cast<int64_t>(Hv) * D * D;  // one state
+  const int64_t ho = static_cast<int64_t>(h) * D * D;
+  const int k = threadIdx.x / TPR, col = (threadIdx.x % TPR) * OPT;
+  const int64_t off = ho + static_cast<int64_t>(k) * D + blk * CB + col;
+#pragma unroll
+  for (int o = 0; o < OPT; ++o) Ss[k][col + o] = c.S[off + o];
+  __syncthreads();
+  for (int s = 0; s < c.m; ++s) {
+    float acc[OPT];
+#pragma unroll
+    for (int o = 0; o < OPT; ++o) acc[o] = c.R[s * hs + off + o];
+    const float4* prow = reinterpret_cast<const float4*>(c.P + s * hs + ho + static_cast<int64_t>(k) * D);
+    for (int m4 = 0; m4 < D / 4; ++m4) {
+      const float4 p4 = prow[m4];
+      const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int o = 0; o < OPT; ++o) acc[o] = fmaf(pv[e], Ss[4 * m4 + e][col + o], acc[o]);
+    }
+    __syncthreads();  // every row of S_s is read
+#pragma unroll
+    for (int o = 0; o < OPT; ++o) {
+      Ss[k][col + o] = acc[o];
+      c.S[(s + 1) * hs + off + o] = acc[o];
+    }
+    __syncthreads();
+  }
+}
+
+// Segment plan of one call: how many segments each sequence is cut into.
+// Only when few workgroups would run otherwise (n_seqs * Hv * NCB < 128) and
+// the host knows the lengths.  max_segments: 0 = automatic (segments of at
+// least 16 chunks, at most one workgroup per CU in the second pass), 1 =
+// never, k >= 2 = up to k segments per sequence.
+inline bool seg_eligible(int n_seqs, int Hv, int D) { return static_cast<int64_t>(n_seqs) * Hv * (D / kCB) < 128; }
+
+// scratch bytes for the segment states of one call (an upper bound)
+inline int64_t seg_scratch_bytes(int n_seqs, int Hv, int D) {
+  if (!seg_eligible(n_seqs, Hv, D)) return 0;
+  return static_cast<int64_t>(n_seqs) * (3 * kMaxSeg - 5) * Hv * D * D * 4;
+}
+
+struct SegPlan {
+  int nseg[kMaxChains * 4];  // per sequence (<= 3 sequences eligible at Hv = 16)
+  int len[kMaxChains * 4];   // chunks per segment
+  bool any = false;
+};
+
+inline SegPlan plan_segments(const int64_t* cu_host, int n_seqs, int Hv, int D, int max_segments) {
+  SegPlan pl;
+  if (!cu_host || max_segments == 1 || !seg_eligible(n_seqs, Hv, D) || n_seqs > kMaxChains * 4) return pl;
+  const int per_item = Hv * (D / kCB);
+  int pass1 = 0, pass3 = 0, chains = 0;
+  for (int r = 0; r < n_seqs; ++r) {
+    const int64_t nch = (cu_host[r + 1] - cu_host[r] + kC - 1) / kC;
+    int S = 1;
+    if (max_segments >= 2) {
+      S = static_cast<int>(std::min<int64_t>(std::min(max_segments, kMaxSeg), nch));
+    } else if (nch >= 32) {
+      S = static_cast<int>(std::min<int64_t>(std::min(kMaxSeg, 256 / (per_item * n_seqs) + 1), nch / 16));
+    }
+    int L = 1;
+    if (S >= 2) {
+      L = static_cast<int>((nch + S - 1) / S);
+      S = static_cast<int>((nch + L - 1) / L);  // no empty last segment
+    }
+    if (S >= 2 && (chains + (S >= 3) > kMaxChains || pass1 + 2 * S - 3 > kMaxSegItems ||
+                   pass3 + S - 1 > kMaxSegItems))
+      S = 1;
+    if (S < 2) {
+      S = 1;
+      pass1 += 1;
+    } else {
+      pass1 += 2 * S - 3;
+      pass3 += S - 1;
+      chains += S >= 3;
+      pl.any = true;
+    }
+    if (pass1 > kMaxSegItems) return SegPlan{};
+    pl.nseg[r] = S;
+    pl.len[r] = L;
+  }
+  return pl;
+}
+
 template <int D>
 int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, const uint16_t* v,
                  int64_t sv, const float* g, const uint16_t* beta, const float* h0, float* hT,
-                 const int64_t* ids, int64_t sstride, const int64_t* cu, int n_seqs, int64_t nc_bound,
-                 int Hk, int Hv, float scale, int l2norm, uint16_t* o, uint8_t* ws, const ConvIn* cv,
-                 hipStream_t stream) {
+                 const int64_t* ids, int64_t sstride, const int64_t* cu, const int64_t* cu_host, int max_segments,
+                 int n_seqs, int64_t nc_bound, int Hk, int Hv, float scale, int l2norm, uint16_t* o, uint8_t* ws,
+                 uint8_t* seg_ws, const ConvIn* cv, hipStream_t stream) {
   const int64_t lwork = nc_bound * Hv;
   const int64_t lgrid = gdn::kNumXcd * ((lwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
   ConvRoll cr{};
@@ -1387,13 +1576,74 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
     chunk_prep_kernel<D, false><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
         q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, ConvIn{});
   }
-  const int st = gdn_launch_status();
+  int st = gdn_launch_status();
   if (st != GDN_OK) return st;
-  const int64_t cwork = static_cast<int64_t>(n_seqs) * Hv * (D / kCB);
-  const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
-      v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, cv ? cv->fresh : nullptr);
-  return gdn_launch_status();
+  const uint8_t* fresh = cv ? cv->fresh : nullptr;
+  const int per_item = Hv * (D / kCB);
+  auto state_launch = [&](const SegList& sl, int64_t items) {
+    const int64_t cwork = items * per_item;
+    const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
+    chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
+        v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
+    return gdn_launch_status();
+  };
+  const SegPlan pl = plan_segments(cu_host, n_seqs, Hv, D, max_segments);
+  if (!pl.any || !seg_ws) {
+    SegList none;
+    none.n = 0;
+    return state_launch(none, n_seqs);
+  }
+  // segment states: per split sequence S_1 .. S_{m+1}, P_1 .. P_m, R_1 .. R_m
+  const int64_t hs = static_cast<int64_t>(Hv) * D * D;
+  float* scratch = reinterpret_cast<float*>(seg_ws);
+  SegList p1, p3;
+  p1.n = 0;
+  p3.n = 0;
+  ScanList sc;
+  sc.n = 0;
+  auto item = [](int r, int64_t a, int64_t b, int mode, int ph0, int phT, const float* i0, float* iT) {
+    SegItem it;
+    it.r = r;
+    it.c0 = static_cast<int>(a);
+    it.c1 = static_cast<int>(b);
+    it.mode = mode;
+    it.pool_h0 = ph0;
+    it.pool_hT = phT;
+    it.h0 = i0;
+    it.hT = iT;
+    return it;
+  };
+  for (int r = 0; r < n_seqs; ++r) {
+    const int S = pl.nseg[r];
+    const int64_t L = pl.len[r];
+    const int64_t nch = (cu_host[r + 1] - cu_host[r] + kC - 1) / kC;
+    if (S < 2) {
+      p1.it[p1.n++] = item(r, 0, nch, kSegOut, 1, 1, nullptr, nullptr);
+      continue;
+    }
+    const int m = S - 2;
+    float* Sst = scratch;  // S_1 .. S_{m+1}
+    float* P = Sst + (m + 1) * hs;
+    float* R = P + m * hs;
+    scratch = R + m * hs;
+    p1.it[p1.n++] = item(r, 0, L, kSegOut, 1, 0, nullptr, Sst);
+    for (int s = 1; s <= m; ++s) {
+      p1.it[p1.n++] = item(r, s * L, (s + 1) * L, kSegState, 0, 0, nullptr, R + (s - 1) * hs);
+      p1.it[p1.n++] = item(r, s * L, (s + 1) * L, kSegTransition, 0, 0, nullptr, P + (s - 1) * hs);
+    }
+    for (int s = 1; s < S; ++s)
+      p3.it[p3.n++] = item(r, s * L, std::min<int64_t>((s + 1) * L, nch), kSegOut, 0, s == S - 1, Sst + (s - 1) * hs,
+                           nullptr);
+    if (m > 0) sc.c[sc.n++] = ScanChain{Sst, P, R, m};
+  }
+  st = state_launch(p1, p1.n);
+  if (st != GDN_OK) return st;
+  if (sc.n) {
+    seg_scan_kernel<D><<<dim3(static_cast<unsigned>(sc.n * Hv * (D / 16))), dim3(256), 0, stream>>>(sc, Hv);
+    st = gdn_launch_status();
+    if (st != GDN_OK) return st;
+  }
+  return state_launch(p3, p3.n);
 }
 
 }  // namespace
@@ -1401,14 +1651,15 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
 extern "C" int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D) {
   if (N < 0 || n_seqs < 0 || Hv <= 0 || (D != 64 && D != 128)) return -1;
   const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
-  return nc_bound * Hv * rec_bytes(D);
+  return nc_bound * Hv * rec_bytes(D) + seg_scratch_bytes(n_seqs, Hv, D);
 }
 
 extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k,
                                  int64_t sk_tok, const uint16_t* v, int64_t sv_tok, const float* g,
                                  const uint16_t* beta, const float* h0, float* hT,
                                  const int64_t* state_ids, int64_t state_stride,
-                                 const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv,
+                                 const int64_t* cu_seqlens, const int64_t* cu_seqlens_host, int max_segments,
+                                 int n_seqs, int64_t N, int Hk, int Hv,
                                  int D, float scale, int l2norm, uint16_t* o, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
@@ -1425,24 +1676,32 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
       reinterpret_cast<uintptr_t>(workspace) % 256 ||
       ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
     return GDN_ERR_INVALID_ARG;
+  if (max_segments < 0) return GDN_ERR_INVALID_ARG;
   const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
-  if (workspace_bytes < nc_bound * Hv * rec_bytes(D)) return GDN_ERR_INVALID_ARG;
+  if (workspace_bytes < gdn_chunk_prefill_workspace_size(N, n_seqs, Hv, D)) return GDN_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint8_t* seg_ws = seg_scratch_bytes(n_seqs, Hv, D) ? ws + nc_bound * Hv * rec_bytes(D) : nullptr;
   if (D == 128)
     return launch_chunk<128>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
-                             cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, nullptr, s);
+                             cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm,
+                             o, ws, seg_ws, nullptr, s);
   return launch_chunk<64>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
-                          cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, nullptr, s);
+                          cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
+                          ws, seg_ws, nullptr, s);
 }
 
 // workspace of the fused entry point: the records, then the conv's v rows
 static int64_t fused_v_offset(int64_t nc_bound, int Hv, int D) { return nc_bound * Hv * rec_bytes(D); }
 
+static int64_t fused_seg_offset(int64_t N, int64_t nc_bound, int Hv, int D) {
+  return fused_v_offset(nc_bound, Hv, D) + ((N * Hv * D * 2 + 255) / 256) * 256;
+}
+
 extern "C" int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D) {
   if (N < 0 || n_seqs < 0 || Hv <= 0 || (D != 64 && D != 128)) return -1;
   const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
-  return fused_v_offset(nc_bound, Hv, D) + ((N * Hv * D * 2 + 255) / 256) * 256;
+  return fused_seg_offset(N, nc_bound, Hv, D) + seg_scratch_bytes(n_seqs, Hv, D);
 }
 
 extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_state,
@@ -1450,7 +1709,8 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
                                       const uint16_t* b, const uint16_t* a, const void* A_log,
                                       const void* dt_bias, int param_is_fp32, const float* h0, float* hT,
                                       const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
-                                      const int64_t* cu_seqlens, int n_seqs, int64_t N, int Hk, int Hv,
+                                      const int64_t* cu_seqlens, const int64_t* cu_seqlens_host,
+                                      int max_segments, int n_seqs, int64_t N, int Hk, int Hv,
                                       int D, float scale, int l2norm, uint16_t* o, void* workspace,
                                       int64_t workspace_bytes, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
@@ -1458,6 +1718,7 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   if (n_seqs == 0) return GDN_OK;
   if (!x || !conv_state || !conv_w || !a || !b || !A_log || !dt_bias || !cu_seqlens || !o || !workspace)
     return GDN_ERR_INVALID_ARG;
+  if (max_segments < 0) return GDN_ERR_INVALID_ARG;
   const int64_t C = 2LL * Hk * D + static_cast<int64_t>(Hv) * D;
   // 16-byte row segments of x, 8-byte output pieces, 256-byte workspace records
   if (sx_row % 8 || sx_row < C || reinterpret_cast<uintptr_t>(x) % 16 ||
@@ -1473,9 +1734,12 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, fresh, conv_w, Hk * D, vws, a, b, A_log, dt_bias,
                   param_is_fp32 ? 1 : 0};
   const int64_t sv = static_cast<int64_t>(Hv) * D;
+  uint8_t* seg_ws = seg_scratch_bytes(n_seqs, Hv, D) ? ws + fused_seg_offset(N, nc_bound, Hv, D) : nullptr;
   if (D == 128)
     return launch_chunk<128>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
-                             cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, &cv, s);
+                             cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm,
+                             o, ws, seg_ws, &cv, s);
   return launch_chunk<64>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
-                          cu_seqlens, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o, ws, &cv, s);
+                          cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
+                          ws, seg_ws, &cv, s);
 }

@@ -157,17 +157,18 @@ class GatedDeltaNetCore:
         if self.sw.fused_prefill and self.sw.gbeta and self.sw.conv_kernel and self.K == 4:
             # gates + conv + chunk rule in one call (the same results as the
             # three calls below)
-            cu64_gpu = varlen_meta(lens_q, mixed.device)[3]
+            _, _, cu64_cpu, cu64_gpu = varlen_meta(lens_q, mixed.device)
             with self._timed("conv_chunk_prefill"):
                 o = ops.conv_chunk_prefill_varlen(mixed, conv_cache, self.conv_w, b, a, self.A_log, self.dt_bias,
-                                                  cu64_gpu, s_cache, ids, Hk, Hv, D, fresh=fresh)
+                                                  cu64_gpu, s_cache, ids, Hk, Hv, D, fresh=fresh,
+                                                  cu_seqlens_cpu=cu64_cpu)
             return self._norm(o, z.view(N, Hv, D))
         if fresh is not None:
             zero = ids[fresh.to(device=ids.device, dtype=torch.bool)]
             conv_cache[zero] = 0
             s_cache[zero] = 0
         g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
-        cu_gpu, lens_gpu, _, cu64_gpu = varlen_meta(lens_q, mixed.device)
+        cu_gpu, lens_gpu, cu64_cpu, cu64_gpu = varlen_meta(lens_q, mixed.device)
         if self.sw.conv_kernel:
             with self._timed("conv_varlen"):
                 q, k, v = ops.causal_conv_silu_varlen_parts(mixed, conv_cache, self.conv_w, lens_gpu, cu_gpu[:-1],
@@ -177,7 +178,7 @@ class GatedDeltaNetCore:
         with self._timed("chunk_prefill"):
             o, _ = ops.chunk_gated_delta_rule_varlen(q.view(N, Hk, D), k.view(N, Hk, D), v.view(N, Hv, D),
                                                      g, beta, cu64_gpu, s_cache, state_ids=ids,
-                                                     final_state=s_cache)
+                                                     final_state=s_cache, cu_seqlens_cpu=cu64_cpu)
         return self._norm(o, z.view(N, Hv, D))
 
     def _conv_varlen_eager(self, mixed, lens_q, ids, conv_cache):

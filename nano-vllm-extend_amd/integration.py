@@ -58,10 +58,11 @@ def _fused_prefill_method(mod, orig):
         dt_bias = self.dt_bias[self._v_head_slice]
         z = self.in_proj_z(hidden)
         mixed = self.in_proj_qkv(hidden)
-        cu64_gpu = mod._varlen_meta(lens_q)[3]
+        _, _, cu64_cpu, cu64_gpu = mod._varlen_meta(lens_q)
         core = ops.conv_chunk_prefill_varlen(
             mixed, self.conv_cache, self.conv1d.weight.view(self.conv_dim, self.conv_kernel), b, a, A_log, dt_bias,
-            cu64_gpu, self.s_cache, ids, self.num_k_heads, self.num_v_heads, self.head_k_dim)
+            cu64_gpu, self.s_cache, ids, self.num_k_heads, self.num_v_heads, self.head_k_dim,
+            cu_seqlens_cpu=cu64_cpu)
         core = self.norm(core, z.view(-1, self.num_v_heads, self.head_v_dim))
         return self.out_proj(core.reshape(-1, self.value_dim))
 

@@ -165,6 +165,23 @@ def causal_conv_silu(x: torch.Tensor, state: torch.Tensor, weight: torch.Tensor,
 
 
 # -------------------------------------------------------------- chunk rule --
+def _host_offsets(cu_cpu, n: int):
+    """int64 host copy of the sequence offsets [n + 1], or None."""
+    if cu_cpu is None:
+        return None
+    t = torch.as_tensor(cu_cpu)
+    if t.device.type != "cpu":
+        raise ValueError("cu_seqlens_cpu must be in host memory")
+    t = t.to(torch.int64).contiguous()
+    assert t.shape == (n + 1,)
+    return t
+
+
+def _host_ptr(t):
+    """Host pointer of a CPU tensor (the caller keeps the tensor alive)."""
+    return None if t is None else t.data_ptr()
+
+
 def _state_view_ok(s: torch.Tensor, H: int, D: int) -> bool:
     return (s.dtype == torch.float32 and s.dim() == 4 and tuple(s.shape[1:]) == (H, D, D)
             and s.stride(1) == D * D and s.stride(2) == D and s.stride(3) == 1)
@@ -182,7 +199,8 @@ def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
                                   output_final_state: bool = True,
                                   use_qk_l2norm_in_kernel: bool = True, scale: float | None = None,
                                   state_ids: torch.Tensor | None = None,
-                                  final_state: torch.Tensor | None = None):
+                                  final_state: torch.Tensor | None = None,
+                                  cu_seqlens_cpu: torch.Tensor | None = None, max_segments: int = 0):
     """Varlen chunked gated delta rule (chunk 64) on packed rows.
 
     q, k [N, Hk, D]; v [N, Hv, D] (bf16, head dim contiguous, any token
@@ -192,6 +210,9 @@ def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     [slots, Hv, D, D] (any slot stride) read at rows state_ids.
     Final states go to `final_state` (same indexing; may be the pool itself
     for an in-place update) or to a new [n, Hv, D, D] tensor.
+    cu_seqlens_cpu: the offsets on the host (as the fla call passes them);
+    with them a call of few long sequences is cut into segments that run in
+    parallel (max_segments: 0 automatic, 1 never, k up to k per sequence).
     Returns (o [N, Hv, D] bf16, final or None)."""
     dev = _check_cuda(q, k, v, g, beta, cu_seqlens, initial_state, state_ids, final_state)
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
@@ -240,10 +261,11 @@ def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     if ws_bytes < 0:
         raise ValueError(f"unsupported chunk shape N={N} n_seqs={n} Hv={Hv} D={D}")
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    cu_host = _host_offsets(cu_seqlens_cpu, n)
     _lib.call("gdn_chunk_prefill", _lib.ptr(q), q.stride(0), _lib.ptr(k), k.stride(0), _lib.ptr(v),
               v.stride(0), _lib.ptr(g), _lib.ptr(beta), _lib.ptr(h0), _lib.ptr(hT), _lib.ptr(ids),
-              sstride, _lib.ptr(cu), n, N, Hk, Hv, D, float(scale), int(bool(use_qk_l2norm_in_kernel)),
-              _lib.ptr(o), _lib.ptr(ws), ws_bytes, _stream(dev))
+              sstride, _lib.ptr(cu), _host_ptr(cu_host), int(max_segments), n, N, Hk, Hv, D, float(scale),
+              int(bool(use_qk_l2norm_in_kernel)), _lib.ptr(o), _lib.ptr(ws), ws_bytes, _stream(dev))
     return o, hT
 
 
@@ -251,7 +273,8 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
                               b: torch.Tensor, a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
                               cu_seqlens: torch.Tensor, state: torch.Tensor, state_ids: torch.Tensor | None,
                               num_k_heads: int, num_v_heads: int, head_dim: int,
-                              scale: float | None = None, fresh: torch.Tensor | None = None) -> torch.Tensor:
+                              scale: float | None = None, fresh: torch.Tensor | None = None,
+                              cu_seqlens_cpu: torch.Tensor | None = None, max_segments: int = 0) -> torch.Tensor:
     """Gates, varlen causal conv1d + SiLU and the chunked gated delta rule in
     one call (two kernels), the prefill sequence of _gdn_prefill_varlen
     (nanovllm/models/qwen3_5.py:934-961): the same results as fused_g_beta ->
@@ -265,7 +288,8 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     dt_bias [Hv]; cu_seqlens [n+1] (device).  fresh: optional bool/uint8 [n]:
     those sequences start from zero recurrent and conv states and their pool
     rows are not read (the slot zeroing of a fresh prefill,
-    model_runner.py:305-322, folded into the call).  Returns o [N, Hv, D] bf16."""
+    model_runner.py:305-322, folded into the call).  cu_seqlens_cpu /
+    max_segments: as chunk_gated_delta_rule_varlen.  Returns o [N, Hv, D] bf16."""
     dev = _check_cuda(mixed, conv_state, conv_weight, b, a, a_log, dt_bias, cu_seqlens, state, state_ids)
     _bf16(mixed, "mixed")
     _bf16(conv_state, "conv_state")
@@ -307,11 +331,12 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     if ws_bytes < 0:
         raise ValueError(f"unsupported chunk shape N={N} n_seqs={n} Hv={Hv} D={D}")
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=mixed.device)
+    cu_host = _host_offsets(cu_seqlens_cpu, n)
     _lib.call("gdn_conv_chunk_prefill", _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_state),
               conv_state.stride(0), conv_state.stride(1), _lib.ptr(w), _lib.ptr(b), _lib.ptr(a),
               _lib.ptr(a_log), _lib.ptr(dt_bias), int(a_log.dtype == torch.float32), _lib.ptr(state),
-              _lib.ptr(state), _lib.ptr(ids), _lib.ptr(fr), state.stride(0), _lib.ptr(cu), n, N, Hk, Hv, D,
-              float(scale), 1,
+              _lib.ptr(state), _lib.ptr(ids), _lib.ptr(fr), state.stride(0), _lib.ptr(cu),
+              _host_ptr(cu_host), int(max_segments), n, N, Hk, Hv, D, float(scale), 1,
               _lib.ptr(o), _lib.ptr(ws), ws_bytes, _stream(dev))
     return o
 
@@ -349,7 +374,7 @@ def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, ini
     o, final = chunk_gated_delta_rule_varlen(qf, kf, vf, gf, bf, cu, initial_state,
                                              output_final_state=output_final_state,
                                              use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
-                                             scale=scale)
+                                             scale=scale, cu_seqlens_cpu=cu_seqlens_cpu)
     return o.view(B, T, Hv, D), final
 
 

@@ -61,14 +61,17 @@ def test_argument_validation_before_launch(pkg):
     lib = pkg._lib.load()
     _lib = pkg._lib
     # unsupported head dim
-    assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, 1, 64,
+    assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, None, 0, 1, 64,
                                  1, 1, 96, 1.0, 1, None, None, 0, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_recurrent(None, 0, 0, None, 0, 0, None, 0, 0, None, None, None, 0, None, 0, None, None,
                              None, 1, 1, 1, 1, 32, 1.0, 1, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_rmsnorm_gated(None, 0, None, 0, None, None, 4, 1, 256, 1e-6, None) == _lib.GDN_ERR_UNSUPPORTED
     # head grouping must divide
-    assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, 1, 64,
+    assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, None, 0, 1, 64,
                                  3, 4, 128, 1.0, 1, None, None, 0, None) == _lib.GDN_ERR_INVALID_ARG
+    # a negative segment count is rejected
+    assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, None, -1, 1, 64,
+                                 4, 4, 128, 1.0, 1, None, None, 0, None) == _lib.GDN_ERR_INVALID_ARG
     # conv width other than 4, and misaligned channel counts
     assert lib.gdn_conv_decode(None, 0, None, 0, 0, None, None, None, 0, 1, 64, 3, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_conv_varlen(None, 0, None, 0, 0, None, None, None, 8, None, None, 1, 4, 30, 4,
