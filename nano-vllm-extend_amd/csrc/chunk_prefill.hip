@@ -1459,47 +1459,82 @@ struct ScanList {
   ScanChain c[kMaxChains];
 };
 
-// grid = n_chains * Hv * D / 16, block = 256: workgroup (chain, head, 16 state
-// columns); thread = one key row, OPT consecutive columns.
+// grid = 8 * ceil(n_chains * Hv * D / 16 / 8), block = 256: workgroup (chain,
+// head, 16 state columns); thread = one key row k and OPT consecutive columns.
+// Each step is P_s (D x D) times the block of S_s (D x 16) in fp32 FMAs, the
+// sum over keys in order.  P_s is staged in LDS with rows padded to D + 1
+// floats (the threads' reads of their rows at one key hit distinct banks);
+// P_s and R_s are loaded one step ahead and the barriers order LDS only, so
+// those loads stay in flight across them (every step issues the same loads,
+// the last one repeating itself).
 template <int D>
 __global__ __launch_bounds__(256) void seg_scan_kernel(ScanList sl, int Hv) {
   constexpr int CB = 16;
   constexpr int NB = D / CB;
-  constexpr int OPT = D * CB / 256;  // outputs per thread: 8 or 4
-  constexpr int TPR = CB / OPT;      // threads per row
+  constexpr int OPT = D * CB / 256;    // outputs per thread: 8 or 4
+  constexpr int TPR = CB / OPT;        // threads per row
+  constexpr int PL = D + 1;            // padded row of P in LDS
+  constexpr int NV = D * D / 4 / 256;  // float4 loads of P per thread
+  __shared__ float Ps[D * PL];
   __shared__ __align__(16) float Ss[D][CB];
-  const int blk = blockIdx.x % NB;
-  const int h = (blockIdx.x / NB) % Hv;
-  const int ci = blockIdx.x / (NB * Hv);
-  if (ci >= sl.n) return;
+  // the column blocks of a head share one XCD, so its L2 fetches each P_s once
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(sl.n) * Hv * NB);
+  if (wi < 0) return;
+  const int blk = static_cast<int>(wi % NB);
+  const int h = static_cast<int>((wi / NB) % Hv);
+  const int ci = static_cast<int>(wi / (NB * Hv));
   const ScanChain& c = sl.c[ci];
   const int64_t hs = static_cast<int64_t>(Hv) * D * D;  // one state
-  const int64_t ho = static_cast<int64_t>(h) * D * D;
+  const int64_t hp = static_cast<int64_t>(h) * D * D;
   const int k = threadIdx.x / TPR, col = (threadIdx.x % TPR) * OPT;
-  const int64_t off = ho + static_cast<int64_t>(k) * D + blk * CB + col;
+  const int64_t off = hp + static_cast<int64_t>(k) * D + blk * CB + col;
 #pragma unroll
   for (int o = 0; o < OPT; ++o) Ss[k][col + o] = c.S[off + o];
-  __syncthreads();
+  float4 pre[NV];
+  float rpre[OPT];
+  auto prefetch = [&](int st) {
+    const float4* pg = reinterpret_cast<const float4*>(c.P + st * hs + hp);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) pre[i] = pg[threadIdx.x + 256 * i];
+#pragma unroll
+    for (int o = 0; o < OPT; ++o) rpre[o] = c.R[st * hs + off + o];
+  };
+  prefetch(0);
+  gdn::keep_loads_here();
   for (int s = 0; s < c.m; ++s) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = 4 * (threadIdx.x + 256 * i);
+      float* dst = &Ps[(e / D) * PL + e % D];
+      dst[0] = pre[i].x;
+      dst[1] = pre[i].y;
+      dst[2] = pre[i].z;
+      dst[3] = pre[i].w;
+    }
     float acc[OPT];
 #pragma unroll
-    for (int o = 0; o < OPT; ++o) acc[o] = c.R[s * hs + off + o];
-    const float4* prow = reinterpret_cast<const float4*>(c.P + s * hs + ho + static_cast<int64_t>(k) * D);
-    for (int m4 = 0; m4 < D / 4; ++m4) {
-      const float4 p4 = prow[m4];
-      const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+    for (int o = 0; o < OPT; ++o) acc[o] = rpre[o];
+    gdn::lds_barrier();  // P_s and S_s are in LDS
+    prefetch(min(s + 1, c.m - 1));
+    gdn::keep_loads_here();
+#pragma unroll 8
+    for (int m = 0; m < D; ++m) {
+      const float pv = Ps[k * PL + m];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int o = 0; o < OPT; ++o) acc[o] = fmaf(pv[e], Ss[4 * m4 + e][col + o], acc[o]);
+      for (int o4 = 0; o4 < OPT / 4; ++o4) {
+        const float4 sv = *reinterpret_cast<const float4*>(&Ss[m][col + 4 * o4]);
+        acc[4 * o4] = fmaf(pv, sv.x, acc[4 * o4]);
+        acc[4 * o4 + 1] = fmaf(pv, sv.y, acc[4 * o4 + 1]);
+        acc[4 * o4 + 2] = fmaf(pv, sv.z, acc[4 * o4 + 2]);
+        acc[4 * o4 + 3] = fmaf(pv, sv.w, acc[4 * o4 + 3]);
+      }
     }
-    __syncthreads();  // every row of S_s is read
+    gdn::lds_barrier();  // every row of S_s and P_s is read
 #pragma unroll
     for (int o = 0; o < OPT; ++o) {
       Ss[k][col + o] = acc[o];
       c.S[(s + 1) * hs + off + o] = acc[o];
     }
-    __syncthreads();
   }
 }
 
@@ -1639,7 +1674,9 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   st = state_launch(p1, p1.n);
   if (st != GDN_OK) return st;
   if (sc.n) {
-    seg_scan_kernel<D><<<dim3(static_cast<unsigned>(sc.n * Hv * (D / 16))), dim3(256), 0, stream>>>(sc, Hv);
+    const int64_t swork = static_cast<int64_t>(sc.n) * Hv * (D / 16);
+    const int64_t sgrid = gdn::kNumXcd * ((swork + gdn::kNumXcd - 1) / gdn::kNumXcd);
+    seg_scan_kernel<D><<<dim3(static_cast<unsigned>(sgrid)), dim3(256), 0, stream>>>(sc, Hv);
     st = gdn_launch_status();
     if (st != GDN_OK) return st;
   }
