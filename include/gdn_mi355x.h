@@ -167,6 +167,13 @@ int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
  *          this folds that into the call).  Its final states are written.
  *   workspace: at least gdn_conv_chunk_prefill_workspace_size() bytes,
  *          256-byte aligned (the chunk records, then the conv's v rows)
+ *   phase  3 = the whole call; 1 = the prep kernel only; 2 = the state pass
+ *          only (after a phase-1 call with the same arguments and workspace,
+ *          ordered after it on the caller's side: the two state calls of a
+ *          split may run on different streams)
+ *   select_host  uint8 [n_seqs] in host memory or NULL: the state pass runs
+ *          only the selected sequences (needs cu_seqlens_host, n_seqs <= 64);
+ *          each sequence's state pass, conv roll included, must run exactly once
  * Two launches, as gdn_chunk_prefill: the prep kernel also runs the conv and
  * the gates of its chunk; the state kernel also rolls the conv states.
  */
@@ -175,7 +182,7 @@ int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_sta
                            const void* A_log, const void* dt_bias, int param_is_fp32, const float* h0,
                            float* hT, const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
                            const int64_t* cu_seqlens, const int64_t* cu_seqlens_host, int max_segments,
-                           int n_seqs, int64_t N, int Hk, int Hv, int D,
+                           int phase, const uint8_t* select_host, int n_seqs, int64_t N, int Hk, int Hv, int D,
                            float scale, int l2norm, uint16_t* o, void* workspace,
                            int64_t workspace_bytes, void* stream);
 
@@ -227,6 +234,18 @@ int gdn_state_commit(float* pool, int64_t slot_stride, const int64_t* ids, const
 int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16_t* z, int64_t sz_tok,
                       const uint16_t* w, uint16_t* y, int64_t n_tok, int H, int D, float eps,
                       void* stream);
+
+/*
+ * The gated norm over some token ranges only (the same arithmetic):
+ * ranges int64 [3 * n_ranges] on the device, (first token, token count,
+ * selected tokens before this range) each; n_sel_tok = all selected tokens.
+ * x, z, y as gdn_rmsnorm_gated (y rows at the tokens' own positions).  No
+ * reference counterpart: it lets the norm of the sequences whose state pass
+ * ends early run while the longest ones are still in the state kernel.
+ */
+int gdn_rmsnorm_gated_ranges(const uint16_t* x, int64_t sx_tok, const uint16_t* z, int64_t sz_tok,
+                             const uint16_t* w, uint16_t* y, const int64_t* ranges, int n_ranges,
+                             int64_t n_sel_tok, int H, int D, float eps, void* stream);
 
 #ifdef __cplusplus
 }

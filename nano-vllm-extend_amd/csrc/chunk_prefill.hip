@@ -1117,6 +1117,8 @@ constexpr int kSegOut = 0;         // outputs; state from h0 (NULL: zero), final
 constexpr int kSegState = 1;       // no outputs; state from h0 (NULL: zero), final to hT
 constexpr int kSegTransition = 2;  // no outputs, U = 0, state from the identity's columns
 constexpr int kMaxSegItems = 64;
+constexpr int kPhasePrep = 1;   // launch the prep kernel
+constexpr int kPhaseState = 2;  // launch the state pass
 
 struct SegItem {
   int r, c0, c1, mode;  // sequence r, its chunks [c0, c1)
@@ -1557,18 +1559,26 @@ struct SegPlan {
   bool any = false;
 };
 
-inline SegPlan plan_segments(const int64_t* cu_host, int n_seqs, int Hv, int D, int max_segments) {
+// (over the sequences selected by select_host, all if NULL)
+inline SegPlan plan_segments(const int64_t* cu_host, const uint8_t* select_host, int n_seqs, int Hv, int D,
+                             int max_segments, bool have_scratch) {
   SegPlan pl;
-  if (!cu_host || max_segments == 1 || !seg_eligible(n_seqs, Hv, D) || n_seqs > kMaxChains * 4) return pl;
+  int n_sel = 0;
+  for (int r = 0; r < n_seqs; ++r) n_sel += !select_host || select_host[r];
+  if (!cu_host || !have_scratch || max_segments == 1 || !seg_eligible(n_sel, Hv, D) || n_seqs > kMaxChains * 4)
+    return pl;
   const int per_item = Hv * (D / kCB);
   int pass1 = 0, pass3 = 0, chains = 0;
   for (int r = 0; r < n_seqs; ++r) {
+    pl.nseg[r] = 1;
+    pl.len[r] = 1;
+    if (select_host && !select_host[r]) continue;
     const int64_t nch = (cu_host[r + 1] - cu_host[r] + kC - 1) / kC;
     int S = 1;
     if (max_segments >= 2) {
       S = static_cast<int>(std::min<int64_t>(std::min(max_segments, kMaxSeg), nch));
     } else if (nch >= 32) {
-      S = static_cast<int>(std::min<int64_t>(std::min(kMaxSeg, 256 / (per_item * n_seqs) + 1), nch / 16));
+      S = static_cast<int>(std::min<int64_t>(std::min(kMaxSeg, 256 / (per_item * n_sel) + 1), nch / 16));
     }
     int L = 1;
     if (S >= 2) {
@@ -1599,20 +1609,23 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
                  int64_t sv, const float* g, const uint16_t* beta, const float* h0, float* hT,
                  const int64_t* ids, int64_t sstride, const int64_t* cu, const int64_t* cu_host, int max_segments,
                  int n_seqs, int64_t nc_bound, int Hk, int Hv, float scale, int l2norm, uint16_t* o, uint8_t* ws,
-                 uint8_t* seg_ws, const ConvIn* cv, hipStream_t stream) {
+                 uint8_t* seg_ws, const ConvIn* cv, int phase, const uint8_t* select_host, hipStream_t stream) {
   const int64_t lwork = nc_bound * Hv;
   const int64_t lgrid = gdn::kNumXcd * ((lwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
   ConvRoll cr{};
-  if (cv) {
-    chunk_prep_kernel<D, true><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
-        q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, *cv);
-    cr = ConvRoll{cv->x, cv->sx, const_cast<uint16_t*>(cv->cstate), cv->ss_seq, cv->ss_ch, cv->key_dim, Hv / Hk};
-  } else {
-    chunk_prep_kernel<D, false><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
-        q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, ConvIn{});
+  if (cv) cr = ConvRoll{cv->x, cv->sx, const_cast<uint16_t*>(cv->cstate), cv->ss_seq, cv->ss_ch, cv->key_dim, Hv / Hk};
+  int st = GDN_OK;
+  if (phase & kPhasePrep) {
+    if (cv)
+      chunk_prep_kernel<D, true><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
+          q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, *cv);
+    else
+      chunk_prep_kernel<D, false><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
+          q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, ConvIn{});
+    st = gdn_launch_status();
+    if (st != GDN_OK) return st;
   }
-  int st = gdn_launch_status();
-  if (st != GDN_OK) return st;
+  if (!(phase & kPhaseState)) return GDN_OK;
   const uint8_t* fresh = cv ? cv->fresh : nullptr;
   const int per_item = Hv * (D / kCB);
   auto state_launch = [&](const SegList& sl, int64_t items) {
@@ -1622,8 +1635,8 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
         v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
     return gdn_launch_status();
   };
-  const SegPlan pl = plan_segments(cu_host, n_seqs, Hv, D, max_segments);
-  if (!pl.any || !seg_ws) {
+  const SegPlan pl = plan_segments(cu_host, select_host, n_seqs, Hv, D, max_segments, seg_ws != nullptr);
+  if (!pl.any && !select_host) {
     SegList none;
     none.n = 0;
     return state_launch(none, n_seqs);
@@ -1649,8 +1662,9 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
     return it;
   };
   for (int r = 0; r < n_seqs; ++r) {
-    const int S = pl.nseg[r];
-    const int64_t L = pl.len[r];
+    if (select_host && !select_host[r]) continue;
+    const int S = pl.any ? pl.nseg[r] : 1;
+    const int64_t L = pl.any ? pl.len[r] : 1;
     const int64_t nch = (cu_host[r + 1] - cu_host[r] + kC - 1) / kC;
     if (S < 2) {
       p1.it[p1.n++] = item(r, 0, nch, kSegOut, 1, 1, nullptr, nullptr);
@@ -1671,6 +1685,7 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
                            nullptr);
     if (m > 0) sc.c[sc.n++] = ScanChain{Sst, P, R, m};
   }
+  if (p1.n == 0) return GDN_OK;
   st = state_launch(p1, p1.n);
   if (st != GDN_OK) return st;
   if (sc.n) {
@@ -1680,7 +1695,7 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
     st = gdn_launch_status();
     if (st != GDN_OK) return st;
   }
-  return state_launch(p3, p3.n);
+  return p3.n ? state_launch(p3, p3.n) : GDN_OK;
 }
 
 }  // namespace
@@ -1722,10 +1737,10 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
   if (D == 128)
     return launch_chunk<128>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
                              cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm,
-                             o, ws, seg_ws, nullptr, s);
+                             o, ws, seg_ws, nullptr, kPhasePrep | kPhaseState, nullptr, s);
   return launch_chunk<64>(q, sq_tok, k, sk_tok, v, sv_tok, g, beta, h0, hT, state_ids, state_stride,
                           cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
-                          ws, seg_ws, nullptr, s);
+                          ws, seg_ws, nullptr, kPhasePrep | kPhaseState, nullptr, s);
 }
 
 // workspace of the fused entry point: the records, then the conv's v rows
@@ -1747,7 +1762,8 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
                                       const void* dt_bias, int param_is_fp32, const float* h0, float* hT,
                                       const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
                                       const int64_t* cu_seqlens, const int64_t* cu_seqlens_host,
-                                      int max_segments, int n_seqs, int64_t N, int Hk, int Hv,
+                                      int max_segments, int phase, const uint8_t* select_host, int n_seqs,
+                                      int64_t N, int Hk, int Hv,
                                       int D, float scale, int l2norm, uint16_t* o, void* workspace,
                                       int64_t workspace_bytes, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
@@ -1755,7 +1771,8 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   if (n_seqs == 0) return GDN_OK;
   if (!x || !conv_state || !conv_w || !a || !b || !A_log || !dt_bias || !cu_seqlens || !o || !workspace)
     return GDN_ERR_INVALID_ARG;
-  if (max_segments < 0) return GDN_ERR_INVALID_ARG;
+  if (max_segments < 0 || phase < 1 || phase > 3) return GDN_ERR_INVALID_ARG;
+  if (select_host && (!cu_seqlens_host || n_seqs > kMaxSegItems)) return GDN_ERR_INVALID_ARG;
   const int64_t C = 2LL * Hk * D + static_cast<int64_t>(Hv) * D;
   // 16-byte row segments of x, 8-byte output pieces, 256-byte workspace records
   if (sx_row % 8 || sx_row < C || reinterpret_cast<uintptr_t>(x) % 16 ||
@@ -1775,8 +1792,8 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   if (D == 128)
     return launch_chunk<128>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
                              cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm,
-                             o, ws, seg_ws, &cv, s);
+                             o, ws, seg_ws, &cv, phase, select_host, s);
   return launch_chunk<64>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
                           cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
-                          ws, seg_ws, &cv, s);
+                          ws, seg_ws, &cv, phase, select_host, s);
 }

@@ -15,14 +15,26 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const uint16_t* __re
                                                             int64_t sz_tok,
                                                             const uint16_t* __restrict__ w,
                                                             uint16_t* __restrict__ y,
-                                                            int64_t rows, int H, float eps) {
+                                                            int64_t rows, int H, float eps,
+                                                            const int64_t* __restrict__ ranges, int n_ranges) {
   constexpr int kLanes = D / 8;                 // lanes per row
   constexpr int kRowsPerBlock = 256 / kLanes;
   const int lane = threadIdx.x % kLanes;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
-  const bool active = row < rows;
-  const int64_t tok = active ? row / H : 0;
-  const int h = active ? static_cast<int>(row % H) : 0;
+  const int64_t r_sel = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
+  const bool active = r_sel < rows;
+  int64_t tok = active ? r_sel / H : 0;
+  const int h = active ? static_cast<int>(r_sel % H) : 0;
+  if (ranges && active) {
+    // token ranges (start, count, tokens before it): the t-th selected token
+    for (int i = 0; i < n_ranges; ++i) {
+      const int64_t start = ranges[3 * i], cnt = ranges[3 * i + 1], before = ranges[3 * i + 2];
+      if (tok < before + cnt) {
+        tok = start + (tok - before);
+        break;
+      }
+    }
+  }
+  const int64_t row = tok * H + h;
 
   uint4 xv = make_uint4(0, 0, 0, 0), zv = make_uint4(0, 0, 0, 0);
   if (active) {
@@ -65,7 +77,7 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const uint16_t* __re
   out.y = gdn::f2bf2(yv[2], yv[3]);
   out.z = gdn::f2bf2(yv[4], yv[5]);
   out.w = gdn::f2bf2(yv[6], yv[7]);
-  if (active) *reinterpret_cast<uint4*>(y + row * D + lane * 8) = out;
+  if (active) *reinterpret_cast<uint4*>(y + row * D + lane * 8) = out;  // y rows [tok, h] dense
 }
 
 }  // namespace
@@ -86,10 +98,37 @@ extern "C" int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128) {
     const int64_t nb = (rows + 15) / 16;
-    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps);
+    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
+                                                                                     nullptr, 0);
   } else {
     const int64_t nb = (rows + 31) / 32;
-    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps);
+    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
+                                                                                    nullptr, 0);
+  }
+  return gdn_launch_status();
+}
+
+extern "C" int gdn_rmsnorm_gated_ranges(const uint16_t* x, int64_t sx_tok, const uint16_t* z, int64_t sz_tok,
+                                        const uint16_t* w, uint16_t* y, const int64_t* ranges, int n_ranges,
+                                        int64_t n_sel_tok, int H, int D, float eps, void* stream) {
+  if (n_sel_tok < 0 || H <= 0 || n_ranges < 0) return GDN_ERR_INVALID_ARG;
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (n_sel_tok == 0) return GDN_OK;
+  if (!x || !z || !w || !y || !ranges || n_ranges == 0) return GDN_ERR_INVALID_ARG;
+  if ((sx_tok % 8) || (sz_tok % 8) || (reinterpret_cast<uintptr_t>(x) % 16) ||
+      (reinterpret_cast<uintptr_t>(z) % 16) || (reinterpret_cast<uintptr_t>(w) % 16) ||
+      (reinterpret_cast<uintptr_t>(y) % 16))
+    return GDN_ERR_INVALID_ARG;
+  const int64_t rows = n_sel_tok * H;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 128) {
+    const int64_t nb = (rows + 15) / 16;
+    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
+                                                                                     ranges, n_ranges);
+  } else {
+    const int64_t nb = (rows + 31) / 32;
+    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
+                                                                                    ranges, n_ranges);
   }
   return gdn_launch_status();
 }

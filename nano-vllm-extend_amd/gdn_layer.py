@@ -39,6 +39,7 @@ class Switches:
     fla_chunk: bool = True
     fla_recurrent: bool = True
     fused_prefill: bool = True
+    split_state: bool = False
 
     @classmethod
     def from_env(cls) -> "Switches":
@@ -49,7 +50,67 @@ class Switches:
                    varlen=e("NANOVLLM_GDN_VARLEN", "1") == "1",
                    fla_chunk=e("FLA_CHUNK", "1") == "1",
                    fla_recurrent=e("FLA_RECURRENT", "1") == "1",
-                   fused_prefill=e("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1")
+                   fused_prefill=e("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1",
+                   split_state=e("NANOVLLM_GDN_SPLIT_STATE", "0") == "1")
+
+
+# State-pass split policy (off by default: measured at config 1 the split
+# costs more than it saves -- each event between the prep and the state
+# launches delays the stream by ~6 us, the long sequence's chain slows under
+# the concurrent traffic, and the bandwidth-bound norm overlaps only the last
+# ~18 us of the state pass).  The state pass of a varlen group lasts as long
+# as its longest sequence's chain (~1.9 us per 64-token chunk when the GPU is
+# full); the gated norm streams ~768 B per token and head (~5.4 TB/s).  With
+# the k longest sequences on one stream and the rest on another, the rest's
+# norm overlaps the long sequences' chains; k is chosen to minimise
+# max(T_long, T_rest + norm_rest) + norm_long.
+_CHUNK_US = 1.9
+_NORM_US_PER_TOKEN_HEAD = 768 / 5.4e6
+
+_SPLIT_CACHE: dict = {}
+
+
+def late_split(lens_q: list[int], Hv: int):
+    """(late flags per sequence, (early token ranges, count), (late ranges,
+    count)) with the ranges as host int64 [3 * n] (first token, tokens,
+    selected tokens before), or None when splitting gains under 5 us."""
+    key = (tuple(lens_q), Hv)
+    if key in _SPLIT_CACHE:
+        return _SPLIT_CACHE[key]
+    n = len(lens_q)
+    res = None
+    if 2 <= n <= 64 and sum(lens_q) >= 4096:
+        ch = [(l + 63) // 64 for l in lens_q]
+        order = sorted(range(n), key=lambda r: -ch[r])
+        norm = lambda toks: toks * Hv * _NORM_US_PER_TOKEN_HEAD
+        whole = ch[order[0]] * _CHUNK_US + norm(sum(lens_q))
+        best, best_k = whole - 5.0, 0
+        for k in range(1, n):
+            long_toks = sum(lens_q[r] for r in order[:k])
+            t = max(ch[order[0]] * _CHUNK_US, ch[order[k]] * _CHUNK_US + norm(sum(lens_q) - long_toks)) \
+                + norm(long_toks)
+            if t < best:
+                best, best_k = t, k
+        if best_k:
+            late = [False] * n
+            for r in order[:best_k]:
+                late[r] = True
+            starts = [0]
+            for l in lens_q:
+                starts.append(starts[-1] + l)
+
+            def ranges(flag):
+                rows, before = [], 0
+                for r in range(n):
+                    if late[r] == flag and lens_q[r]:
+                        rows += [starts[r], lens_q[r], before]
+                        before += lens_q[r]
+                t = torch.tensor(rows, dtype=torch.int64)
+                return (t.pin_memory() if torch.cuda.is_available() else t), before
+
+            res = (late, ranges(False), ranges(True))
+    _SPLIT_CACHE[key] = res
+    return res
 
 
 class GatedDeltaNetCore:
@@ -158,6 +219,10 @@ class GatedDeltaNetCore:
             # gates + conv + chunk rule in one call (the same results as the
             # three calls below)
             _, _, cu64_cpu, cu64_gpu = varlen_meta(lens_q, mixed.device)
+            split = late_split(lens_q, Hv) if self.sw.split_state else None
+            if split is not None:
+                return self._prefill_split(mixed, z, b, a, lens_q, ids, conv_cache, s_cache, fresh, cu64_cpu,
+                                           cu64_gpu, split)
             with self._timed("conv_chunk_prefill"):
                 o = ops.conv_chunk_prefill_varlen(mixed, conv_cache, self.conv_w, b, a, self.A_log, self.dt_bias,
                                                   cu64_gpu, s_cache, ids, Hk, Hv, D, fresh=fresh,
@@ -180,6 +245,41 @@ class GatedDeltaNetCore:
                                                      g, beta, cu64_gpu, s_cache, state_ids=ids,
                                                      final_state=s_cache, cu_seqlens_cpu=cu64_cpu)
         return self._norm(o, z.view(N, Hv, D))
+
+    def _prefill_split(self, mixed, z, b, a, lens_q, ids, conv_cache, s_cache, fresh, cu64_cpu, cu64_gpu, split):
+        """Fused prefill with the state pass split over two streams: the longest
+        sequences on the current stream, the others on a side stream where
+        their gated norm then runs while the long ones are still in the state
+        kernel.  The same results as the one-stream path, bit for bit."""
+        late, (r_early, n_early), (r_late, n_late) = split
+        N = mixed.shape[0]
+        Hk, Hv, D = self.Hk, self.Hv, self.D
+        dev = mixed.device
+        side = self._side_stream(dev)
+        cur = torch.cuda.current_stream(dev)
+        keep = []
+        with self._timed("conv_chunk_prefill"):
+            o, side_done = ops.conv_chunk_prefill_varlen(mixed, conv_cache, self.conv_w, b, a, self.A_log,
+                                                         self.dt_bias, cu64_gpu, s_cache, ids, Hk, Hv, D,
+                                                         fresh=fresh, cu_seqlens_cpu=cu64_cpu, late=late,
+                                                         side_stream=side, keep=keep)
+            cur.wait_event(side_done)   # (the long sequences' state pass is the longer one)
+        y = torch.empty(N, Hv, D, dtype=torch.bfloat16, device=dev)
+        zz = z.view(N, Hv, D)
+        r_e = r_early.to(dev, non_blocking=True)
+        r_l = r_late.to(dev, non_blocking=True)
+        with torch.cuda.stream(side):
+            ops.rms_norm_gated_ranges(o, zz, self.norm_w, self.eps, y, r_e, n_early)
+        with self._timed("rmsnorm_gated"):
+            ops.rms_norm_gated_ranges(o, zz, self.norm_w, self.eps, y, r_l, n_late)
+            cur.wait_stream(side)
+        keep.extend([y, zz, r_e, r_l])
+        return y
+
+    def _side_stream(self, dev):
+        if getattr(self, "_side", None) is None or self._side.device != dev:
+            self._side = torch.cuda.Stream(dev)   # default priority
+        return self._side
 
     def _conv_varlen_eager(self, mixed, lens_q, ids, conv_cache):
         """F.conv1d chain per sequence (the reference's NANOVLLM_CONV_TRITON=0 form)."""

@@ -274,7 +274,8 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
                               cu_seqlens: torch.Tensor, state: torch.Tensor, state_ids: torch.Tensor | None,
                               num_k_heads: int, num_v_heads: int, head_dim: int,
                               scale: float | None = None, fresh: torch.Tensor | None = None,
-                              cu_seqlens_cpu: torch.Tensor | None = None, max_segments: int = 0) -> torch.Tensor:
+                              cu_seqlens_cpu: torch.Tensor | None = None, max_segments: int = 0,
+                              late: list[bool] | None = None, side_stream=None, keep: list | None = None):
     """Gates, varlen causal conv1d + SiLU and the chunked gated delta rule in
     one call (two kernels), the prefill sequence of _gdn_prefill_varlen
     (nanovllm/models/qwen3_5.py:934-961): the same results as fused_g_beta ->
@@ -289,7 +290,15 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     those sequences start from zero recurrent and conv states and their pool
     rows are not read (the slot zeroing of a fresh prefill,
     model_runner.py:305-322, folded into the call).  cu_seqlens_cpu /
-    max_segments: as chunk_gated_delta_rule_varlen.  Returns o [N, Hv, D] bf16."""
+    max_segments: as chunk_gated_delta_rule_varlen.
+
+    late / side_stream (split state pass): after the prep kernel on the
+    current stream, the state pass of the sequences with late[r] runs on the
+    current stream and that of the others on side_stream, concurrently.  The
+    caller orders later work on side_stream's results itself (e.g. the current
+    stream waits for side_stream) and keeps the tensors appended to `keep`
+    alive until then.  Returns o [N, Hv, D] bf16, and with `late` also an
+    event recorded on side_stream after its state pass."""
     dev = _check_cuda(mixed, conv_state, conv_weight, b, a, a_log, dt_bias, cu_seqlens, state, state_ids)
     _bf16(mixed, "mixed")
     _bf16(conv_state, "conv_state")
@@ -332,13 +341,33 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
         raise ValueError(f"unsupported chunk shape N={N} n_seqs={n} Hv={Hv} D={D}")
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=mixed.device)
     cu_host = _host_offsets(cu_seqlens_cpu, n)
-    _lib.call("gdn_conv_chunk_prefill", _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_state),
-              conv_state.stride(0), conv_state.stride(1), _lib.ptr(w), _lib.ptr(b), _lib.ptr(a),
-              _lib.ptr(a_log), _lib.ptr(dt_bias), int(a_log.dtype == torch.float32), _lib.ptr(state),
-              _lib.ptr(state), _lib.ptr(ids), _lib.ptr(fr), state.stride(0), _lib.ptr(cu),
-              _host_ptr(cu_host), int(max_segments), n, N, Hk, Hv, D, float(scale), 1,
-              _lib.ptr(o), _lib.ptr(ws), ws_bytes, _stream(dev))
-    return o
+
+    def launch(phase, select, stream):
+        _lib.call("gdn_conv_chunk_prefill", _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_state),
+                  conv_state.stride(0), conv_state.stride(1), _lib.ptr(w), _lib.ptr(b), _lib.ptr(a),
+                  _lib.ptr(a_log), _lib.ptr(dt_bias), int(a_log.dtype == torch.float32), _lib.ptr(state),
+                  _lib.ptr(state), _lib.ptr(ids), _lib.ptr(fr), state.stride(0), _lib.ptr(cu),
+                  _host_ptr(cu_host), int(max_segments), phase, _host_ptr(select), n, N, Hk, Hv, D, float(scale),
+                  1, _lib.ptr(o), _lib.ptr(ws), ws_bytes, stream)
+
+    if late is None:
+        launch(3, None, _stream(dev))
+        return o
+    assert side_stream is not None and cu_host is not None and len(late) == n
+    sel_late = torch.tensor([bool(x) for x in late], dtype=torch.uint8)
+    sel_early = 1 - sel_late
+    cur = torch.cuda.current_stream(dev)
+    launch(1, None, cur.cuda_stream)                       # prep
+    ev = torch.cuda.Event()
+    ev.record(cur)
+    side_stream.wait_event(ev)
+    launch(2, sel_late, cur.cuda_stream)                   # the long sequences
+    launch(2, sel_early, side_stream.cuda_stream)          # the others, concurrently
+    side_done = torch.cuda.Event()
+    side_done.record(side_stream)
+    if keep is not None:
+        keep.extend([mixed, w, a, b, a_log, dt_bias, cu, ids, fr, o, ws, conv_state, state])
+    return o, side_done
 
 
 def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, initial_state=None,
@@ -503,6 +532,25 @@ def rms_norm_gated(hidden_states: torch.Tensor, gate: torch.Tensor, weight: torc
     _lib.call("gdn_rmsnorm_gated", _lib.ptr(x2), x2.stride(0), _lib.ptr(z2), z2.stride(0), _lib.ptr(w),
               _lib.ptr(y), n_tok, H, D, float(eps), _stream(dev))
     return y.view(hidden_states.shape)
+
+
+def rms_norm_gated_ranges(hidden_states: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float,
+                          out: torch.Tensor, ranges: torch.Tensor, n_sel_tok: int) -> None:
+    """rms_norm_gated on the tokens of some ranges only, into `out` (the same
+    arithmetic, rows at the tokens' positions).  hidden_states / gate / out
+    [N, H, D] bf16 with head-contiguous rows; ranges int64 [3 * n] on the
+    device: (first token, token count, selected tokens before it)."""
+    dev = _check_cuda(hidden_states, gate, weight, out, ranges)
+    _bf16(hidden_states, "hidden_states")
+    _bf16(gate, "gate")
+    N, H, D = hidden_states.shape
+    assert gate.shape == hidden_states.shape and out.shape == hidden_states.shape and out.is_contiguous()
+    assert hidden_states.stride(2) == 1 and hidden_states.stride(1) == D
+    assert gate.stride(2) == 1 and gate.stride(1) == D
+    w = weight.to(torch.bfloat16).contiguous()
+    _lib.call("gdn_rmsnorm_gated_ranges", _lib.ptr(hidden_states), hidden_states.stride(0), _lib.ptr(gate),
+              gate.stride(0), _lib.ptr(w), _lib.ptr(out), _lib.ptr(ranges), ranges.numel() // 3, n_sel_tok, H, D,
+              float(eps), _stream(dev))
 
 
 class Qwen3_5RMSNormGated(torch.nn.Module):

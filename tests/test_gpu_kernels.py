@@ -333,3 +333,27 @@ def test_chunk_pool_inplace_and_padded_api(pkg, dev):
         gb.view(Bn, T, H).to(dev), bb.view(Bn, T, H).to(dev))
     assert_out(o2.view(-1, H, D).cpu(), ro2.to(BF16), "batched chunk out")
     assert_state(S2.cpu(), rS2, "batched chunk final")
+
+
+def test_rmsnorm_gated_token_ranges(pkg, dev):
+    """The range form normalises exactly the selected tokens, as the full form
+    does, and leaves the other rows of the output alone."""
+    gen = _gen(61)
+    N, H, D = 300, 4, 128
+    x = torch.randn(N, H, D, generator=gen).to(BF16).to(dev)
+    z = torch.randn(N, H, D, generator=gen).to(BF16).to(dev)
+    w = (1 + 0.02 * torch.randn(D, generator=gen)).to(BF16).to(dev)
+    full = pkg.ops.rms_norm_gated(x, z, w, 1e-6)
+    sel = [(0, 10), (50, 1), (120, 100), (299, 1)]
+    rows, before = [], 0
+    for st, cnt in sel:
+        rows += [st, cnt, before]
+        before += cnt
+    out = torch.full((N, H, D), 7.0, dtype=BF16, device=dev)
+    pkg.ops.rms_norm_gated_ranges(x, z, w, 1e-6, out, torch.tensor(rows, device=dev), before)
+    torch.cuda.synchronize()
+    mask = torch.zeros(N, dtype=torch.bool)
+    for st, cnt in sel:
+        mask[st:st + cnt] = True
+    assert torch.equal(out.cpu()[mask].view(torch.int16), full.cpu()[mask].view(torch.int16))
+    assert torch.all(out.cpu()[~mask] == 7.0)

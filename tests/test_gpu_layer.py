@@ -337,3 +337,26 @@ def test_installed_prefill_method_equals_layer_core(pkg, dev):
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
     assert torch.equal(layer.s_cache, sp1)
     assert torch.equal(layer.conv_cache.view(torch.int16), cp1.view(torch.int16))
+
+
+def test_split_state_pass_equals_one_stream(pkg, dev):
+    """Config 1 with the state pass split over two streams (the long sequences
+    on the current stream, the rest and their gated norm on a side stream)
+    gives the one-stream results bit for bit, pools included."""
+    cfg = bench.make_prefill(1, None)
+    assert pkg.gdn_layer.late_split(cfg["lens"], cfg["Hv"]) is not None, "config 1 should split"
+    n = len(cfg["lens"])
+    outs = []
+    for split in (False, True):
+        core = _core(pkg, dev, cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"], cfg["A_log"], cfg["dt_bias"],
+                     cfg["norm_w"], split_state=split)
+        cp, sp = cfg["conv_state"].to(dev), cfg["h0"].to(dev)
+        for rep in range(2):      # twice: the second call reuses cached split metadata and allocator blocks
+            out = core.prefill_varlen(cfg["x"].to(dev), cfg["z"].to(dev), cfg["b"].to(dev), cfg["a"].to(dev),
+                                      cfg["lens"], torch.arange(n, device=dev), cp, sp)
+        torch.cuda.synchronize()
+        outs.append((out.cpu(), cp.cpu(), sp.cpu()))
+    (o1, c1, s1), (o2, c2, s2) = outs
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), "outputs differ"
+    assert torch.equal(c1.view(torch.int16), c2.view(torch.int16)), "conv pool differs"
+    assert torch.equal(s1, s2), "state pool differs"
