@@ -349,9 +349,9 @@ def main():
                 "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                 "traffic": _profiled_traffic("conv_chunk_prefill_config1" if fused else "chunk_prefill_config1"),
                 "kernel": ("gates + conv1d/SiLU + chunk rule = chunk_prep_kernel<128, true> + "
-                           "chunk_state_kernel<128> (one launch pair per call; the time includes the conv and "
+                           "chunk_state_kernel<128, true> (one launch pair per call; the time includes the conv and "
                            "gates, the flop count is the chunk rule's matrix products)" if fused else
-                           "chunk prefill = chunk_prep_kernel<128> + chunk_state_kernel<128> "
+                           "chunk prefill = chunk_prep_kernel<128, false> + chunk_state_kernel<128, false> "
                            "(one launch pair per call)"),
                 "kernel_us": round(chunk_us, 2), "algorithmic_flop_per_launch": flops}
     kernels1 = {k: round(v, 2) for k, v in k1.items()}

@@ -153,7 +153,8 @@ int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
  * points above called in that order (gdn_g_beta, gdn_conv_varlen with
  * key_dim = Hk*D, gdn_chunk_prefill with l2norm), bit for bit.
  *   x      [N, C] bf16 raw q | k | v rows, C = 2*Hk*D + Hv*D, row stride
- *          sx_row (a multiple of 8), channel stride 1, 16-byte aligned
+ *          sx_row (a multiple of 8, below 2^24), channel stride 1, 16-byte
+ *          aligned
  *   conv_state, ss_seq, ss_ch, conv_w: as gdn_conv_varlen with K = 4; the
  *          pool row of sequence r is state_ids[r] (r if NULL), the same row
  *          as the recurrent state's
@@ -166,7 +167,7 @@ int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
  *          reference zeroes a fresh prefill's slot first, model_runner.py:305-322;
  *          this folds that into the call).  Its final states are written.
  *   workspace: at least gdn_conv_chunk_prefill_workspace_size() bytes,
- *          256-byte aligned (the chunk records, then the conv's v rows)
+ *          256-byte aligned (the chunk records, as gdn_chunk_prefill's)
  *   phase  3 = the whole call; 1 = the prep kernel only; 2 = the state pass
  *          only (after a phase-1 call with the same arguments and workspace,
  *          ordered after it on the caller's side: the two state calls of a
@@ -174,8 +175,9 @@ int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
  *   select_host  uint8 [n_seqs] in host memory or NULL: the state pass runs
  *          only the selected sequences (needs cu_seqlens_host, n_seqs <= 64);
  *          each sequence's state pass, conv roll included, must run exactly once
- * Two launches, as gdn_chunk_prefill: the prep kernel also runs the conv and
- * the gates of its chunk; the state kernel also rolls the conv states.
+ * Two launches, as gdn_chunk_prefill: the prep kernel also runs the gates and
+ * the q and k channels' conv of its chunk; the state kernel runs the v
+ * channels' conv and rolls the conv states.
  */
 int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_state, int64_t ss_seq,
                            int64_t ss_ch, const uint16_t* conv_w, const uint16_t* b, const uint16_t* a,

@@ -14,14 +14,17 @@
 //   chunk_prep_kernel: one workgroup per (chunk, value head), all chunks in
 //     parallel.  Everything that needs only the chunk's own q, k, g, beta:
 //     the row norms, K K^T, Q K^T, the triangular inverse T (fp32), and it
-//     writes a 26 KiB record: T diag(beta e^G), T diag(beta) and A as fp16
-//     64x64 tiles plus the per-token scales.
+//     writes a 51 KiB record: -T' = -T diag(beta e^G / |k|), T'' = T diag(beta)
+//     and A as fp16 tiles, the per-token scales, and the q rows and K^T as
+//     fp16 operand fragments.  The fused variant first computes the gates
+//     and the conv1d + SiLU of the chunk's q and k channels from the raw rows.
 //   chunk_state_kernel: one workgroup per (sequence, value head, block of 64
 //     value columns), persistent over the sequence's chunks.  Producer waves
-//     stage the next chunk (raw q rows, K^ and V transposed, all fp16; the
-//     record's tiles; W = T' K^ by MFMA) into a double-buffered LDS stage
-//     while two chain waves run the state-dependent products of the current
-//     chunk with their 128 x 32 slice of S in registers.
+//     stage the next chunk (the record's K^T; -W = -T' K^ by MFMA; U = T'' V,
+//     where the fused variant's V is the conv1d + SiLU of the raw v channels,
+//     computed by the U waves) into a double-buffered LDS stage while two
+//     chain waves run the state-dependent products of the current chunk with
+//     their 128 x 32 slice of S in registers.
 //
 // Numerics.  Every state-path product runs on the fp16 matrix cores
 // (v_mfma_f32_32x32x16_f16, fp32 accumulation) with one pass: fp16 keeps 11
@@ -294,7 +297,6 @@ struct ConvIn {
   const uint8_t* fresh;    // per sequence, nonzero: zero initial states, pools not read (NULL: none)
   const uint16_t* w;       // [C, 4] conv taps
   int key_dim;             // Hk * D
-  uint16_t* vout;          // [N, Hv, D] conv output of the v channels
   const uint16_t* a;       // [N, Hv] gate inputs
   const uint16_t* b;
   const void* A_log;       // [Hv], bf16 or fp32 (param_f32)
@@ -302,14 +304,14 @@ struct ConvIn {
   int param_f32;
 };
 
-// Fused variant, phase 1: causal conv (width 4) + SiLU of the chunk's q, k and
-// v rows.  Each output row needs the 3 raw rows before it: inside the chunk
+// Fused variant, phase 1: causal conv (width 4) + SiLU of the chunk's q and k
+// rows (the v channels' conv runs in the state kernel).  Each output row needs the 3 raw rows before it: inside the chunk
 // and the previous chunk they are rows of x, before a sequence's first token
 // they are the conv state's taps.  Thread (16-byte channel segment c8, rows
 // t0 .. t0 + RPT - 1) loads its RPT + 3 raw rows of a part (q, k or v) and the
 // part's taps, and writes q -> Qc and k -> Kr (bf16 rows in LDS, zero past the
 // sequence end), the k rows' sums of squares -> ssk (in the plain path's
-// summation order), and v -> vout (rows of this sequence only).
+// summation order).
 // The loads of a part are unconditional (rows clamped into x) so that the
 // three parts' loads can be in flight together; the few lanes whose window
 // starts before the sequence replace those rows with the conv state after the
@@ -424,10 +426,6 @@ __device__ __forceinline__ void conv_compute(const ConvRaw<D>& R, const ConvIn& 
   for (int rr = 0; rr < RPT; ++rr) {
     const int t = t0 + rr;
     u32x4_t out = {yp[rr][0], yp[rr][1], yp[rr][2], yp[rr][3]};
-    if (part == 2) {
-      if (t < len) *reinterpret_cast<u32x4_t*>(cv.vout + ((tok0 + t) * Hv + h) * D + 8 * c8) = out;
-      continue;
-    }
     if (t >= len) out = u32x4_t{0u, 0u, 0u, 0u};
     if (part == 0) {
       *reinterpret_cast<u32x4_t*>(&Qc[t][8 * c8]) = out;
@@ -447,8 +445,7 @@ __device__ __forceinline__ void conv_compute(const ConvRaw<D>& R, const ConvIn& 
   }
 }
 
-// The three parts with two register sets: q and k in flight together, v's
-// loads issued once q's registers are free.
+// The two parts with two register sets: q and k in flight together.
 template <int D>
 __device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)[D + 8], uint16_t (*Kr)[D + 8],
                                                 float* ssk, int64_t tok0, int len, bool first, int r, int kh,
@@ -462,16 +459,12 @@ __device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)
   conv_compute<D>(R0, cv, 0, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
   conv_state_halo<D>(R1, cv, 1, first, r, kh, h, tid);
   conv_compute<D>(R1, cv, 1, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
-  conv_load<D>(R0, cv, 2, tok0, len, kh, h, tid);
-  gdn::keep_loads_here();
-  conv_state_halo<D>(R0, cv, 2, first, r, kh, h, tid);
-  conv_compute<D>(R0, cv, 2, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
 }
 
 // grid = 8 * ceil(nc_bound * Hv / 8); block = 256.  One workgroup per
 // (chunk, value head); writes the chunk's record.
-// kConv: q, k, v are the conv1d + SiLU of cv.x and g, beta the gates of
-// cv.a, cv.b, all computed here (q, k, g, beta unused); v goes to cv.vout.
+// kConv: q, k are the conv1d + SiLU of cv.x and g, beta the gates of cv.a,
+// cv.b, all computed here (the q, k, g, beta arguments unused).
 template <int D, bool kConv>
 __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
@@ -831,20 +824,24 @@ struct __align__(16) StateSmem {
   StateStage<D> st[2];
   StateXchg<D> xc[2];
   uint16_t ot[2][32 * kCB];  // each output wave's bf16 tile on its way out, swz<64>
+  uint16_t vtile[2][67 * 16];  // fused: each U wave's conv window rows (one k-step's 16 channels)
+  uint16_t vw[2][32 * 4];      // fused: each U wave's 32 channels' conv taps
 };
 
 constexpr int kStateWaves = 8;
 
 // Wave roles of the state kernel (wave w; waves land on the SIMDs in the
-// order 0, 2, 1, 3, 0, 2, 1, 3 or a rotation of it, so each SIMD runs two
-// roles):
+// order 0, 2, 1, 3, 0, 2, 1, 3 or a rotation of it, so waves w and w + 4
+// share a SIMD: each chain wave shares with a K wave, each output wave with a
+// U wave, whose VALU-heavy conv (fused variant) stays off the chain's SIMDs):
 //   w 0, 1  chain: the recurrence for state columns 32 w .. 32 w + 31 of the
 //           workgroup's 64 (Vn = U - W S, S <- e^gamma S + K^T diag(cK) Vn)
 //   w 2, 3  output: O^T = S^T Q'^T + Vn^T A^T of token tile w - 2 (both
 //           chains' columns), one chunk behind the chain
-//   w 4, 5  U: U = T'' V for value-column tile w - 4
-//   w 6, 7  K: the record's K^T and -W = -T' K for key tiles w - 6 (+ 2), and
+//   w 4, 5  K: the record's K^T and -W = -T' K for key tiles w - 4 (+ 2), and
 //           the record's vec block, into the stage
+//   w 6, 7  U: U = T'' V for value-column tile w - 6 (fused variant: V is the
+//           conv1d + SiLU of the raw v channels, computed here)
 // Per chunk the chain, U, output and K roles issue 32, 10, 24 and 12
 // matrix-core products of 32x32x16.
 
@@ -857,8 +854,20 @@ struct KPrefetch {
   s16x8_t vec;                        // the lane's 16 bytes of the record vec block
 };
 
+// Conv inputs of the fused variant: the U waves compute the conv1d + SiLU of
+// their v channels from the raw rows, and the output waves roll the conv state.
+struct StateConv {
+  const uint16_t* x;  // [N, C] raw rows, row stride sx (NULL: not fused)
+  int64_t sx;
+  uint16_t* cstate;   // conv state pool: row slot, channel c, tap j at cstate + slot*ss_seq + c*ss_ch + j
+  int64_t ss_seq, ss_ch;
+  const uint16_t* w;  // [C, 4] conv taps
+  int key_dim;        // Hk * D; the v channels start at 2 key_dim
+  int ratio;          // Hv / Hk
+};
+
 struct UPrefetch {
-  s16x8_t v[2][2];  // raw V rows: token tile tt, value k-step h
+  s16x8_t v[2][2];  // V rows (fused: raw rows): token tile tt, value k-step h
   s16x8_t tb[6];    // T'' fragments
 };
 
@@ -913,6 +922,7 @@ __device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int
     p.v[tt][0] = buf_ld(rv, off, 0);
     p.v[tt][1] = buf_ld(rv, off, 32);
   }
+
   const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
   for (int j = 0; j < 6; ++j) p.tb[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * j);
@@ -970,15 +980,76 @@ __device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int p
 
 // U waves: V^T of column tile c by the natural identity, then U = T'' V; U's
 // C tiles are stored lane-major for the chain wave that owns the columns.
-template <int D>
-__device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, int c, int lane) {
+// Fused variant: the conv1d + SiLU of the lane's V elements (token 32 tt + li,
+// channels 32 c + 16 h + 8 g + 0..7) from the raw rows.  The window rows come
+// through the wave's LDS tile (tile row i = chunk row i - 3, the 16 channels
+// of one k-step h): the lanes' own rows, and in rows 0..2 the carry -- the
+// previous chunk's last 3 rows, or before a sequence its conv state's taps.
+// The carry for the next chunk is taken from the tile.  wt holds the 32
+// channels' taps (channel-major, 4 taps each).  Every conv goes through
+// gdn::conv4_silu in the standalone kernel's operation order, so the values
+// are bit-identical.
+__device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], uint16_t* tile, const uint16_t* wt,
+                                       int lane, s16x8_t (&vc)[2][2]) {
+  const int li = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    *reinterpret_cast<s16x8_t*>(&tile[(3 + li) * 16 + 8 * g]) = p.v[0][h];
+    *reinterpret_cast<s16x8_t*>(&tile[(35 + li) * 16 + 8 * g]) = p.v[1][h];
+    if (li < 3) *reinterpret_cast<s16x8_t*>(&tile[li * 16 + 8 * g]) = carry[h];
+    wave_sync();
+    uint4 x[2][3], w4[4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) x[tt][i] = *reinterpret_cast<const uint4*>(&tile[(32 * tt + li + i) * 16 + 8 * g]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w4[j] = reinterpret_cast<const uint4*>(wt + (16 * h + 8 * g) * 4)[j];
+    carry[h] = *reinterpret_cast<const s16x8_t*>(&tile[(64 + min(li, 2)) * 16 + 8 * g]);
+    uint32_t y[2][4];
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      float yy[2][2];
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const int e = 2 * e2 + cc;
+        float wk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wk[j] = bf_elem(w4[(4 * e + j) / 8], (4 * e + j) % 8);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          yy[tt][cc] = gdn::conv4_silu(bf_elem(x[tt][0], e), bf_elem(x[tt][1], e), bf_elem(x[tt][2], e),
+                                       bf_elem(__builtin_bit_cast(uint4, p.v[tt][h]), e), wk);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) y[tt][e2] = gdn::f2bf2(yy[tt][0], yy[tt][1]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) vc[tt][h] = __builtin_bit_cast(s16x8_t, u32x4_t{y[tt][0], y[tt][1], y[tt][2], y[tt][3]});
+    wave_sync();  // the tile is read before the next half's rows go in
+  }
+}
+
+template <int D, bool kX>
+__device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, int c, int lane, s16x8_t (&carry)[2],
+                                        uint16_t* tile, const uint16_t* wt) {
   const int li = lane & 31, g = lane >> 5;
   const s16x8_t in0 = ident_frag(0, li, g), in1 = ident_frag(1, li, g);
+  s16x8_t vc[2][2];
+  if constexpr (kX) {
+    u_conv(p, carry, tile, wt, lane, vc);
+  } else {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      vc[tt][0] = p.v[tt][0];
+      vc[tt][1] = p.v[tt][1];
+    }
+  }
   f32x16_t vt[2];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    vt[tt] = mfma32_bf16(p.v[tt][0], in0, zero16());
-    vt[tt] = mfma32_bf16(p.v[tt][1], in1, vt[tt]);
+    vt[tt] = mfma32_bf16(vc[tt][0], in0, zero16());
+    vt[tt] = mfma32_bf16(vc[tt][1], in1, vt[tt]);
   }
   h16x8_t vb[4];
 #pragma unroll
@@ -1064,26 +1135,19 @@ __device__ __forceinline__ void o_chunk(const OPrefetch<D>& p, const StateXchg<D
 }
 
 // Conv-state roll of the fused variant, done here because the prep kernel
-// reads the old state from every chunk-0 workgroup of a sequence (the value
-// heads that share a key head included), and this kernel runs after all of
-// them.  Workgroup (sequence r, value head h, column block cb) rolls its 64 v
-// channels, and the q and k channels of its columns when h is the first value
-// head of its key head: state taps j = 0..2 <- the raw inputs at positions
-// T - 3 + j (old taps T + j where that is negative), as the standalone conv
-// kernel does.
-struct ConvRoll {
-  const uint16_t* x;  // [N, C] raw rows, row stride sx (NULL: not fused, no roll)
-  int64_t sx;
-  uint16_t* cstate;
-  int64_t ss_seq, ss_ch;
-  int key_dim;
-  int ratio;  // Hv / Hk
-};
-
+// reads the old q and k taps from every chunk-0 workgroup of a sequence (the
+// value heads that share a key head included), and this kernel runs after all
+// of them.  Workgroup (sequence r, value head h, column block cb) rolls its 64
+// v channels, and the q and k channels of its columns when h is the first
+// value head of its key head: state taps j = 0..2 <- the raw inputs at
+// positions T - 3 + j (old taps T + j where that is negative), as the
+// standalone conv kernel does.  The output waves roll after their last chunk:
+// the U waves read the v channels' old taps for their first chunk before the
+// first workgroup barrier.
 // (a fresh sequence rolls from a zero state: its old taps are not read)
 
 template <int D>
-__device__ __forceinline__ void conv_roll(const ConvRoll& cr, int64_t slot, bool fresh, int64_t bos, int64_t T, int h,
+__device__ __forceinline__ void conv_roll(const StateConv& cr, int64_t slot, bool fresh, int64_t bos, int64_t T, int h,
                                           int cb, int i0, int nthreads) {
   const bool qk = h % cr.ratio == 0;
   const int kh = h / cr.ratio;
@@ -1137,11 +1201,11 @@ struct SegList {
 // chain consumes stage j % 2 and writes exchange j % 2, the K and U waves fill
 // stage (j + 1) % 2, and the output waves read exchange (j - 1) % 2.  No wave
 // reads what another wave wrote before the barrier that separates them.
-template <int D>
+template <int D, bool kX>
 __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     const uint16_t* __restrict__ v, int64_t sv, const uint8_t* __restrict__ ws, const float* h0, float* hT,
     const int64_t* __restrict__ ids, int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hv,
-    uint16_t* __restrict__ o, ConvRoll cr, const uint8_t* __restrict__ fresh, SegList segs) {
+    uint16_t* __restrict__ o, StateConv cr, const uint8_t* __restrict__ fresh, SegList segs) {
   constexpr int NCB = D / kCB;
   constexpr int NR = D / 32;  // 32-row tiles of the state
   constexpr int KS = D / 16;  // k-steps over keys
@@ -1206,14 +1270,28 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 
 #define GDN_LEN(j_) static_cast<int>(min<int64_t>(kC, seqlen - (j_) * kC))
   if (wave >= 2) {
-    // the output waves have two chunk steps before their first product; one
-    // item per sequence (its first chunk, with outputs) rolls the conv state
-    if (cr.x && wave < 4 && c0 == 0 && mode == kSegOut)
-      conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], seq_bos, seq_len, h, cb, threadIdx.x - 128, 128);
-    if (nch == 0) return;
+    // one item per sequence (its first chunk, with outputs) rolls the conv
+    // state, in its output waves after their last chunk
+    const bool roll = kX && wave < 4 && c0 == 0 && mode == kSegOut;
+#define GDN_ROLL() conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], seq_bos, seq_len, h, cb, threadIdx.x - 128, 128)
+    if (nch == 0) {
+      if (roll) GDN_ROLL();
+      return;
+    }
     // roles with nothing to do for this item keep the chain's barrier count
     // (one before the first chunk, one per chunk)
-    if ((wave < 4 && mode != kSegOut) || (wave >= 4 && wave < 6 && mode == kSegTransition)) {
+    if ((wave < 4 && mode != kSegOut) || (wave >= 6 && mode == kSegTransition)) {
+      if (wave >= 6) {
+        // a transition item runs with U = 0: the U waves clear their tile in
+        // both stages once, and nothing else writes it
+        const int c = wave - 6;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) sm.st[b].U[c][mt][qd][lane] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
       for (int64_t i = 0; i <= nch; ++i) gdn::lds_barrier();
       return;
     }
@@ -1254,8 +1332,10 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
         o_chunk<D>(p1, sm.xc[1], sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, nt, lane);
       else
         o_chunk<D>(p0, sm.xc[0], sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, nt, lane);
+      if (roll) GDN_ROLL();
+#undef GDN_ROLL
     } else {
-      // --------------------------------------------------------- U and copy --
+      // ------------------------------------------------------------ U and K --
       // Chunk c's inputs live in register set c % 3; the loads of chunk j + 3
       // go out before chunk j + 1 is staged, two iterations ahead of their use.
       // The loop runs three chunks per trip so each set stays a fixed set of
@@ -1264,14 +1344,37 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #define GDN_PITER(jj, LD, ST, PREFETCH, STAGE)               \
   PREFETCH(LD, min<int64_t>((jj) + 3, nch - 1));             \
   gdn::keep_loads_here();                                    \
-  if ((jj) + 1 < nch) STAGE(ST, ((jj) + 1) & 1);             \
+  if ((jj) + 1 < nch) STAGE(ST, (jj) + 1);                   \
   gdn::lds_barrier();
-      if (wave < 6) {
-        const int c = wave - 4;
+      if (wave >= 6) {
+        const int c = wave - 6;
         const uint16_t* vh = v + static_cast<int64_t>(h) * D + cb * kCB;
         const int svi = static_cast<int>(sv);
+        // fused: the conv taps of the wave's channels into LDS, and the carry
+        // rows of the first chunk's window (the rows before the item, or
+        // before a sequence its state's taps -- zero, not read, when fresh)
+        s16x8_t carry[2] = {s16x8_t{0, 0, 0, 0, 0, 0, 0, 0}, s16x8_t{0, 0, 0, 0, 0, 0, 0, 0}};
+        if constexpr (kX) {
+          const int li = lane & 31, g = lane >> 5;
+          const int64_t ch0 = 2LL * cr.key_dim + static_cast<int64_t>(h) * D + cb * kCB + 32 * c;
+          if (lane < 16)
+            reinterpret_cast<uint4*>(sm.vw[c])[lane] = reinterpret_cast<const uint4*>(cr.w + ch0 * 4)[lane];
+          const int64_t ch = ch0 + 8 * g;
+          if (c0 != 0) {
+            const uint16_t* hp = vh + (bos - 3 + min(li, 2)) * sv + 32 * c + 8 * g;
+            carry[0] = *reinterpret_cast<const s16x8_t*>(hp);
+            carry[1] = *reinterpret_cast<const s16x8_t*>(hp + 16);
+          } else if (!(fresh && fresh[r])) {
+            const uint16_t* sp = cr.cstate + (ids ? ids[r] : r) * cr.ss_seq + ch * cr.ss_ch + min(li, 2);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) carry[hh][e] = static_cast<short>(sp[(16 * hh + e) * cr.ss_ch]);
+          }
+          wave_sync();
+        }
 #define GDN_UPF(P, jc) u_prefetch(P, vh, svi, rec0 + (jc) * rec_stride, bos + (jc) * kC, GDN_LEN(jc), c, lane)
-#define GDN_UST(P, b) u_stage<D>(P, sm.st[b], c, lane)
+#define GDN_UST(P, jc) u_stage<D, kX>(P, sm.st[(jc) & 1], c, lane, carry, sm.vtile[c], sm.vw[c])
         UPrefetch p0, p1, p2;
         GDN_UPF(p0, 0);
         gdn::keep_loads_here();  // the sets go out oldest first, as in the loop
@@ -1296,18 +1399,31 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #undef GDN_UPF
 #undef GDN_UST
       } else {
-        // One register set: each stage issues the next chunk's loads as soon
-        // as it has read the registers they land in.
-        const int pk = wave - 6;
-#define GDN_KSTAGE(jc, jn) k_stage<D>(p, sm.st[(jc) & 1], pk, lane, rec0 + (jn) * rec_stride)
-        KPrefetch<D> p;
-        k_prefetch_kt<D>(p, rec0, pk, lane);
-        k_prefetch_tw<D>(p, rec0, lane);
+        // Chunk c's inputs live in register set c % 2; each stage issues the
+        // loads of the chunk two ahead as soon as it has read the registers
+        // they land in, so a load has two chunk steps to arrive.  As for the
+        // other roles, every path issues the same loads, oldest set first, and
+        // the loop (two chunks per trip) has a single exit.
+        const int pk = wave - 4;
+#define GDN_KSTAGE(P, jc, jn) k_stage<D>(P, sm.st[(jc) & 1], pk, lane, rec0 + (jn) * rec_stride)
+        KPrefetch<D> p0, p1;
+        k_prefetch_kt<D>(p0, rec0, pk, lane);
+        k_prefetch_tw<D>(p0, rec0, lane);
         gdn::keep_loads_here();
-        GDN_KSTAGE(0, min<int64_t>(1, nch - 1));
+        k_prefetch_kt<D>(p1, rec0 + min<int64_t>(1, nch - 1) * rec_stride, pk, lane);
+        k_prefetch_tw<D>(p1, rec0 + min<int64_t>(1, nch - 1) * rec_stride, lane);
+        gdn::keep_loads_here();
+        GDN_KSTAGE(p0, 0, min<int64_t>(2, nch - 1));
         gdn::lds_barrier();
-        for (int64_t j = 0; j + 1 < nch; ++j) {  // an unconditional body keeps the load counters exact
-          GDN_KSTAGE(j + 1, min<int64_t>(j + 2, nch - 1));
+        int64_t j = 0;
+        for (; j + 2 < nch; j += 2) {
+          GDN_KSTAGE(p1, j + 1, min<int64_t>(j + 3, nch - 1));
+          gdn::lds_barrier();
+          GDN_KSTAGE(p0, j + 2, min<int64_t>(j + 4, nch - 1));
+          gdn::lds_barrier();
+        }
+        if (j + 1 < nch) {
+          GDN_KSTAGE(p1, j + 1, min<int64_t>(j + 3, nch - 1));
           gdn::lds_barrier();
         }
         gdn::lds_barrier();  // the last chunk: nothing left to stage
@@ -1356,78 +1472,81 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 
     // Operand fragments of each product are read from LDS as one batch ahead
     // of its MFMAs, so the reads overlap each other instead of each MFMA
-    // waiting out an LDS latency.
-    // S as fp16 fragments: B operand of W S here, A operand of the output
-    // wave's S^T Q'^T
+    // waiting out an LDS latency: first the U tiles that the first products
+    // accumulate onto, then -W in k-step order.
+    f32x16_t U[2];
+    h16x8_t wf[2][KS];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4_t u4 = B.U[wave][mt][qd][ln];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = u4[rr];
+      }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      wf[0][s] = B.W[s][ln];
+      wf[1][s] = B.W[KS + s][ln];
+    }
+    const float eg = B.vec[2 * kC];
+    __builtin_amdgcn_sched_barrier(0);
+    // S as fp16 fragments (B operand of W S here, A operand of the output
+    // wave's S^T Q'^T), packed while the reads are in flight.  Vn = U + (-W) S
+    // with both 32-token tiles interleaved; tile 1's last product is issued
+    // after the fence below, so tile 0 is packed while it runs.
     h16x8_t Sh[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) Sh[s] = (s & 1) ? pack_h8<8>(S[s >> 1]) : pack_h8<0>(S[s >> 1]);
-    // Vn = U + (-W) S, both 32-token tiles interleaved, accumulated onto U
-    f32x16_t U[2];
-    {
-      h16x8_t wf[2][KS];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        wf[0][s] = B.W[s][ln];
-        wf[1][s] = B.W[KS + s][ln];
-      }
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const f32x4_t u4 = B.U[wave][mt][qd][ln];
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = mode == kSegTransition ? 0.f : u4[rr];
-        }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        U[0] = mfma32(wf[0][s], Sh[s], U[0]);
-        U[1] = mfma32(wf[1][s], Sh[s], U[1]);
-      }
+    for (int s = 0; s < KS - 1; ++s) {
+      U[0] = mfma32(wf[0][s], Sh[s], U[0]);
+      U[1] = mfma32(wf[1][s], Sh[s], U[1]);
     }
-    // the exchange copy of S, and the decay of the old state, while W S runs
+    U[0] = mfma32(wf[0][KS - 1], Sh[KS - 1], U[0]);
+    // the exchange copy of S, the decay of the old state and the update's
+    // operand reads, while W S runs
 #pragma unroll
     for (int s = 0; s < KS; ++s) X.Sh[wave][s][ln] = Sh[s];
-    const float eg = B.vec[2 * kC];
 #pragma unroll
     for (int rt = 0; rt < NR; ++rt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) S[rt][e] *= eg;
-    // S <- e^gamma S + K^T diag(cK) Vn
-    {
-      h16x8_t kf[NR][4];
+    h16x8_t kf[NR][4];
 #pragma unroll
-      for (int rt = 0; rt < NR; ++rt)
+    for (int rt = 0; rt < NR; ++rt)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kf[rt][s] = B.Kt[rt * 4 + s][ln];
-      // cK of the tokens 32 mt + 8 i + 4 lgp + r held by this lane's Vn elements
-      f32x4_t ck[2][4];
+      for (int s = 0; s < 4; ++s) kf[rt][s] = B.Kt[rt * 4 + s][ln];
+    // cK of the tokens 32 mt + 8 i + 4 lgp + r held by this lane's Vn elements
+    f32x4_t ck[2][4];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          ck[mt][i] = *reinterpret_cast<const f32x4_t*>(&B.vec[kC + 32 * mt + 8 * i + 4 * (ln >> 5)]);
-      // Vn as fp16 (A operand of Vn^T A^T) and diag(cK) Vn as fp16 (B operand
-      // of the update)
-      h16x8_t Vh[4], Vk[4];
+      for (int i = 0; i < 4; ++i)
+        ck[mt][i] = *reinterpret_cast<const f32x4_t*>(&B.vec[kC + 32 * mt + 8 * i + 4 * (ln >> 5)]);
+    __builtin_amdgcn_sched_barrier(0);
+    U[1] = mfma32(wf[1][KS - 1], Sh[KS - 1], U[1]);
+    // S <- e^gamma S + K^T diag(cK) Vn, one token tile at a time: Vn as fp16
+    // (A operand of Vn^T A^T, to the exchange) and diag(cK) Vn as fp16 (B
+    // operand of the update); tile 1 is packed while tile 0's products run.
+    h16x8_t Vh[4], Vk[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Vh[s] = (s & 1) ? pack_h8<8>(U[s >> 1]) : pack_h8<0>(U[s >> 1]);
+    for (int mt = 0; mt < 2; ++mt) {
+      Vh[2 * mt] = pack_h8<0>(U[mt]);
+      Vh[2 * mt + 1] = pack_h8<8>(U[mt]);
+      X.Vh[wave][2 * mt][ln] = Vh[2 * mt];
+      X.Vh[wave][2 * mt + 1][ln] = Vh[2 * mt + 1];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) U[mt][4 * i + r] *= ck[mt][i][r];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) Vk[s] = (s & 1) ? pack_h8<8>(U[s >> 1]) : pack_h8<0>(U[s >> 1]);
+        for (int r = 0; r < 4; ++r) U[mt][4 * i + r] *= ck[mt][i][r];
+      Vk[2 * mt] = pack_h8<0>(U[mt]);
+      Vk[2 * mt + 1] = pack_h8<8>(U[mt]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 2 * mt; s < 2 * mt + 2; ++s)
 #pragma unroll
         for (int rt = 0; rt < NR; ++rt) S[rt] = mfma32(kf[rt][s], Vk[s], S[rt]);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) X.Vh[wave][s][ln] = Vh[s];
     }
     gdn::lds_barrier();
   }
@@ -1612,8 +1731,9 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
                  uint8_t* seg_ws, const ConvIn* cv, int phase, const uint8_t* select_host, hipStream_t stream) {
   const int64_t lwork = nc_bound * Hv;
   const int64_t lgrid = gdn::kNumXcd * ((lwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  ConvRoll cr{};
-  if (cv) cr = ConvRoll{cv->x, cv->sx, const_cast<uint16_t*>(cv->cstate), cv->ss_seq, cv->ss_ch, cv->key_dim, Hv / Hk};
+  StateConv cr{};
+  if (cv)
+    cr = StateConv{cv->x, cv->sx, const_cast<uint16_t*>(cv->cstate), cv->ss_seq, cv->ss_ch, cv->w, cv->key_dim, Hv / Hk};
   int st = GDN_OK;
   if (phase & kPhasePrep) {
     if (cv)
@@ -1631,8 +1751,12 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   auto state_launch = [&](const SegList& sl, int64_t items) {
     const int64_t cwork = items * per_item;
     const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
-    chunk_state_kernel<D><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
-        v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
+    if (cv)
+      chunk_state_kernel<D, true><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
+          v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
+    else
+      chunk_state_kernel<D, false><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
+          v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
     return gdn_launch_status();
   };
   const SegPlan pl = plan_segments(cu_host, select_host, n_seqs, Hv, D, max_segments, seg_ws != nullptr);
@@ -1743,17 +1867,10 @@ extern "C" int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16
                           ws, seg_ws, nullptr, kPhasePrep | kPhaseState, nullptr, s);
 }
 
-// workspace of the fused entry point: the records, then the conv's v rows
-static int64_t fused_v_offset(int64_t nc_bound, int Hv, int D) { return nc_bound * Hv * rec_bytes(D); }
-
-static int64_t fused_seg_offset(int64_t N, int64_t nc_bound, int Hv, int D) {
-  return fused_v_offset(nc_bound, Hv, D) + ((N * Hv * D * 2 + 255) / 256) * 256;
-}
-
+// workspace of the fused entry point: the same as the plain one's (the
+// records, then the segment scratch)
 extern "C" int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D) {
-  if (N < 0 || n_seqs < 0 || Hv <= 0 || (D != 64 && D != 128)) return -1;
-  const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
-  return fused_seg_offset(N, nc_bound, Hv, D) + seg_scratch_bytes(n_seqs, Hv, D);
+  return gdn_chunk_prefill_workspace_size(N, n_seqs, Hv, D);
 }
 
 extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_state,
@@ -1775,7 +1892,7 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   if (select_host && (!cu_seqlens_host || n_seqs > kMaxSegItems)) return GDN_ERR_INVALID_ARG;
   const int64_t C = 2LL * Hk * D + static_cast<int64_t>(Hv) * D;
   // 16-byte row segments of x, 8-byte output pieces, 256-byte workspace records
-  if (sx_row % 8 || sx_row < C || reinterpret_cast<uintptr_t>(x) % 16 ||
+  if (sx_row % 8 || sx_row < C || sx_row >= (1LL << 24) || reinterpret_cast<uintptr_t>(x) % 16 ||
       reinterpret_cast<uintptr_t>(conv_w) % 16 || reinterpret_cast<uintptr_t>(o) % 8 ||
       reinterpret_cast<uintptr_t>(workspace) % 256 || ss_ch < 3 || ss_seq < C * ss_ch ||
       ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
@@ -1784,16 +1901,16 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   if (workspace_bytes < gdn_conv_chunk_prefill_workspace_size(N, n_seqs, Hv, D)) return GDN_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  uint16_t* vws = reinterpret_cast<uint16_t*>(ws + fused_v_offset(nc_bound, Hv, D));
-  const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, fresh, conv_w, Hk * D, vws, a, b, A_log, dt_bias,
+  const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, fresh, conv_w, Hk * D, a, b, A_log, dt_bias,
                   param_is_fp32 ? 1 : 0};
-  const int64_t sv = static_cast<int64_t>(Hv) * D;
-  uint8_t* seg_ws = seg_scratch_bytes(n_seqs, Hv, D) ? ws + fused_seg_offset(N, nc_bound, Hv, D) : nullptr;
+  // the state kernel's U waves read the raw v channels and run their conv
+  const uint16_t* xv = x + 2LL * Hk * D;
+  uint8_t* seg_ws = seg_scratch_bytes(n_seqs, Hv, D) ? ws + nc_bound * Hv * rec_bytes(D) : nullptr;
   if (D == 128)
-    return launch_chunk<128>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
+    return launch_chunk<128>(x, sx_row, x, sx_row, xv, sx_row, nullptr, nullptr, h0, hT, state_ids, state_stride,
                              cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm,
                              o, ws, seg_ws, &cv, phase, select_host, s);
-  return launch_chunk<64>(x, sx_row, x, sx_row, vws, sv, nullptr, nullptr, h0, hT, state_ids, state_stride,
+  return launch_chunk<64>(x, sx_row, x, sx_row, xv, sx_row, nullptr, nullptr, h0, hT, state_ids, state_stride,
                           cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
                           ws, seg_ws, &cv, phase, select_host, s);
 }
