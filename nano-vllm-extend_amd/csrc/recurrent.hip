@@ -8,13 +8,21 @@
 // The last identity lets one cross-wave reduction pass produce both kv and o.
 //
 // HBM-bound: the D x D fp32 state tile of each (sequence, head) is read once
-// into registers and written once (plus optional per-token states).  One
+// into registers and written once (plus optional per-token states).  The
+// state stores are non-temporal: a layer's states come back only after every
+// other layer's have streamed through, so allocating them in the caches only
+// evicts other data (measured: 6 % faster with the pool out of cache, the
+// same with it cached).  One
 // workgroup of 256 threads owns a (sequence, head, v-block) tile of D x VB
 // columns, VB = D / NVB; each thread holds float4 column groups of NP rows so
 // every wave access is a contiguous run of VB*4 bytes per row.
 #include "gdn_common.h"
 
 namespace {
+
+__device__ __forceinline__ void store_nt(float* p, const float4& v) {
+  __builtin_nontemporal_store(gdn::f32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<gdn::f32x4_t*>(p));
+}
 
 template <int D, int NVB>
 __global__ __launch_bounds__(256) void recurrent_kernel(
@@ -147,7 +155,7 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
     if (inter) {
       float* ip = inter + (static_cast<int64_t>(b) * T + t) * Hv * D * D + static_cast<int64_t>(h) * D * D + col;
 #pragma unroll
-      for (int j = 0; j < NP; ++j) *reinterpret_cast<float4*>(ip + static_cast<int64_t>(r0 + RPP * j) * D) = S[j];
+      for (int j = 0; j < NP; ++j) store_nt(ip + static_cast<int64_t>(r0 + RPP * j) * D, S[j]);
     }
     if (r0 == 0) {
       uint2 u;
@@ -161,8 +169,7 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
   if (s_out) {
     float* sout = s_out + row * s_out_stride + static_cast<int64_t>(h) * D * D + col;
 #pragma unroll
-    for (int j = 0; j < NP; ++j)
-      *reinterpret_cast<float4*>(sout + static_cast<int64_t>(r0 + RPP * j) * D) = S[j];
+    for (int j = 0; j < NP; ++j) store_nt(sout + static_cast<int64_t>(r0 + RPP * j) * D, S[j]);
   }
 }
 
