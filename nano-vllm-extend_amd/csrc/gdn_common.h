@@ -39,24 +39,6 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) 
   lo = f2bf(x - bf2f(hi));
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
-
-// e^y through the hardware exp2 with the argument's rounding error put back:
-// y log2(e) = t + err exactly up to ~2^-48 |y| (two-product and the low part
-// of log2(e)), and 2^(t + err) = 2^t (1 + err ln 2) to second order.  A few
-// ulp in fp32 for |y| < 88 (the hardware exp2 itself is within 1 ulp);
-// overflow and underflow come out as inf and 0 like expf.
-__device__ __forceinline__ float exp_acc(float y) {
-  constexpr float kLog2e = 1.44269504088896340736f;       // rounded to fp32
-  constexpr float kLog2eLo = 1.925963033500011e-08f;      // log2(e) - kLog2e
-  constexpr float kLn2 = 0.69314718055994530942f;
-  const float t = y * kLog2e;
-  const float err = fmaf(y, kLog2e, -t) + y * kLog2eLo;
-  const float p = __builtin_amdgcn_exp2f(t);
-  return fmaf(p, err * kLn2, p);
-}
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
-
 // y = acc * sigmoid(acc), the reference conv epilogue's form (acc *
 // tl.sigmoid(acc), which lowers to an exp2 of the scaled argument and a
 // reciprocal): e^-acc as the hardware exp2 of -acc log2(e), then the hardware
@@ -71,8 +53,9 @@ __device__ __forceinline__ float silu_acc(float acc) {
 
 // Causal depthwise conv of width 4 at one channel (x0 the oldest input, x3 the
 // current one; w the channel's 4 taps) followed by SiLU, in one fixed operation
-// order: every varlen conv path (the standalone conv kernel and the conv fused
-// into the chunk prep kernel) goes through this, so they agree bit for bit.
+// order: every varlen conv path (the standalone conv kernel, and the conv fused
+// into the chunk kernels: q and k in the prep kernel, v in the state kernel's
+// U waves) goes through this, so they agree bit for bit.
 __device__ __forceinline__ float conv4_silu(float x0, float x1, float x2, float x3, const float* w) {
   float acc = x0 * w[0];
   acc = fmaf(x1, w[1], acc);
