@@ -825,7 +825,7 @@ struct __align__(16) StateSmem {
   StateXchg<D> xc[2];
   uint16_t ot[2][32 * kCB];  // each output wave's bf16 tile on its way out, swz<64>
   uint16_t vtile[2][67 * 16];  // fused: each U wave's conv window rows (one k-step's 16 channels)
-  uint16_t vw[2][32 * 4];      // fused: each U wave's 32 channels' conv taps
+  float vw[2][32 * 4];         // fused: each U wave's 32 channels' conv taps (fp32)
 };
 
 constexpr int kStateWaves = 8;
@@ -978,18 +978,16 @@ __device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int p
   }
 }
 
-// U waves: V^T of column tile c by the natural identity, then U = T'' V; U's
-// C tiles are stored lane-major for the chain wave that owns the columns.
 // Fused variant: the conv1d + SiLU of the lane's V elements (token 32 tt + li,
 // channels 32 c + 16 h + 8 g + 0..7) from the raw rows.  The window rows come
 // through the wave's LDS tile (tile row i = chunk row i - 3, the 16 channels
 // of one k-step h): the lanes' own rows, and in rows 0..2 the carry -- the
 // previous chunk's last 3 rows, or before a sequence its conv state's taps.
 // The carry for the next chunk is taken from the tile.  wt holds the 32
-// channels' taps (channel-major, 4 taps each).  Every conv goes through
+// channels' taps (fp32, 4 per channel).  Every conv goes through
 // gdn::conv4_silu in the standalone kernel's operation order, so the values
 // are bit-identical.
-__device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], uint16_t* tile, const uint16_t* wt,
+__device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], uint16_t* tile, const float* wt,
                                        int lane, s16x8_t (&vc)[2][2]) {
   const int li = lane & 31, g = lane >> 5;
 #pragma unroll
@@ -998,13 +996,11 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
     *reinterpret_cast<s16x8_t*>(&tile[(35 + li) * 16 + 8 * g]) = p.v[1][h];
     if (li < 3) *reinterpret_cast<s16x8_t*>(&tile[li * 16 + 8 * g]) = carry[h];
     wave_sync();
-    uint4 x[2][3], w4[4];
+    uint4 x[2][3];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int i = 0; i < 3; ++i) x[tt][i] = *reinterpret_cast<const uint4*>(&tile[(32 * tt + li + i) * 16 + 8 * g]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w4[j] = reinterpret_cast<const uint4*>(wt + (16 * h + 8 * g) * 4)[j];
     carry[h] = *reinterpret_cast<const s16x8_t*>(&tile[(64 + min(li, 2)) * 16 + 8 * g]);
     uint32_t y[2][4];
 #pragma unroll
@@ -1013,9 +1009,8 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
         const int e = 2 * e2 + cc;
-        float wk[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wk[j] = bf_elem(w4[(4 * e + j) / 8], (4 * e + j) % 8);
+        const float4 w4 = reinterpret_cast<const float4*>(wt)[16 * h + 8 * g + e];
+        const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
           yy[tt][cc] = gdn::conv4_silu(bf_elem(x[tt][0], e), bf_elem(x[tt][1], e), bf_elem(x[tt][2], e),
@@ -1030,9 +1025,11 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
   }
 }
 
+// U waves: V^T of column tile c by the natural identity, then U = T'' V; U's
+// C tiles are stored lane-major for the chain wave that owns the columns.
 template <int D, bool kX>
 __device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, int c, int lane, s16x8_t (&carry)[2],
-                                        uint16_t* tile, const uint16_t* wt) {
+                                        uint16_t* tile, const float* wt) {
   const int li = lane & 31, g = lane >> 5;
   const s16x8_t in0 = ident_frag(0, li, g), in1 = ident_frag(1, li, g);
   s16x8_t vc[2][2];
@@ -1357,8 +1354,12 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
         if constexpr (kX) {
           const int li = lane & 31, g = lane >> 5;
           const int64_t ch0 = 2LL * cr.key_dim + static_cast<int64_t>(h) * D + cb * kCB + 32 * c;
-          if (lane < 16)
-            reinterpret_cast<uint4*>(sm.vw[c])[lane] = reinterpret_cast<const uint4*>(cr.w + ch0 * 4)[lane];
+          if (lane < 32) {
+            // channel ch0 + lane's 4 taps, as fp32
+            const uint2 wb = reinterpret_cast<const uint2*>(cr.w + ch0 * 4)[lane];
+            reinterpret_cast<float4*>(sm.vw[c])[lane] =
+                make_float4(lo_half(wb.x), hi_half(wb.x), lo_half(wb.y), hi_half(wb.y));
+          }
           const int64_t ch = ch0 + 8 * g;
           if (c0 != 0) {
             const uint16_t* hp = vh + (bos - 3 + min(li, 2)) * sv + 32 * c + 8 * g;
