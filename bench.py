@@ -250,20 +250,31 @@ def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, R=20):
     slots with the pool's other slots, so no launch finds its states cached
     from the one before (the pool is larger than the last-level cache)."""
     B, Hk, Hv, D = x.shape[0], cfg["Hk"], cfg["Hv"], cfg["D"]
-    g, beta = pkg.ops.fused_g_beta(b, a, core.A_log, core.dt_bias, None)
-    y = pkg.ops.conv_decode_step(x, conv_pool, ids, core.conv_w)
     kd = Hk * D
-    q, k, v = y[:, :kd].view(B, 1, Hk, D), y[:, kd:2 * kd].view(B, 1, Hk, D), y[:, 2 * kd:].view(B, 1, Hv, D)
-    g1, b1 = g.view(B, 1, Hv), beta.view(B, 1, Hv)
     used = set(ids.tolist())
     other = [i for i in range(s_pool.shape[0]) if i not in used][:B]
     sets = [ids, torch.tensor(other, device=ids.device)] if len(other) == B else [ids]
-    pkg.ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_pool, sets[-1])
+    if core.sw.fused_decode:
+        # the kernel the decode step runs: gates + v conv + state update
+        qk = pkg.ops.conv_decode_step(x[:, :2 * kd], conv_pool[:, :2 * kd], ids, core.conv_w[:2 * kd])
+
+        def launch(sl):
+            pkg.ops.recurrent_decode_fused(qk, x, conv_pool, core.conv_w, b, a, core.A_log, core.dt_bias, s_pool,
+                                           sl, Hk, Hv, D)
+    else:
+        g, beta = pkg.ops.fused_g_beta(b, a, core.A_log, core.dt_bias, None)
+        y = pkg.ops.conv_decode_step(x, conv_pool, ids, core.conv_w)
+        q, k, v = y[:, :kd].view(B, 1, Hk, D), y[:, kd:2 * kd].view(B, 1, Hk, D), y[:, 2 * kd:].view(B, 1, Hv, D)
+        g1, b1 = g.view(B, 1, Hv), beta.view(B, 1, Hv)
+
+        def launch(sl):
+            pkg.ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_pool, sl)
+    launch(sets[-1])
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(R):
-        pkg.ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_pool, sets[i % len(sets)])
+        launch(sets[i % len(sets)])
     e1.record()
     torch.cuda.synchronize()
     return 1e3 * e0.elapsed_time(e1) / R
@@ -393,7 +404,8 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4),
                          "traffic": _profiled_traffic("recurrent_decode_config2"),
-                         "kernel": "recurrent_kernel<128,1>", "kernel_us": round(rec_us, 2),
+                         "kernel": "recurrent_kernel<128,1,true> (the decode step's fused kernel: gates, v "
+                                   "conv with its state roll, state update)", "kernel_us": round(rec_us, 2),
                          "timing": "20 back-to-back launches between one event pair, alternating two disjoint "
                                    "slot sets of the pool",
                          "algorithmic_bytes_per_launch": state_bytes}}

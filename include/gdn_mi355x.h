@@ -218,6 +218,30 @@ int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t*
                   void* stream);
 
 /*
+ * The decode step after the q/k conv, in one launch: the gates (as
+ * gdn_g_beta), the conv1d + SiLU of the v channels with their conv-state roll
+ * (as gdn_conv_decode), and the in-place recurrent update (as gdn_recurrent
+ * with T = 1, s_in = s_out = s_pool).  Replaces fused_g_beta
+ * (nanovllm/models/qwen3_5.py:345-360) and the v part of conv_decode_step
+ * (:546-558) ahead of recurrent_gdn_inplace (:597-613) in the T == 1 branch
+ * (:1008-1030), with the same results bit for bit.
+ *   q, k   the decode conv's q and k outputs (gdn_conv_decode over the first
+ *          2*Hk*D channels), row strides sq_b, sk_b, head dim contiguous
+ *   x      [B, C] raw rows (C = 2*Hk*D + Hv*D), row stride sx_row (multiple of 4)
+ *   conv_pool, cp_slot, cp_ch, conv_w: as gdn_conv_decode with K = 4, over all
+ *          C channels (only the v channels are read and rolled here)
+ *   a, b   [B, Hv] bf16 contiguous; A_log, dt_bias [Hv] (param_is_fp32 as gdn_g_beta)
+ *   s_pool, s_stride, ids, o, scale, l2norm: as gdn_recurrent (o [B, Hv, D])
+ * One launch; each v channel belongs to one workgroup, which rolls its taps.
+ */
+int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const uint16_t* k, int64_t sk_b,
+                               const uint16_t* x, int64_t sx_row, uint16_t* conv_pool, int64_t cp_slot,
+                               int64_t cp_ch, const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
+                               const void* A_log, const void* dt_bias, int param_is_fp32, float* s_pool,
+                               int64_t s_stride, const int64_t* ids, uint16_t* o, int B, int Hk, int Hv, int D,
+                               float scale, int l2norm, void* stream);
+
+/*
  * Speculative-verify commit: pool[ids[b]] <- inter[b, accepted[b] - 1]
  * (accepted[b] in [1, T]; 0 leaves the slot untouched).  No counterpart in
  * the reference (spec decode is disabled for qwen3_5, nanovllm/config.py:84);

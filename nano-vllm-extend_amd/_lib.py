@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "gdn_conv_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],
     "gdn_recurrent": [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
                       _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
+    "gdn_recurrent_decode_fused": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32,
+                                   _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _f32, _i32, _p],
     "gdn_state_commit": [_p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _p],
     "gdn_rmsnorm_gated": [_p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p],
     "gdn_rmsnorm_gated_ranges": [_p, _i64, _p, _i64, _p, _p, _p, _i32, _i64, _i32, _i32, _f32, _p],

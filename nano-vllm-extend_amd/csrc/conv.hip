@@ -220,10 +220,10 @@ __global__ __launch_bounds__(256) void conv_decode_kernel(
   uint16_t* ys = reinterpret_cast<uint16_t*>(&yu);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float acc = gdn::bf2f(xs[i]) * gdn::bf2f(wr[i * kK + 3]);
-#pragma unroll
-    for (int j = 0; j < 3; ++j) acc += gdn::bf2f(s[i][j]) * gdn::bf2f(wr[i * kK + j]);
-    ys[i] = gdn::f2bf(silu_acc(acc));
+    const float wk[4] = {gdn::bf2f(wr[i * kK]), gdn::bf2f(wr[i * kK + 1]), gdn::bf2f(wr[i * kK + 2]),
+                         gdn::bf2f(wr[i * kK + 3])};
+    ys[i] = gdn::f2bf(gdn::conv_decode_silu(gdn::bf2f(xs[i]), gdn::bf2f(s[i][0]), gdn::bf2f(s[i][1]),
+                                            gdn::bf2f(s[i][2]), wk));
   }
   *reinterpret_cast<uint4*>(y + b * sy_row + c0) = yu;
   // roll: s0 <- s1, s1 <- s2, s2 <- x (bit copies)

@@ -64,6 +64,18 @@ __device__ __forceinline__ float conv4_silu(float x0, float x1, float x2, float 
   return silu_acc(acc);
 }
 
+// Decode conv of one channel (one token): y = silu(x w[3] + s0 w[0] + s1 w[1] +
+// s2 w[2]) in that accumulation order (the reference's decode epilogue), with
+// s0 the oldest state tap.  Shared by the decode conv kernel and the fused
+// decode step, so they agree bit for bit.
+__device__ __forceinline__ float conv_decode_silu(float x, float s0, float s1, float s2, const float* w) {
+  float acc = x * w[3];
+  acc = fmaf(s0, w[0], acc);
+  acc = fmaf(s1, w[1], acc);
+  acc = fmaf(s2, w[2], acc);
+  return silu_acc(acc);
+}
+
 // The reference writes the rolled conv state as (x + s) with the other operand
 // masked to zero, which maps -0.0 to +0.0 and is otherwise a bit copy.
 __device__ __forceinline__ uint16_t roll_value(uint16_t bits) {

@@ -24,14 +24,31 @@ __device__ __forceinline__ void store_nt(float* p, const float4& v) {
   __builtin_nontemporal_store(gdn::f32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<gdn::f32x4_t*>(p));
 }
 
-template <int D, int NVB>
+// Inputs of the fused decode step (one token per sequence): the gates from
+// their raw inputs, and the v channels' conv with its state roll from the raw
+// rows, computed in the kernel (q and k come from the decode conv as usual).
+// Each v channel belongs to one workgroup, so its roll races with no reader.
+struct DecodeIn {
+  const uint16_t* xv;      // raw rows at the first v channel, row stride sx (NULL: not fused)
+  int64_t sx;
+  uint16_t* vpool;         // conv state pool at the first v channel: slot s, channel c, tap j
+  int64_t sp_slot, sp_ch;  //   at vpool + s*sp_slot + c*sp_ch + j
+  const uint16_t* wv;      // [Hv*D, 4] conv taps of the v channels
+  const uint16_t* a;       // [B, Hv] gate inputs
+  const uint16_t* b;
+  const void* A_log;       // [Hv], bf16 or fp32 (param_f32)
+  const void* dt_bias;
+  int param_f32;
+};
+
+template <int D, int NVB, bool kFused>
 __global__ __launch_bounds__(256) void recurrent_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, const uint16_t* __restrict__ k,
     int64_t sk_b, int64_t sk_t, const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t,
     const float* __restrict__ g, const uint16_t* __restrict__ beta, const float* s_in,
     int64_t s_in_stride, float* s_out, int64_t s_out_stride, const int64_t* __restrict__ ids,
     float* __restrict__ inter, uint16_t* __restrict__ o, int B, int T, int Hk, int Hv,
-    float scale, int l2norm) {
+    float scale, int l2norm, DecodeIn din) {
   constexpr int VB = D / NVB;     // state columns per workgroup
   constexpr int CPR = VB / 4;     // float4 column groups per row
   constexpr int RPP = 256 / CPR;  // rows per pass of the workgroup
@@ -96,10 +113,39 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
       if (lane == 0) skq[buf] = kq;
     }
     const int64_t gi = (static_cast<int64_t>(b) * T + t) * Hv + h;
-    const float eg = expf(g[gi]);
-    const float bt = gdn::bf2f(beta[gi]);
+    float eg, bt;
     float vv[4];
-    {
+    uint16_t vx[4], vs[4][3];  // fused: the raw v inputs and the old state taps, for the roll
+    if constexpr (kFused) {
+      // the gate kernel's arithmetic (g in fp32, beta rounded to bf16), and the
+      // decode conv of this thread's 4 v channels (rounded to bf16 as the conv
+      // kernel's output is)
+      eg = expf(gdn::gate_g(gdn::bf2f(din.a[gi]), gdn::load_param(din.A_log, h, din.param_f32),
+                            gdn::load_param(din.dt_bias, h, din.param_f32)));
+      bt = gdn::bf2f(gdn::gate_beta(gdn::bf2f(din.b[gi])));
+      const int64_t ch = static_cast<int64_t>(h) * D + col;
+      const uint2 xu = *reinterpret_cast<const uint2*>(din.xv + static_cast<int64_t>(b) * din.sx + ch);
+      const uint4 w01 = reinterpret_cast<const uint4*>(din.wv + ch * 4)[0];
+      const uint4 w23 = reinterpret_cast<const uint4*>(din.wv + ch * 4)[1];
+      const uint16_t* sp = din.vpool + row * din.sp_slot + ch * din.sp_ch;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) vs[i][j] = sp[static_cast<int64_t>(i) * din.sp_ch + j];
+      const uint16_t* xs = reinterpret_cast<const uint16_t*>(&xu);
+      const uint16_t* ws = reinterpret_cast<const uint16_t*>(&w01);
+      const uint16_t* ws2 = reinterpret_cast<const uint16_t*>(&w23);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t* wi = i < 2 ? ws + 4 * i : ws2 + 4 * (i - 2);
+        const float wk[4] = {gdn::bf2f(wi[0]), gdn::bf2f(wi[1]), gdn::bf2f(wi[2]), gdn::bf2f(wi[3])};
+        vx[i] = xs[i];
+        vv[i] = gdn::bf2f(gdn::f2bf(gdn::conv_decode_silu(gdn::bf2f(xs[i]), gdn::bf2f(vs[i][0]), gdn::bf2f(vs[i][1]),
+                                                          gdn::bf2f(vs[i][2]), wk)));
+      }
+    } else {
+      eg = expf(g[gi]);
+      bt = gdn::bf2f(beta[gi]);
       const uint16_t* vp = v + static_cast<int64_t>(b) * sv_b + static_cast<int64_t>(t) * sv_t + static_cast<int64_t>(h) * D + col;
       const uint2 u = *reinterpret_cast<const uint2*>(vp);
       const uint16_t* us = reinterpret_cast<const uint16_t*>(&u);
@@ -107,6 +153,18 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
       for (int i = 0; i < 4; ++i) vv[i] = gdn::bf2f(us[i]);
     }
     __syncthreads();
+    if constexpr (kFused) {
+      // every thread of these columns has read the old taps: roll (bit copies)
+      if (r0 == 0) {
+        uint16_t* sp = din.vpool + row * din.sp_slot + (static_cast<int64_t>(h) * D + col) * din.sp_ch;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sp[static_cast<int64_t>(i) * din.sp_ch] = vs[i][1];
+          sp[static_cast<int64_t>(i) * din.sp_ch + 1] = vs[i][2];
+          sp[static_cast<int64_t>(i) * din.sp_ch + 2] = vx[i];
+        }
+      }
+    }
 
     // --- decay, then partial S^T k and S^T q over this thread's rows ---
     float kv[4] = {0.f, 0.f, 0.f, 0.f}, qv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -195,13 +253,25 @@ int launch_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16
                      int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t, const float* g,
                      const uint16_t* beta, const float* s_in, int64_t s_in_stride, float* s_out,
                      int64_t s_out_stride, const int64_t* ids, float* inter, uint16_t* o, int B,
-                     int T, int Hk, int Hv, float scale, int l2norm, hipStream_t stream) {
+                     int T, int Hk, int Hv, float scale, int l2norm, const DecodeIn& din, hipStream_t stream) {
   const int64_t work = static_cast<int64_t>(B) * Hv * NVB;
   const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  recurrent_kernel<D, NVB><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
-      q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
-      ids, inter, o, B, T, Hk, Hv, scale, l2norm);
+  if (din.xv)
+    recurrent_kernel<D, NVB, true><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
+        q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
+        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din);
+  else
+    recurrent_kernel<D, NVB, false><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
+        q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
+        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din);
   return gdn_launch_status();
+}
+
+// v-split: more workgroups when there are few (b, h) tiles, so the launch
+// still covers the 256 CUs with enough bytes in flight
+static int recurrent_nvb(int B, int Hv) {
+  const int64_t heads = static_cast<int64_t>(B) * Hv;
+  return heads >= 2048 ? 1 : (heads >= 512 ? 2 : 4);
 }
 
 }  // namespace
@@ -224,12 +294,10 @@ extern "C" int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, cons
       reinterpret_cast<uintptr_t>(o) % 8)
     return GDN_ERR_INVALID_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t heads = static_cast<int64_t>(B) * Hv;
-  // Split the v columns over more workgroups when there are few (b, h) tiles,
-  // so the launch still covers the 256 CUs with enough bytes in flight.
-  const int nvb = heads >= 2048 ? 1 : (heads >= 512 ? 2 : 4);
+  const int nvb = recurrent_nvb(B, Hv);
+  const DecodeIn din{};
 #define GDN_REC_ARGS q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, \
-                     s_out_stride, ids, inter, o, B, T, Hk, Hv, scale, l2norm, s
+                     s_out_stride, ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, s
   if (D == 128) {
     if (nvb == 1) return launch_recurrent<128, 1>(GDN_REC_ARGS);
     if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);
@@ -251,4 +319,39 @@ extern "C" int gdn_state_commit(float* pool, int64_t slot_stride, const int64_t*
   state_commit_kernel<<<dim3(static_cast<unsigned>(B * Hv)), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
       pool, slot_stride, ids, inter, accepted, T, Hv, D);
   return gdn_launch_status();
+}
+
+extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const uint16_t* k, int64_t sk_b,
+                                          const uint16_t* x, int64_t sx_row, uint16_t* conv_pool,
+                                          int64_t cp_slot, int64_t cp_ch, const uint16_t* conv_w,
+                                          const uint16_t* a, const uint16_t* b, const void* A_log,
+                                          const void* dt_bias, int param_is_fp32, float* s_pool,
+                                          int64_t s_stride, const int64_t* ids, uint16_t* o, int B, int Hk,
+                                          int Hv, int D, float scale, int l2norm, void* stream) {
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (B < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
+  if (B == 0) return GDN_OK;
+  if (!q || !k || !x || !conv_pool || !conv_w || !a || !b || !A_log || !dt_bias || !s_pool || !ids || !o)
+    return GDN_ERR_INVALID_ARG;
+  const int64_t vbase = 2LL * Hk * D;  // first v channel of a raw row
+  // float4 state access; 8-byte raw v and 16-byte tap reads
+  if (s_stride % 4 || reinterpret_cast<uintptr_t>(s_pool) % 16 || sx_row % 4 ||
+      reinterpret_cast<uintptr_t>(x) % 8 || reinterpret_cast<uintptr_t>(conv_w) % 16 ||
+      reinterpret_cast<uintptr_t>(o) % 8 || cp_ch < 3 || cp_slot < (vbase + static_cast<int64_t>(Hv) * D) * cp_ch)
+    return GDN_ERR_INVALID_ARG;
+  const DecodeIn din{x + vbase, sx_row, conv_pool + vbase * cp_ch, cp_slot, cp_ch, conv_w + vbase * 4, a, b,
+                     A_log, dt_bias, param_is_fp32 ? 1 : 0};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int nvb = recurrent_nvb(B, Hv);
+#define GDN_REC_ARGS q, sq_b, 0, k, sk_b, 0, nullptr, 0, 0, nullptr, nullptr, s_pool, s_stride, s_pool, s_stride, \
+                     ids, nullptr, o, B, 1, Hk, Hv, scale, l2norm, din, s
+  if (D == 128) {
+    if (nvb == 1) return launch_recurrent<128, 1>(GDN_REC_ARGS);
+    if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);
+    return launch_recurrent<128, 4>(GDN_REC_ARGS);
+  }
+  if (nvb == 1) return launch_recurrent<64, 1>(GDN_REC_ARGS);
+  if (nvb == 2) return launch_recurrent<64, 2>(GDN_REC_ARGS);
+  return launch_recurrent<64, 4>(GDN_REC_ARGS);
+#undef GDN_REC_ARGS
 }

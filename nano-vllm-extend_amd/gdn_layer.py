@@ -40,6 +40,7 @@ class Switches:
     fla_recurrent: bool = True
     fused_prefill: bool = True
     split_state: bool = False
+    fused_decode: bool = True
 
     @classmethod
     def from_env(cls) -> "Switches":
@@ -51,7 +52,8 @@ class Switches:
                    fla_chunk=e("FLA_CHUNK", "1") == "1",
                    fla_recurrent=e("FLA_RECURRENT", "1") == "1",
                    fused_prefill=e("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1",
-                   split_state=e("NANOVLLM_GDN_SPLIT_STATE", "0") == "1")
+                   split_state=e("NANOVLLM_GDN_SPLIT_STATE", "0") == "1",
+                   fused_decode=e("NANOVLLM_GDN_FUSED_DECODE", "1") == "1")
 
 
 # State-pass split policy (off by default: measured at config 1 the split
@@ -184,6 +186,16 @@ class GatedDeltaNetCore:
         self._to(mixed.device)
         B = mixed.shape[0]
         Hk, Hv, D = self.Hk, self.Hv, self.D
+        kd = self.key_dim
+        if self.sw.fused_decode and self.sw.gbeta and self.sw.conv_kernel and self.sw.inplace and self.K == 4:
+            # q/k conv, then gates + v conv + recurrent update in one kernel
+            # (the same results as the calls below)
+            with self._timed("conv_decode"):
+                qk = ops.conv_decode_step(mixed[:, :2 * kd], conv_cache[:, :2 * kd], ids, self.conv_w[:2 * kd])
+            with self._timed("recurrent_decode"):
+                out = ops.recurrent_decode_fused(qk, mixed, conv_cache, self.conv_w, b, a, self.A_log, self.dt_bias,
+                                                 s_cache, ids, Hk, Hv, D)
+            return self._norm(out.view(B, Hv, D), z.view(B, Hv, D))
         g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
         if self.sw.conv_kernel:
             with self._timed("conv_decode"):
@@ -192,7 +204,6 @@ class GatedDeltaNetCore:
             window = torch.cat([conv_cache[ids], mixed.unsqueeze(-1)], dim=-1)
             conv_cache[ids] = window[..., 1:]
             y = F.silu(F.conv1d(window, self.conv_w.unsqueeze(1), groups=self.conv_dim))[..., 0]
-        kd = self.key_dim
         q = y[:, :kd].view(B, 1, Hk, D)
         k = y[:, kd:2 * kd].view(B, 1, Hk, D)
         v = y[:, 2 * kd:].view(B, 1, Hv, D)

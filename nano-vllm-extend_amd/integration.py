@@ -26,6 +26,13 @@ Qwen3_5GatedDeltaNet._gdn_prefill_varlen (qwen3_5.py:922-965) with one whose
 gates, conv and chunk rule are the single fused call
 ops.conv_chunk_prefill_varlen (the same results as the three calls the
 method makes, bit for bit), on the layer's own pools and slot ids.
+
+With NANOVLLM_GDN_FUSED_DECODE=1 (the default; it also needs the gate, conv
+and in-place kernels on) it replaces Qwen3_5GatedDeltaNet._gdn_padded
+(qwen3_5.py:967-1085) with one whose T == 1 branch runs the q/k decode conv
+and then ops.recurrent_decode_fused (gates, the v channels' conv and the
+in-place recurrent update in one kernel; the same results bit for bit); other
+T keep the original method.
 """
 from __future__ import annotations
 
@@ -69,6 +76,38 @@ def _fused_prefill_method(mod, orig):
     return _gdn_prefill_varlen
 
 
+def _fused_decode_method(orig):
+    def _gdn_padded(self, x, lens, ids, T):
+        """Fused T == 1 branch of Qwen3_5GatedDeltaNet._gdn_padded
+        (nanovllm/models/qwen3_5.py:967-1030, :1079-1085); other T and conv
+        widths keep the original method."""
+        if T != 1 or self.conv_kernel != 4:
+            return orig(self, x, lens, ids, T)
+        n = x.size(0)
+        Hv, Dv = self.num_v_heads, self.head_v_dim
+        b = self.in_proj_b(x).reshape(n, Hv)
+        a = self.in_proj_a(x).reshape(n, Hv)
+        A_log = self.A_log[self._v_head_slice]
+        dt_bias = self.dt_bias[self._v_head_slice]
+        z = self.in_proj_z(x)
+        proj = self.in_proj_qkv(x).reshape(-1, self.conv_dim)
+        w = self.conv1d.weight.view(self.conv_dim, 4)
+        kd = self.key_dim
+        qk = ops.conv_decode_step(proj[:, :2 * kd], self.conv_cache[:, :2 * kd], ids, w[:2 * kd])
+        out = ops.recurrent_decode_fused(qk, proj, self.conv_cache, w, b, a, A_log, dt_bias, self.s_cache, ids,
+                                         self.num_k_heads, Hv, self.head_k_dim)
+        core = self.norm(out.reshape(n, 1, Hv, Dv), z.view(n, 1, Hv, Dv))
+        return self.out_proj(core.reshape(n, 1, self.value_dim))
+
+    return _gdn_padded
+
+
+def _fused_decode_enabled() -> bool:
+    e = os.environ.get
+    return (e("NANOVLLM_GDN_FUSED_DECODE", "1") == "1" and e("NANOVLLM_GDN_GBETA", "1") == "1"
+            and e("NANOVLLM_CONV_TRITON", "1") == "1" and e("NANOVLLM_GDN_INPLACE", "1") == "1")
+
+
 def _fused_prefill_enabled() -> bool:
     e = os.environ.get
     return (e("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1" and e("NANOVLLM_GDN_GBETA", "1") == "1"
@@ -96,19 +135,22 @@ def install(mod) -> dict:
     mod._USE_FLA_RECURRENT = os.environ.get("FLA_RECURRENT", "1") == "1"
     mod._USE_GDN_VARLEN = mod._USE_FLA_CHUNK and os.environ.get("NANOVLLM_GDN_VARLEN", "1") == "1"
     cls = getattr(mod, "Qwen3_5GatedDeltaNet", None)
-    if cls is not None and _fused_prefill_enabled():
+    if cls is not None and _fused_prefill_enabled() and hasattr(cls, "_gdn_prefill_varlen"):
         prev["Qwen3_5GatedDeltaNet._gdn_prefill_varlen"] = cls.__dict__.get("_gdn_prefill_varlen")
         cls._gdn_prefill_varlen = _fused_prefill_method(mod, cls._gdn_prefill_varlen)
+    if cls is not None and _fused_decode_enabled() and hasattr(cls, "_gdn_padded"):
+        prev["Qwen3_5GatedDeltaNet._gdn_padded"] = cls.__dict__.get("_gdn_padded")
+        cls._gdn_padded = _fused_decode_method(cls._gdn_padded)
     return prev
 
 
 def uninstall(mod, prev: dict) -> None:
     for name, val in prev.items():
-        if name == "Qwen3_5GatedDeltaNet._gdn_prefill_varlen":
-            cls = mod.Qwen3_5GatedDeltaNet
+        if name.startswith("Qwen3_5GatedDeltaNet."):
+            cls, attr = mod.Qwen3_5GatedDeltaNet, name.split(".", 1)[1]
             if val is None:
-                del cls._gdn_prefill_varlen
+                delattr(cls, attr)
             else:
-                cls._gdn_prefill_varlen = val
+                setattr(cls, attr, val)
             continue
         setattr(mod, name, val)

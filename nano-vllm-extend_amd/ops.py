@@ -462,6 +462,44 @@ def recurrent_gdn_inplace(q, k, v, g, beta, s_pool, ids):
     return _recurrent(q, k, v, g, beta, s_pool, s_pool, ids, None, None, True)
 
 
+def recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bias, s_pool, ids, Hk, Hv, D,
+                           scale=None):
+    """The decode step after the q/k conv, in one kernel: the gates from a, b,
+    the v channels' conv1d + SiLU (their conv state rolled in place at `ids`)
+    and the in-place recurrent update.  qk [B, 2*Hk*D] is conv_decode_step's
+    output for the q and k channels; mixed [B, C] the raw rows; conv_pool
+    [slots, C, 3] and s_pool [slots, Hv, D, D] per-layer pool views; b, a
+    [B, Hv] bf16.  Returns out [B, 1, Hv, D] bf16, the same bits as
+    fused_g_beta -> conv_decode_step -> recurrent_gdn_inplace
+    (nanovllm/models/qwen3_5.py:1008-1030)."""
+    dev = _check_cuda(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bias, s_pool, ids)
+    for t, nm in ((qk, "qk"), (mixed, "mixed"), (conv_pool, "conv_pool"), (b, "b"), (a, "a")):
+        _bf16(t, nm)
+    B, C = mixed.shape
+    kd = Hk * D
+    assert C == 2 * kd + Hv * D and qk.shape == (B, 2 * kd)
+    assert qk.stride(1) == 1 and mixed.stride(1) == 1 and conv_pool.stride(2) == 1
+    w = conv_weight.reshape(C, -1)
+    assert w.shape[1] == 4
+    w = w.contiguous()
+    b, a = b.contiguous(), a.contiguous()
+    assert b.shape == (B, Hv) and a.shape == (B, Hv)
+    assert a_log.dtype == dt_bias.dtype and a_log.dtype in (torch.bfloat16, torch.float32)
+    a_log, dt_bias = a_log.contiguous(), dt_bias.contiguous()
+    assert a_log.numel() == Hv and dt_bias.numel() == Hv
+    assert _state_view_ok(s_pool, Hv, D)
+    ids64 = ids.to(torch.int64).contiguous()
+    out = torch.empty(B, 1, Hv, D, dtype=mixed.dtype, device=mixed.device)
+    if scale is None:
+        scale = D ** -0.5
+    _lib.call("gdn_recurrent_decode_fused", _lib.ptr(qk), qk.stride(0), _lib.ptr(qk[:, kd:]), qk.stride(0),
+              _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_pool), conv_pool.stride(0), conv_pool.stride(1),
+              _lib.ptr(w), _lib.ptr(a), _lib.ptr(b), _lib.ptr(a_log), _lib.ptr(dt_bias),
+              int(a_log.dtype == torch.float32), _lib.ptr(s_pool), s_pool.stride(0), _lib.ptr(ids64),
+              _lib.ptr(out), B, Hk, Hv, D, float(scale), 1, _stream(dev))
+    return out
+
+
 def recurrent_gated_delta_rule(query, key, value, g=None, beta=None, initial_state=None, scale=None,
                                output_final_state=True, use_qk_l2norm_in_kernel=True, **kwargs):
     """Gathered-state recurrent rule (T >= 1 tokens per row).

@@ -26,7 +26,7 @@ def test_header_declares_entry_points():
     d = _declared()
     for name in ("gdn_abi_version", "gdn_g_beta", "gdn_conv_varlen", "gdn_conv_decode", "gdn_conv_padded",
                  "gdn_chunk_prefill", "gdn_chunk_prefill_workspace_size", "gdn_recurrent", "gdn_state_commit",
-                 "gdn_rmsnorm_gated"):
+                 "gdn_rmsnorm_gated", "gdn_conv_chunk_prefill", "gdn_recurrent_decode_fused"):
         assert name in d
 
 
@@ -78,6 +78,16 @@ def test_argument_validation_before_launch(pkg):
                                None) == _lib.GDN_ERR_INVALID_ARG
     # NULL operands with real work are rejected
     assert lib.gdn_g_beta(None, None, None, None, 0, None, None, None, 32, 16, None) == _lib.GDN_ERR_INVALID_ARG
+    # the fused decode step: unsupported head dim, NULL operands, grouped heads that do not divide
+    fd = lib.gdn_recurrent_decode_fused
+    assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
+              4, 2, 4, 96, 1.0, 1, None) == _lib.GDN_ERR_UNSUPPORTED
+    assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
+              4, 2, 4, 128, 1.0, 1, None) == _lib.GDN_ERR_INVALID_ARG
+    assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
+              4, 3, 4, 128, 1.0, 1, None) == _lib.GDN_ERR_INVALID_ARG
+    assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
+              0, 2, 4, 128, 1.0, 1, None) == _lib.GDN_OK
     # empty work is a no-op success
     assert lib.gdn_g_beta(None, None, None, None, 0, None, None, None, 0, 16, None) == _lib.GDN_OK
     with pytest.raises(_lib.GDNKernelError):

@@ -41,6 +41,7 @@ SWITCH_SETS = [
     {"inplace": False},
     {"varlen": False},
     {"fused_prefill": False},
+    {"fused_decode": False},
 ]
 
 
@@ -331,6 +332,59 @@ def test_installed_prefill_method_equals_layer_core(pkg, dev):
         layer.out_proj = lambda x: x
         layer.conv_cache, layer.s_cache = conv0.clone(), s0.clone()
         out = layer._gdn_prefill_varlen(None, lens, ids)
+    finally:
+        pkg.integration.uninstall(mod, prev)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(layer.s_cache, sp1)
+    assert torch.equal(layer.conv_cache.view(torch.int16), cp1.view(torch.int16))
+
+
+def test_installed_decode_method_equals_layer_core(pkg, dev):
+    """integration.install's fused _gdn_padded (T == 1) on a stand-in layer
+    with the reference's attribute names gives the layer core's decode (with
+    the fused decode switched off: fused_g_beta -> conv_decode_step ->
+    recurrent_gdn_inplace) bit for bit, and updates the same pools."""
+    import types
+
+    gen = torch.Generator().manual_seed(36)
+    Hk, Hv, D = 2, 4, 128
+    C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
+    B = 5
+    mixed, z, b, a = (t.to(dev) for t in _rows(gen, B, C, Hv, D))
+    slots = 8
+    conv0 = torch.randn(slots, C, 3, generator=gen).to(BF16).to(dev)
+    s0 = (torch.randn(slots, Hv, D, D, generator=gen) * 0.1).to(dev)
+    ids = torch.tensor([6, 1, 3, 0, 5], device=dev)
+
+    core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w, fused_decode=False)
+    cp1, sp1 = conv0.clone(), s0.clone()
+    ref = core.decode(mixed, z, b, a, ids, cp1, sp1).reshape(B, 1, Hv * D)
+
+    mod = types.ModuleType("qwen3_5_stub")
+
+    class Qwen3_5GatedDeltaNet:
+        def _gdn_padded(self, x, lens, ids, T):
+            raise AssertionError("the original method must not run")
+
+    mod.Qwen3_5GatedDeltaNet = Qwen3_5GatedDeltaNet
+    prev = pkg.integration.install(mod)
+    try:
+        layer = Qwen3_5GatedDeltaNet()
+        layer.num_k_heads, layer.num_v_heads, layer.head_k_dim, layer.head_v_dim = Hk, Hv, D, D
+        layer.key_dim, layer.value_dim, layer.conv_dim, layer.conv_kernel = Hk * D, Hv * D, C, 4
+        layer.in_proj_b = lambda h: b.view(B, 1, Hv)
+        layer.in_proj_a = lambda h: a.view(B, 1, Hv)
+        layer.in_proj_z = lambda h: z.view(B, 1, Hv * D)
+        layer.in_proj_qkv = lambda h: mixed.view(B, 1, C)
+        layer.A_log, layer.dt_bias, layer._v_head_slice = A_log.to(dev), dt_bias.to(dev), slice(0, Hv)
+        layer.conv1d = types.SimpleNamespace(weight=conv_w.to(dev).view(C, 1, 4))
+        norm = pkg.ops.Qwen3_5RMSNormGated(D)
+        norm.weight.data = norm_w.to(dev)
+        layer.norm = norm
+        layer.out_proj = lambda x: x
+        layer.conv_cache, layer.s_cache = conv0.clone(), s0.clone()
+        out = layer._gdn_padded(torch.empty(B, 1, 8, device=dev), None, ids, 1)
     finally:
         pkg.integration.uninstall(mod, prev)
     torch.cuda.synchronize()

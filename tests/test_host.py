@@ -88,9 +88,34 @@ def test_install_replaces_varlen_prefill_method(pkg, monkeypatch):
     assert layer._gdn_prefill_varlen(None, [1], None) == "original"
     pkg.integration.uninstall(mod, prev)
     assert Qwen3_5GatedDeltaNet.__dict__["_gdn_prefill_varlen"] is orig
+    assert "_gdn_padded" not in Qwen3_5GatedDeltaNet.__dict__   # no such method on the stub: left alone
     monkeypatch.setenv("NANOVLLM_GDN_FUSED_PREFILL", "0")
     prev = pkg.integration.install(mod)
     assert Qwen3_5GatedDeltaNet.__dict__["_gdn_prefill_varlen"] is orig
+    pkg.integration.uninstall(mod, prev)
+
+
+def test_install_replaces_padded_method(pkg, monkeypatch):
+    mod = types.ModuleType("qwen3_5_stub")
+
+    class Qwen3_5GatedDeltaNet:
+        def _gdn_padded(self, x, lens, ids, T):
+            return "original"
+
+    mod.Qwen3_5GatedDeltaNet = Qwen3_5GatedDeltaNet
+    orig = Qwen3_5GatedDeltaNet.__dict__["_gdn_padded"]
+    prev = pkg.integration.install(mod)
+    assert Qwen3_5GatedDeltaNet.__dict__["_gdn_padded"] is not orig
+    layer = Qwen3_5GatedDeltaNet()
+    layer.conv_kernel = 4
+    assert layer._gdn_padded(None, None, None, 5) == "original"   # T > 1 keeps the original method
+    layer.conv_kernel = 3
+    assert layer._gdn_padded(None, None, None, 1) == "original"   # other widths too
+    pkg.integration.uninstall(mod, prev)
+    assert Qwen3_5GatedDeltaNet.__dict__["_gdn_padded"] is orig
+    monkeypatch.setenv("NANOVLLM_GDN_FUSED_DECODE", "0")
+    prev = pkg.integration.install(mod)
+    assert Qwen3_5GatedDeltaNet.__dict__["_gdn_padded"] is orig
     pkg.integration.uninstall(mod, prev)
 
 
