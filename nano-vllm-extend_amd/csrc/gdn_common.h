@@ -39,6 +39,21 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) 
   lo = f2bf(x - bf2f(hi));
 }
 
+// e^y through the hardware exp2 with the argument's rounding error put back:
+// y log2(e) = t + err exactly up to ~2^-48 |y| (two-product and the low part
+// of log2(e)), and 2^(t + err) = 2^t (1 + err ln 2) to second order.  A few
+// ulp in fp32 for |y| < 88 (the hardware exp2 itself is within 1 ulp);
+// overflow and underflow come out as inf and 0 like expf.
+__device__ __forceinline__ float exp_acc(float y) {
+  constexpr float kLog2e = 1.44269504088896340736f;       // rounded to fp32
+  constexpr float kLog2eLo = 1.925963033500011e-08f;      // log2(e) - kLog2e
+  constexpr float kLn2 = 0.69314718055994530942f;
+  const float t = y * kLog2e;
+  const float err = fmaf(y, kLog2e, -t) + y * kLog2eLo;
+  const float p = __builtin_amdgcn_exp2f(t);
+  return fmaf(p, err * kLn2, p);
+}
+
 // y = acc * sigmoid(acc), the reference conv epilogue's form (acc *
 // tl.sigmoid(acc), which lowers to an exp2 of the scaled argument and a
 // reciprocal): e^-acc as the hardware exp2 of -acc log2(e), then the hardware
