@@ -336,6 +336,7 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
   const int64_t vbase = 2LL * Hk * D;  // first v channel of a raw row
   // float4 state access; 8-byte raw v and 16-byte tap reads
   if (s_stride % 4 || reinterpret_cast<uintptr_t>(s_pool) % 16 || sx_row % 4 ||
+      sx_row < vbase + static_cast<int64_t>(Hv) * D || s_stride < static_cast<int64_t>(Hv) * D * D ||
       reinterpret_cast<uintptr_t>(x) % 8 || reinterpret_cast<uintptr_t>(conv_w) % 16 ||
       reinterpret_cast<uintptr_t>(o) % 8 || cp_ch < 3 || cp_slot < (vbase + static_cast<int64_t>(Hv) * D) * cp_ch)
     return GDN_ERR_INVALID_ARG;
