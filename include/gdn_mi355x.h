@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 1
+#define GDN_ABI_VERSION 2
 
 #define GDN_OK 0
 #define GDN_ERR_INVALID_ARG (-1) /* shape / stride / pointer rejected */
@@ -191,6 +191,7 @@ int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_sta
 /* Workspace bytes of gdn_conv_chunk_prefill; -1 on bad args. */
 int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
 
+
 /*
  * Recurrent gated delta rule for decode: T >= 1 tokens per sequence, state
  * read once and written once.  Replaces recurrent_gdn_inplace /
@@ -205,9 +206,17 @@ int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int
  *   s_in  state of sequence b at s_in + row(b)*s_in_stride ([Hv, D, D] dense)
  *   s_out final state written at s_out + row(b)*s_out_stride (may equal s_in:
  *         in-place pool update); NULL = not written
- *   row(b) = ids ? ids[b] : b
+ *   row(b) = ids ? ids[b] : b; with ids (or B > 1) both slot strides must
+ *         be at least Hv*D*D (rows may not overlap), else GDN_ERR_INVALID_ARG
  *   inter [B, T, Hv, D, D] fp32 per-token states (NULL = not written)
  *   o     [B, T, Hv, D] bf16 contiguous
+ *   src_states, src_accepted, src_T (src_states and src_accepted both NULL,
+ *         or both set): deferred commit of a speculative-verify step.  Row b
+ *         starts from src_states[b, src_accepted[b] - 1] (src_states the
+ *         previous verify's per-token states [B, src_T, Hv, D, D], rows in
+ *         the same order; src_accepted int64 [B]) when src_accepted[b] >= 1,
+ *         else from its s_in row.  src_states may be this call's inter: each
+ *         state is read before it is written.
  * Duplicate ids (dummy slot) are tolerated.  D must be 64 or 128.
  */
 int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k,
@@ -215,7 +224,7 @@ int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t*
                   const float* g, const uint16_t* beta, const float* s_in, int64_t s_in_stride,
                   float* s_out, int64_t s_out_stride, const int64_t* ids, float* inter,
                   uint16_t* o, int B, int T, int Hk, int Hv, int D, float scale, int l2norm,
-                  void* stream);
+                  const float* src_states, const int64_t* src_accepted, int src_T, void* stream);
 
 /*
  * The decode step after the q/k conv, in one launch: the gates (as
@@ -232,6 +241,14 @@ int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t*
  *          C channels (only the v channels are read and rolled here)
  *   a, b   [B, Hv] bf16 contiguous; A_log, dt_bias [Hv] (param_is_fp32 as gdn_g_beta)
  *   s_pool, s_stride, ids, o, scale, l2norm: as gdn_recurrent (o [B, Hv, D])
+ *   z, sz_b, norm_w, eps: with z != NULL the gated RMSNorm of the layer
+ *          (Qwen3_5RMSNormGated, qwen3_5.py:1083-1085, :121-131) is applied in
+ *          the same kernel and o receives its output instead of the core
+ *          output, the same bits as gdn_rmsnorm_gated on that core output:
+ *          z [B, Hv*D] bf16 gate rows (row stride sz_b), norm_w [D] bf16.
+ *          The kernel then runs whole heads per workgroup, as it does without
+ *          z from B*Hv >= 2048; below that it otherwise splits a head's
+ *          columns over workgroups, which sums S^T k in another order
  * One launch; each v channel belongs to one workgroup, which rolls its taps.
  */
 int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const uint16_t* k, int64_t sk_b,
@@ -239,11 +256,13 @@ int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const uint16_t* 
                                int64_t cp_ch, const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
                                const void* A_log, const void* dt_bias, int param_is_fp32, float* s_pool,
                                int64_t s_stride, const int64_t* ids, uint16_t* o, int B, int Hk, int Hv, int D,
-                               float scale, int l2norm, void* stream);
+                               float scale, int l2norm, const uint16_t* z, int64_t sz_b, const uint16_t* norm_w,
+                               float eps, void* stream);
 
 /*
  * Speculative-verify commit: pool[ids[b]] <- inter[b, accepted[b] - 1]
- * (accepted[b] in [1, T]; 0 leaves the slot untouched).  No counterpart in
+ * (accepted[b] in [1, T]; 0 leaves the slot untouched); slot_stride >=
+ * Hv*D*D.  No counterpart in
  * the reference (spec decode is disabled for qwen3_5, nanovllm/config.py:84);
  * it consumes the per-token state format of gdn_recurrent.
  */

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = Path(os.environ.get("GDN_MI355X_LIB", Path(__file__).resolve().parent / "lib" / "libgdn_mi355x.so"))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 GDN_OK = 0
 GDN_ERR_INVALID_ARG = -1
@@ -48,9 +48,10 @@ SIGNATURES: dict[str, list] = {
                                _i32, _i32, _p, _i32, _i64, _i32, _i32, _i32, _f32, _i32, _p, _p, _i64, _p],
     "gdn_conv_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],
     "gdn_recurrent": [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
-                      _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p],
+                      _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _p, _i32, _p],
     "gdn_recurrent_decode_fused": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32,
-                                   _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _f32, _i32, _p],
+                                   _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64, _p, _f32,
+                                   _p],
     "gdn_state_commit": [_p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _p],
     "gdn_rmsnorm_gated": [_p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p],
     "gdn_rmsnorm_gated_ranges": [_p, _i64, _p, _i64, _p, _p, _p, _i32, _i64, _i32, _i32, _f32, _p],

@@ -92,6 +92,17 @@ __device__ __forceinline__ uint32_t f2h2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h16x2_t));
 }
 
+// fp16x2 -> two fp32 (exact)
+__device__ __forceinline__ gdn::f32x2_t h22f(uint32_t u) {
+  return __builtin_convertvector(__builtin_bit_cast(h16x2_t, u), gdn::f32x2_t);
+}
+
+// the rounding residuals of a pair already packed as f2h2(a, b)
+__device__ __forceinline__ uint32_t f2h2_lo(float a, float b, uint32_t hi) {
+  const gdn::f32x2_t h = h22f(hi);
+  return f2h2(a - h[0], b - h[1]);
+}
+
 // elements [o, o + 8) of a C tile -> fp16 operand fragment
 template <int O>
 __device__ __forceinline__ h16x8_t pack_h8(const f32x16_t& a) {
@@ -128,6 +139,8 @@ __device__ __forceinline__ void wave_sync() {
 //                      (row tile 1, k-steps 0..3)
 //   TB  [6] frags      T'' = T diag(beta), same order
 //   AQ  [6] frags      A = lower_incl(scale q^.k^ e^{G_t - G_s}), same order
+//   AL  [6] frags      the rounding residual of A: fp16(A_fp32 - fp32(AQ)), same
+//                      order, so that A_fp32 = AQ + AL to ~22 significant bits
 //   VEC fp32 [256]     cQ[64] = scale e^{G_t} / ||q_t||,
 //                      cK[64] = e^{gamma - G_t} / ||k_t|| (0 past the sequence end),
 //                      e^gamma
@@ -138,8 +151,9 @@ struct Rec {
   static constexpr int TW = 0;
   static constexpr int TB = 6144;
   static constexpr int AQ = 12288;
-  static constexpr int VEC = 18432;
-  static constexpr int QP = 19456;
+  static constexpr int AL = 18432;
+  static constexpr int VEC = 24576;
+  static constexpr int QP = 25600;
 };
 __host__ __device__ constexpr int64_t rec_kt(int D) { return Rec::QP + 128LL * D; }
 // bytes of one record (a multiple of 256)
@@ -722,10 +736,13 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
       }
       // tokens 16 ns + 4 lg .. + 3 sit at the positions of quad qswap
       const int pos = qswap(16 * ns + 4 * lg);
-      uint2 pk;
+      uint2 pk, lo;
       pk.x = f2h2(a[0], a[1]);
       pk.y = f2h2(a[2], a[3]);
+      lo.x = f2h2_lo(a[0], a[1], pk.x);
+      lo.y = f2h2_lo(a[2], a[3], pk.y);
       *reinterpret_cast<uint2*>(arec + tri_frag_byte(t, pos)) = pk;
+      *reinterpret_cast<uint2*>(arec + (Rec::AL - Rec::AQ) + tri_frag_byte(t, pos)) = lo;
     }
   }
   __syncthreads();
@@ -810,22 +827,30 @@ struct __align__(16) StateStage {
   float vec[256];               // record VEC: cQ[64], cK[64], e^gamma
 };
 
-// What the chain waves hand the output waves for one chunk: their fp16
-// operand fragments of S (before the chunk's update) and of Vn, in register
-// order.
+// What the chain waves hand the output waves, in register order: the fp16
+// operand fragments of S before the chunk's update (one buffer: the output
+// waves read it in the same barrier interval, after the chain wave's flag
+// says it is there), and of Vn as a rounded part and its rounding residual
+// (Vn = Vh + Vl to ~22 significant bits; two buffers: the output waves use
+// them one interval later).
 template <int D>
-struct __align__(16) StateXchg {
+struct __align__(16) StateXchgS {
   h16x8_t Sh[2][D / 16][64];
+};
+struct __align__(16) StateXchgV {
   h16x8_t Vh[2][4][64];
+  h16x8_t Vl[2][4][64];
 };
 
 template <int D>
 struct __align__(16) StateSmem {
   StateStage<D> st[2];
-  StateXchg<D> xc[2];
+  StateXchgS<D> xs;
+  StateXchgV xv[2];
   uint16_t ot[2][32 * kCB];  // each output wave's bf16 tile on its way out, swz<64>
   uint16_t vtile[2][67 * 16];  // fused: each U wave's conv window rows (one k-step's 16 channels)
   float vw[2][32 * 4];         // fused: each U wave's 32 channels' conv taps (fp32)
+  int sflag[4];                // chain wave w: chunks whose S it has put in xs (sflag[w] = j + 1)
 };
 
 constexpr int kStateWaves = 8;
@@ -837,12 +862,15 @@ constexpr int kStateWaves = 8;
 //   w 0, 1  chain: the recurrence for state columns 32 w .. 32 w + 31 of the
 //           workgroup's 64 (Vn = U - W S, S <- e^gamma S + K^T diag(cK) Vn)
 //   w 2, 3  output: O^T = S^T Q'^T + Vn^T A^T of token tile w - 2 (both
-//           chains' columns), one chunk behind the chain
+//           chains' columns): S^T Q'^T in the chain's interval (once the
+//           chain waves' flags show S), Vn^T A^T in the next one, as three
+//           fp16 products (Vh A + Vl A + Vh A_lo) that carry Vn and A to ~22
+//           significant bits
 //   w 4, 5  K: the record's K^T and -W = -T' K for key tiles w - 4 (+ 2), and
 //           the record's vec block, into the stage
 //   w 6, 7  U: U = T'' V for value-column tile w - 6 (fused variant: V is the
 //           conv1d + SiLU of the raw v channels, computed here)
-// Per chunk the chain, U, output and K roles issue 32, 10, 24 and 12
+// Per chunk the chain, U, output and K roles issue 32, 10, 40 and 12
 // matrix-core products of 32x32x16.
 
 // Per-lane prefetch registers of one chunk, one struct per role.
@@ -872,9 +900,12 @@ struct UPrefetch {
 };
 
 template <int D>
-struct OPrefetch {
+struct QPrefetch {
   s16x8_t q[D / 16];  // Q' fragments of the wave's token tile, per key step
-  s16x8_t a[4];       // A fragments 2 nt .. 2 nt + 3: k-steps 0..1 of tile 0, 0..3 of tile 1
+};
+struct APrefetch {
+  s16x8_t a[4];   // A fragments 2 nt .. 2 nt + 3: k-steps 0..1 of tile 0, 0..3 of tile 1
+  s16x8_t al[4];  // the same fragments of A's residual
 };
 
 // Raw buffer access: a wave-uniform base in the descriptor, the per-lane
@@ -929,14 +960,20 @@ __device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int
 }
 
 template <int D>
-__device__ __forceinline__ void o_prefetch(OPrefetch<D>& p, const uint8_t* rec, int nt, int lane) {
+__device__ __forceinline__ void q_prefetch(QPrefetch<D>& p, const uint8_t* rec, int nt, int lane) {
   const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) p.q[s] = buf_ld(r, 16 * lane, Rec::QP + 1024 * (nt * (D / 16) + s));
-  // four fragments for either tile (tile 0 uses the first two), so every
-  // path issues the same loads
+}
+
+// four fragments for either tile (tile 0 uses the first two), so every path
+// issues the same loads
+__device__ __forceinline__ void a_prefetch(APrefetch& p, const uint8_t* rec, int nt, int lane) {
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) p.a[ks] = buf_ld(r, 16 * lane, Rec::AQ + 1024 * (2 * nt + ks));
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) p.al[ks] = buf_ld(r, 16 * lane, Rec::AL + 1024 * (2 * nt + ks));
 }
 
 // K waves: K^T and -W of key tiles pk (+ 2) into the stage, as fragments.
@@ -1065,46 +1102,78 @@ __device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, in
   }
 }
 
-// Output waves: O^T = S^T Q'^T + Vn^T A^T for token tile nt and the 32
-// columns of each chain (two independent accumulation chains), stored straight
-// from the C tiles: lane (token t, g) holds value columns 8 i + 4 g + 0..3.
+// Output waves, first half of a chunk: acc = S^T Q'^T for token tile nt and
+// the 32 columns of each chain (two independent accumulation chains), once
+// both chain waves have put the chunk's S in the exchange (flag >= j + 1).
 template <int D>
-__device__ __forceinline__ void o_chunk(const OPrefetch<D>& p, const StateXchg<D>& X, uint16_t* ot, uint16_t* ob,
-                                        int len, int Hv, int nt, int lane) {
+__device__ __forceinline__ void o_inter(const QPrefetch<D>& p, const StateXchgS<D>& X, const int* sflag,
+                                        int64_t j, int lane, f32x16_t (&acc)[2]) {
   constexpr int KS = D / 16;
-  h16x8_t sh[2][KS], vh[2][4];
+  const int want = static_cast<int>(j) + 1;
+  while (min(__hip_atomic_load(&sflag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
+             __hip_atomic_load(&sflag[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < want)
+    __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  h16x8_t sh[2][KS];
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
+  for (int c = 0; c < 2; ++c)
 #pragma unroll
     for (int s = 0; s < KS; ++s) sh[c][s] = X.Sh[c][s][lane];
+  __builtin_amdgcn_sched_barrier(0);
+  acc[0] = zero16();
+  acc[1] = zero16();
 #pragma unroll
-    for (int s = 0; s < 4; ++s) vh[c][s] = X.Vh[c][s][lane];
+  for (int s = 0; s < KS; ++s) {
+    acc[0] = mfma32(sh[0][s], as_h8(p.q[s]), acc[0]);
+    acc[1] = mfma32(sh[1][s], as_h8(p.q[s]), acc[1]);
   }
+}
+
+// Output waves, second half (the interval after): acc += Vn^T A^T as
+// Vh A + Vl A + Vh A_lo, then the bf16 tile goes out.  The C tiles give each
+// lane 4 columns of a row per store; rows go out whole instead (8 lanes per
+// 128-byte row), through the wave's own LDS tile.
+__device__ __forceinline__ void o_intra_store(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[2],
+                                              uint16_t* ot, uint16_t* ob, int len, int Hv, int D, int nt,
+                                              int lane) {
+  h16x8_t vh[2][4], vl[2][4];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      vh[c][s] = X.Vh[c][s][lane];
+      vl[c][s] = X.Vl[c][s][lane];
+    }
   __builtin_amdgcn_sched_barrier(0);
   // Tile 0 has no A entries at token steps 2 and 3; the fragments loaded there
   // (tile 1's, so that both tiles issue the same loads) are masked to zero.
   // Every product then runs on every path, and no loaded register is left
   // unread.
   const uint32_t keep_hi = nt ? 0xffffffffu : 0u;
-  h16x8_t af[4];
+  h16x8_t af[4], alf[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const u32x4_t x = __builtin_bit_cast(u32x4_t, p.a[s]);
+    const u32x4_t y = __builtin_bit_cast(u32x4_t, p.al[s]);
     af[s] = __builtin_bit_cast(h16x8_t, s < 2 ? x : (x & keep_hi));
+    alf[s] = __builtin_bit_cast(h16x8_t, s < 2 ? y : (y & keep_hi));
   }
-  f32x16_t acc[2] = {zero16(), zero16()};
+  // the residual products, then the rounded one
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    acc[0] = mfma32(sh[0][s], as_h8(p.q[s]), acc[0]);
-    acc[1] = mfma32(sh[1][s], as_h8(p.q[s]), acc[1]);
+  for (int s = 0; s < 4; ++s) {
+    acc[0] = mfma32(vl[0][s], af[s], acc[0]);
+    acc[1] = mfma32(vl[1][s], af[s], acc[1]);
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    acc[0] = mfma32(vh[0][s], alf[s], acc[0]);
+    acc[1] = mfma32(vh[1][s], alf[s], acc[1]);
   }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     acc[0] = mfma32(vh[0][s], af[s], acc[0]);
     acc[1] = mfma32(vh[1][s], af[s], acc[1]);
   }
-  // The C tiles give each lane 4 columns of a row per store; rows go out
-  // whole instead (8 lanes per 128-byte row), through the wave's own LDS tile.
   const int tl = lane & 31, g = lane >> 5;
 #pragma unroll
   for (int c = 0; c < 2; ++c)
@@ -1192,7 +1261,7 @@ struct SegList {
   SegItem it[kMaxSegItems];
 };
 
-// grid = 8 * ceil(n_items * Hv * NCB / 8), NCB = D / 64; block = 64 * 8.
+// grid = 8 * ceil(n_items * Hv / 8) * NCB, NCB = D / 64; block = 64 * 8.
 // Workgroup (item: sequence r or a segment of it, value head h, column block cb) owns state columns
 // cb*64 .. cb*64 + 63.  One workgroup barrier per chunk j: before it the
 // chain consumes stage j % 2 and writes exchange j % 2, the K and U waves fill
@@ -1209,9 +1278,20 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   __shared__ StateSmem<D> sm;
   __shared__ long long s_base;
 
+  // Work item wi = (item * Hv + h) * NCB + cb.  The (item, head) pairs go
+  // round-robin over the 8 XCDs (workgroup b runs on XCD b % 8), so every
+  // sequence's heads spread over all XCDs and a long sequence does not leave
+  // its XCD's L2 and fabric link loaded while others idle; the NCB column
+  // blocks of a head are consecutive on one XCD and share its record reads
+  // in that XCD's L2.  grid = 8 * ceil(n_items * Hv / 8) * NCB.
   const int64_t n_items = segs.n ? segs.n : n_seqs;
-  const int64_t wi = gdn::xcd_remap(blockIdx.x, n_items * Hv * NCB);
-  if (wi < 0) return;
+  int64_t wi;
+  {
+    const int64_t xcd = blockIdx.x % gdn::kNumXcd, k = blockIdx.x / gdn::kNumXcd;
+    const int64_t pair = (k / NCB) * gdn::kNumXcd + xcd;
+    if (pair >= n_items * Hv) return;
+    wi = pair * NCB + k % NCB;
+  }
   const int cb = static_cast<int>(wi % NCB);
   const int h = static_cast<int>((wi / NCB) % Hv);
   const int item = static_cast<int>(wi / (static_cast<int64_t>(NCB) * Hv));
@@ -1256,6 +1336,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
     if (threadIdx.x == 0) s_base = part;
   }
+  if (threadIdx.x < 4) sm.sflag[threadIdx.x] = 0;
   __syncthreads();
   const int64_t cbase = s_base + c0;
   const int64_t rec_stride = static_cast<int64_t>(Hv) * rec_bytes(D);
@@ -1294,41 +1375,61 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     }
     if (wave < 4) {
       // ------------------------------------------------------------ output --
-      // Chunk c's operands live in register set c % 2; its loads go out right
-      // after chunk c - 2 is done, about one and a half iterations before use.
-      // The compiler's load counters must stay exact for that, so no load may
-      // look younger than it is: every path issues the same loads (past the
-      // last chunk they repeat it), the sets go out oldest first, and the loop
-      // has a single exit (two chunks per trip, the odd one after it).
+      // In the interval of chunk c (between workgroup barriers c and c + 1)
+      // an output wave finishes chunk c - 1 (Vn^T A^T, the store) and runs
+      // S^T Q'^T of chunk c.  Chunk c's Q' fragments live in register set
+      // c % 2 and its A fragments in set c % 2; each set is reloaded (for
+      // chunk c + 2, resp. c + 1) as soon as it has been read, so a load has
+      // more than an interval to arrive.  The compiler's load counters must
+      // stay exact for that, so no load may look younger than it is: every
+      // path issues the same loads (past the last chunk they repeat it), the
+      // sets go out oldest first, and the loop has a single exit (two chunks
+      // per trip, the odd one after it).
       const int nt = wave - 2;
       uint16_t* oh = o + (bos * Hv + h) * D + cb * kCB;
       const int64_t ostride = static_cast<int64_t>(kC) * Hv * D;
-      OPrefetch<D> p0, p1;
-      o_prefetch<D>(p0, rec0, nt, lane);
+      QPrefetch<D> q0, q1;
+      APrefetch a0, a1;
+      f32x16_t acc[2];
+      const uint8_t* rec1 = rec0 + min<int64_t>(1, nch - 1) * rec_stride;
+      q_prefetch<D>(q0, rec0, nt, lane);
       gdn::keep_loads_here();  // the sets go out oldest first, as in the loop
-      o_prefetch<D>(p1, rec0 + min<int64_t>(1, nch - 1) * rec_stride, nt, lane);
+      a_prefetch(a0, rec0, nt, lane);
+      gdn::keep_loads_here();
+      q_prefetch<D>(q1, rec1, nt, lane);
+      gdn::keep_loads_here();
+      a_prefetch(a1, rec1, nt, lane);
       gdn::keep_loads_here();
       gdn::lds_barrier();
-      gdn::lds_barrier();  // iteration 0: no chunk finished yet
-#define GDN_OITER(jj, PC)                                                                     \
-  o_chunk<D>(PC, sm.xc[((jj) - 1) & 1], sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, nt, lane); \
-  __builtin_amdgcn_sched_barrier(0);                                                          \
-  o_prefetch<D>(PC, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);          \
-  gdn::keep_loads_here();                                                                     \
+      // interval 0: S^T Q'^T of chunk 0
+      o_inter<D>(q0, sm.xs, sm.sflag, 0, lane, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      q_prefetch<D>(q0, rec0 + min<int64_t>(2, nch - 1) * rec_stride, nt, lane);
+      gdn::keep_loads_here();
+      gdn::lds_barrier();
+#define GDN_OITER(jj, QC, AP)                                                                               \
+  o_intra_store(AP, sm.xv[((jj) - 1) & 1], acc, sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, D, nt, lane); \
+  __builtin_amdgcn_sched_barrier(0);                                                                        \
+  a_prefetch(AP, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);                            \
+  gdn::keep_loads_here();                                                                                   \
+  o_inter<D>(QC, sm.xs, sm.sflag, jj, lane, acc);                                                           \
+  __builtin_amdgcn_sched_barrier(0);                                                                        \
+  q_prefetch<D>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, nt, lane);                        \
+  gdn::keep_loads_here();                                                                                   \
   gdn::lds_barrier();
       int64_t j = 1;
       for (; j + 1 < nch; j += 2) {
-        GDN_OITER(j, p0)      // computes chunk j - 1 (even), loads chunk j + 1
-        GDN_OITER(j + 1, p1)  // computes chunk j (odd), loads chunk j + 2
+        GDN_OITER(j, q1, a0)      // finishes chunk j - 1 (even), starts chunk j (odd)
+        GDN_OITER(j + 1, q0, a1)  // finishes chunk j (odd), starts chunk j + 1 (even)
       }
       if (j < nch) {
-        GDN_OITER(j, p0)
+        GDN_OITER(j, q1, a0)
       }
 #undef GDN_OITER
       if ((nch - 1) & 1)
-        o_chunk<D>(p1, sm.xc[1], sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, nt, lane);
+        o_intra_store(a1, sm.xv[1], acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
       else
-        o_chunk<D>(p0, sm.xc[0], sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, nt, lane);
+        o_intra_store(a0, sm.xv[0], acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
       if (roll) GDN_ROLL();
 #undef GDN_ROLL
     } else {
@@ -1464,7 +1565,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   if (nch > 0) gdn::lds_barrier();
   for (int64_t jc = 0; jc < nch; ++jc) {
     const StateStage<D>& B = sm.st[jc & 1];
-    StateXchg<D>& X = sm.xc[jc & 1];
+    StateXchgV& X = sm.xv[jc & 1];
     // Re-derive lane indices from an opaque copy each chunk so the compiler
     // does not keep every lane-dependent address live across the loop.
     int tid_l = static_cast<int>(threadIdx.x);
@@ -1505,10 +1606,13 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       U[1] = mfma32(wf[1][s], Sh[s], U[1]);
     }
     U[0] = mfma32(wf[0][KS - 1], Sh[KS - 1], U[0]);
-    // the exchange copy of S, the decay of the old state and the update's
-    // operand reads, while W S runs
+    // the exchange copy of S (then the flag that says it is there), the decay
+    // of the old state and the update's operand reads, while W S runs
 #pragma unroll
-    for (int s = 0; s < KS; ++s) X.Sh[wave][s][ln] = Sh[s];
+    for (int s = 0; s < KS; ++s) sm.xs.Sh[wave][s][ln] = Sh[s];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    if (ln == 0) __hip_atomic_store(&sm.sflag[wave], static_cast<int>(jc) + 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_WORKGROUP);
 #pragma unroll
     for (int rt = 0; rt < NR; ++rt)
 #pragma unroll
@@ -1530,24 +1634,37 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     // S <- e^gamma S + K^T diag(cK) Vn, one token tile at a time: Vn as fp16
     // (A operand of Vn^T A^T, to the exchange) and diag(cK) Vn as fp16 (B
     // operand of the update); tile 1 is packed while tile 0's products run.
+    // The exchange gets Vn as its fp16 rounding Vh and the rounding's
+    // residual Vl, formed while the update's products run.
     h16x8_t Vh[4], Vk[4];
+    f32x16_t Uk[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       Vh[2 * mt] = pack_h8<0>(U[mt]);
       Vh[2 * mt + 1] = pack_h8<8>(U[mt]);
-      X.Vh[wave][2 * mt][ln] = Vh[2 * mt];
-      X.Vh[wave][2 * mt + 1][ln] = Vh[2 * mt + 1];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) U[mt][4 * i + r] *= ck[mt][i][r];
-      Vk[2 * mt] = pack_h8<0>(U[mt]);
-      Vk[2 * mt + 1] = pack_h8<8>(U[mt]);
+        for (int r = 0; r < 4; ++r) Uk[mt][4 * i + r] = U[mt][4 * i + r] * ck[mt][i][r];
+      Vk[2 * mt] = pack_h8<0>(Uk[mt]);
+      Vk[2 * mt + 1] = pack_h8<8>(Uk[mt]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int s = 2 * mt; s < 2 * mt + 2; ++s)
 #pragma unroll
         for (int rt = 0; rt < NR; ++rt) S[rt] = mfma32(kf[rt][s], Vk[s], S[rt]);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4_t hi = __builtin_bit_cast(u32x4_t, Vh[s]);
+      u32x4_t lo;
+#pragma unroll
+      for (int p2 = 0; p2 < 4; ++p2) {
+        const int e = 8 * (s & 1) + 2 * p2;
+        lo[p2] = f2h2_lo(U[s >> 1][e], U[s >> 1][e + 1], hi[p2]);
+      }
+      X.Vh[wave][s][ln] = Vh[s];
+      X.Vl[wave][s][ln] = __builtin_bit_cast(h16x8_t, lo);
     }
     gdn::lds_barrier();
   }
@@ -1748,10 +1865,8 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   }
   if (!(phase & kPhaseState)) return GDN_OK;
   const uint8_t* fresh = cv ? cv->fresh : nullptr;
-  const int per_item = Hv * (D / kCB);
   auto state_launch = [&](const SegList& sl, int64_t items) {
-    const int64_t cwork = items * per_item;
-    const int64_t cgrid = gdn::kNumXcd * ((cwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
+    const int64_t cgrid = gdn::kNumXcd * ((items * Hv + gdn::kNumXcd - 1) / gdn::kNumXcd) * (D / kCB);
     if (cv)
       chunk_state_kernel<D, true><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
           v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);

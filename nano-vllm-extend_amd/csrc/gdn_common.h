@@ -128,6 +128,23 @@ __device__ __forceinline__ f32x4_t mfma16x16x4f32(float a, float b, const f32x4_
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// One element of the gated RMSNorm after the row's r = rsqrt(mean(x^2) + eps)
+// (nanovllm/models/qwen3_5.py:121-131, eager rounding order):
+//   n = bf16(x r), wn = bf16(w n), y = wn * silu(z)   (the caller rounds y)
+// silu(z) = z / (1 + e^-z): e^-z within a few ulp (exp_acc) and the divide as
+// a hardware reciprocal refined by one Newton step (within an ulp of the
+// divide); the exponent is capped at 88 so the step never sees an infinite
+// operand.  Every gated-norm output goes through this function, so the
+// standalone and the fused norms agree bit for bit.
+__device__ __forceinline__ float norm_gate(float x, float r, float w, float z) {
+  const float n = bf2f(f2bf(x * r));
+  const float wn = bf2f(f2bf(w * n));
+  const float d = 1.0f + exp_acc(fminf(-z, 88.0f));
+  float rc = __builtin_amdgcn_rcpf(d);
+  rc = fmaf(rc, fmaf(-d, rc, 1.0f), rc);
+  return wn * (z * rc);
+}
+
 // ---- wave-level reductions (wave64) ----
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

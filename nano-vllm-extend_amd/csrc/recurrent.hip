@@ -41,6 +41,25 @@ struct DecodeIn {
   int param_f32;
 };
 
+// Gated RMSNorm on the output (fused decode step, whole heads per workgroup):
+// o receives bf16(norm_gate(bf16(core), r, w, z)) instead of the core output,
+// the same bits as gdn_rmsnorm_gated on it.
+struct NormIn {
+  const uint16_t* z;  // [B, Hv*D] gate rows, row stride sz (NULL: no norm)
+  int64_t sz;
+  const uint16_t* w;  // [D]
+  float eps;
+};
+
+// Initial states of a speculative-verify step taken from the previous step's
+// per-token states (deferred commit): row b starts from src[b, acc[b] - 1]
+// (src [B, T_src, Hv, D, D]) when acc[b] >= 1, else from its pool row.
+struct SrcIn {
+  const float* src;
+  const int64_t* acc;  // NULL: every row from the pool
+  int T_src;
+};
+
 template <int D, int NVB, bool kFused>
 __global__ __launch_bounds__(256) void recurrent_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, const uint16_t* __restrict__ k,
@@ -48,7 +67,7 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
     const float* __restrict__ g, const uint16_t* __restrict__ beta, const float* s_in,
     int64_t s_in_stride, float* s_out, int64_t s_out_stride, const int64_t* __restrict__ ids,
     float* __restrict__ inter, uint16_t* __restrict__ o, int B, int T, int Hk, int Hv,
-    float scale, int l2norm, DecodeIn din) {
+    float scale, int l2norm, DecodeIn din, NormIn nin, SrcIn src) {
   constexpr int VB = D / NVB;     // state columns per workgroup
   constexpr int CPR = VB / 4;     // float4 column groups per row
   constexpr int RPP = 256 / CPR;  // rows per pass of the workgroup
@@ -74,7 +93,9 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
   const int col = vb * VB + c4 * 4;
 
   const int64_t row = ids ? ids[b] : b;
-  const float* sin = s_in + row * s_in_stride + static_cast<int64_t>(h) * D * D + col;
+  const int64_t acc = src.acc ? src.acc[b] : 0;
+  const float* sin = acc >= 1 ? src.src + ((static_cast<int64_t>(b) * src.T_src + acc - 1) * Hv + h) * D * D + col
+                              : s_in + row * s_in_stride + static_cast<int64_t>(h) * D * D + col;
   float4 S[NP];
 #pragma unroll
   for (int j = 0; j < NP; ++j)
@@ -220,6 +241,35 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
       uint16_t* us = reinterpret_cast<uint16_t*>(&u);
 #pragma unroll
       for (int i = 0; i < 4; ++i) us[i] = gdn::f2bf(out[i]);
+      if (NVB == 1 && nin.z) {
+        // the row's D outputs sit in lanes 0 .. D/4 - 1 of wave 0, 4 each.
+        // mean(x^2) is summed in the standalone norm's order: 8 consecutive
+        // values per group (this lane's and its pair's, lower columns
+        // first), then a butterfly over the D/8 groups.
+        float x[4], pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = gdn::bf2f(us[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[i] = __shfl_xor(x[i], 1, 64);
+        const bool lo = (c4 & 1) == 0;
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss += (lo ? x[i] : pr[i]) * (lo ? x[i] : pr[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss += (lo ? pr[i] : x[i]) * (lo ? pr[i] : x[i]);
+#pragma unroll
+        for (int m = D / 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, 2 * m, 64);
+        const float r = rsqrtf(ss / static_cast<float>(D) + nin.eps);
+        const uint2 zu = *reinterpret_cast<const uint2*>(nin.z + static_cast<int64_t>(b) * nin.sz +
+                                                         static_cast<int64_t>(h) * D + col);
+        const uint2 wu = *reinterpret_cast<const uint2*>(nin.w + col);
+        const uint16_t* zs = reinterpret_cast<const uint16_t*>(&zu);
+        const uint16_t* ws = reinterpret_cast<const uint16_t*>(&wu);
+        u.x = gdn::f2bf2(gdn::norm_gate(x[0], r, gdn::bf2f(ws[0]), gdn::bf2f(zs[0])),
+                         gdn::norm_gate(x[1], r, gdn::bf2f(ws[1]), gdn::bf2f(zs[1])));
+        u.y = gdn::f2bf2(gdn::norm_gate(x[2], r, gdn::bf2f(ws[2]), gdn::bf2f(zs[2])),
+                         gdn::norm_gate(x[3], r, gdn::bf2f(ws[3]), gdn::bf2f(zs[3])));
+      }
       *reinterpret_cast<uint2*>(o + gi * D + col) = u;
     }
   }
@@ -253,17 +303,18 @@ int launch_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16
                      int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t, const float* g,
                      const uint16_t* beta, const float* s_in, int64_t s_in_stride, float* s_out,
                      int64_t s_out_stride, const int64_t* ids, float* inter, uint16_t* o, int B,
-                     int T, int Hk, int Hv, float scale, int l2norm, const DecodeIn& din, hipStream_t stream) {
+                     int T, int Hk, int Hv, float scale, int l2norm, const DecodeIn& din, const NormIn& nin,
+                     const SrcIn& src, hipStream_t stream) {
   const int64_t work = static_cast<int64_t>(B) * Hv * NVB;
   const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
   if (din.xv)
     recurrent_kernel<D, NVB, true><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
         q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
-        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din);
+        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
   else
     recurrent_kernel<D, NVB, false><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
         q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
-        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din);
+        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
   return gdn_launch_status();
 }
 
@@ -282,12 +333,20 @@ extern "C" int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, cons
                              const float* s_in, int64_t s_in_stride, float* s_out,
                              int64_t s_out_stride, const int64_t* ids, float* inter, uint16_t* o,
                              int B, int T, int Hk, int Hv, int D, float scale, int l2norm,
-                             void* stream) {
+                             const float* src_states, const int64_t* src_accepted, int src_T, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
   if (B < 0 || T < 1 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
   if (B == 0) return GDN_OK;
   if (!q || !k || !v || !g || !beta || !s_in || !o) return GDN_ERR_INVALID_ARG;
+  if ((src_accepted != nullptr) != (src_states != nullptr) ||
+      (src_states && (reinterpret_cast<uintptr_t>(src_states) % 16 || src_T < 1)))
+    return GDN_ERR_INVALID_ARG;
   // float4 state access and 8-byte v access
+  // a slot holds all Hv states (D x D, dense); a shorter slot stride would
+  // make neighbouring slots overlap
+  const int64_t slot_elems = static_cast<int64_t>(Hv) * D * D;
+  const bool rows_distinct = ids || B > 1;
+  if (rows_distinct && (s_in_stride < slot_elems || (s_out && s_out_stride < slot_elems))) return GDN_ERR_INVALID_ARG;
   if (s_in_stride % 4 || (s_out && s_out_stride % 4) || sv_b % 4 || sv_t % 4 ||
       reinterpret_cast<uintptr_t>(s_in) % 16 || (s_out && reinterpret_cast<uintptr_t>(s_out) % 16) ||
       (inter && reinterpret_cast<uintptr_t>(inter) % 16) || reinterpret_cast<uintptr_t>(v) % 8 ||
@@ -296,8 +355,10 @@ extern "C" int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, cons
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nvb = recurrent_nvb(B, Hv);
   const DecodeIn din{};
+  const NormIn nin{};
+  const SrcIn src{src_states, src_accepted, src_T};
 #define GDN_REC_ARGS q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, \
-                     s_out_stride, ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, s
+                     s_out_stride, ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src, s
   if (D == 128) {
     if (nvb == 1) return launch_recurrent<128, 1>(GDN_REC_ARGS);
     if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);
@@ -313,7 +374,8 @@ extern "C" int gdn_state_commit(float* pool, int64_t slot_stride, const int64_t*
                                 const float* inter, const int32_t* accepted, int B, int T, int Hv,
                                 int D, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
-  if (B < 0 || T < 1 || Hv <= 0 || slot_stride % 4) return GDN_ERR_INVALID_ARG;
+  if (B < 0 || T < 1 || Hv <= 0 || slot_stride % 4 || slot_stride < static_cast<int64_t>(Hv) * D * D)
+    return GDN_ERR_INVALID_ARG;
   if (B == 0) return GDN_OK;
   if (!pool || !ids || !inter || !accepted) return GDN_ERR_INVALID_ARG;
   state_commit_kernel<<<dim3(static_cast<unsigned>(B * Hv)), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
@@ -327,7 +389,8 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
                                           const uint16_t* a, const uint16_t* b, const void* A_log,
                                           const void* dt_bias, int param_is_fp32, float* s_pool,
                                           int64_t s_stride, const int64_t* ids, uint16_t* o, int B, int Hk,
-                                          int Hv, int D, float scale, int l2norm, void* stream) {
+                                          int Hv, int D, float scale, int l2norm, const uint16_t* z, int64_t sz_b,
+                                          const uint16_t* norm_w, float eps, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
   if (B < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
   if (B == 0) return GDN_OK;
@@ -340,12 +403,19 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
       reinterpret_cast<uintptr_t>(x) % 8 || reinterpret_cast<uintptr_t>(conv_w) % 16 ||
       reinterpret_cast<uintptr_t>(o) % 8 || cp_ch < 3 || cp_slot < (vbase + static_cast<int64_t>(Hv) * D) * cp_ch)
     return GDN_ERR_INVALID_ARG;
+  // the fused norm reads 8-byte pieces of z and of its weight
+  if (z && (!norm_w || sz_b % 4 || sz_b < static_cast<int64_t>(Hv) * D || reinterpret_cast<uintptr_t>(z) % 8 ||
+            reinterpret_cast<uintptr_t>(norm_w) % 8))
+    return GDN_ERR_INVALID_ARG;
   const DecodeIn din{x + vbase, sx_row, conv_pool + vbase * cp_ch, cp_slot, cp_ch, conv_w + vbase * 4, a, b,
                      A_log, dt_bias, param_is_fp32 ? 1 : 0};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int nvb = recurrent_nvb(B, Hv);
+  // the norm needs a head's D outputs in one workgroup
+  const int nvb = z ? 1 : recurrent_nvb(B, Hv);
+  const NormIn nin{z, sz_b, norm_w, eps};
+  const SrcIn src{};
 #define GDN_REC_ARGS q, sq_b, 0, k, sk_b, 0, nullptr, 0, 0, nullptr, nullptr, s_pool, s_stride, s_pool, s_stride, \
-                     ids, nullptr, o, B, 1, Hk, Hv, scale, l2norm, din, s
+                     ids, nullptr, o, B, 1, Hk, Hv, scale, l2norm, din, nin, src, s
   if (D == 128) {
     if (nvb == 1) return launch_recurrent<128, 1>(GDN_REC_ARGS);
     if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);

@@ -57,23 +57,12 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const uint16_t* __re
   for (int m = kLanes / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
   const float r = rsqrtf(ss / static_cast<float>(D) + eps);
 
-  // silu(z) = z / (1 + e^-z): e^-z within a few ulp (exp_acc) and the divide
-  // as a hardware reciprocal refined by one Newton step (within an ulp of the
-  // divide); the exponent is capped at 88 so the step never sees an infinite
-  // operand.  (The conv's exp2 + reciprocal form is 10 % faster here but moves
+  // (the conv's exp2 + reciprocal form of silu is 10 % faster here but moves
   // about 3 in 10^4 outputs by one bf16 ulp: on outputs above 8 that is more
-  // than the 2e-2 max-abs bar.)
+  // than the 2e-2 max-abs bar)
   float yv[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float n = gdn::bf2f(gdn::f2bf(xf[i] * r));
-    const float wn = gdn::bf2f(gdn::f2bf(gdn::bf2f(ws[i]) * n));
-    const float zf = gdn::bf2f(zs[i]);
-    const float d = 1.0f + gdn::exp_acc(fminf(-zf, 88.0f));
-    float rc = __builtin_amdgcn_rcpf(d);
-    rc = fmaf(rc, fmaf(-d, rc, 1.0f), rc);
-    yv[i] = wn * (zf * rc);
-  }
+  for (int i = 0; i < 8; ++i) yv[i] = gdn::norm_gate(xf[i], r, gdn::bf2f(ws[i]), gdn::bf2f(zs[i]));
   uint4 out;
   out.x = gdn::f2bf2(yv[0], yv[1]);
   out.y = gdn::f2bf2(yv[2], yv[3]);

@@ -12,8 +12,12 @@ reads them at import; "1" = HIP kernel):
   NANOVLLM_CONV_TRITON  conv kernels         | "0": F.conv1d chain (:1020-1024, :1057-1065)
   NANOVLLM_GDN_INPLACE  in-place decode      | "0": gather -> recurrent kernel -> scatter (:1028-1030)
   NANOVLLM_GDN_VARLEN   varlen prefill       | "0": padded prefill path (:1032-1077)
-  FLA_CHUNK, FLA_RECURRENT                   | "0" selected the reference's pure-torch ports,
-                                               which this build does not ship: raises.
+  FLA_CHUNK, FLA_RECURRENT                   | "0" selects the reference's own pure-torch ports
+                                               (qwen3_5.py:152-227, :616-651).  This core is
+                                               the package's own and carries no copy of them,
+                                               so here "0" raises; installed into the reference
+                                               module (integration.install) the switches keep
+                                               their meaning and run the module's ports.
 The varlen prefill reads and writes the state pools at the slot ids
 directly (no gather / scatter copies).
 """
@@ -69,6 +73,8 @@ class Switches:
 _CHUNK_US = 1.9
 _NORM_US_PER_TOKEN_HEAD = 768 / 5.4e6
 
+# the last plan only (its pinned host tensors are reused while the batch
+# composition repeats, as by the layers of one step; nothing accumulates)
 _SPLIT_CACHE: dict = {}
 
 
@@ -79,6 +85,7 @@ def late_split(lens_q: list[int], Hv: int):
     key = (tuple(lens_q), Hv)
     if key in _SPLIT_CACHE:
         return _SPLIT_CACHE[key]
+    _SPLIT_CACHE.clear()
     n = len(lens_q)
     res = None
     if 2 <= n <= 64 and sum(lens_q) >= 4096:
@@ -188,14 +195,14 @@ class GatedDeltaNetCore:
         Hk, Hv, D = self.Hk, self.Hv, self.D
         kd = self.key_dim
         if self.sw.fused_decode and self.sw.gbeta and self.sw.conv_kernel and self.sw.inplace and self.K == 4:
-            # q/k conv, then gates + v conv + recurrent update in one kernel
-            # (the same results as the calls below)
+            # q/k conv, then gates + v conv + recurrent update + gated norm in
+            # one kernel (the same results as the calls below)
             with self._timed("conv_decode"):
                 qk = ops.conv_decode_step(mixed[:, :2 * kd], conv_cache[:, :2 * kd], ids, self.conv_w[:2 * kd])
             with self._timed("recurrent_decode"):
                 out = ops.recurrent_decode_fused(qk, mixed, conv_cache, self.conv_w, b, a, self.A_log, self.dt_bias,
-                                                 s_cache, ids, Hk, Hv, D)
-            return self._norm(out.view(B, Hv, D), z.view(B, Hv, D))
+                                                 s_cache, ids, Hk, Hv, D, z=z, norm_weight=self.norm_w, eps=self.eps)
+            return out.view(B, Hv, D)
         g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
         if self.sw.conv_kernel:
             with self._timed("conv_decode"):

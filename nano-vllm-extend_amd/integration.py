@@ -12,13 +12,18 @@ layer code:
   causal_conv_silu             -> ops.causal_conv_silu
   recurrent_gdn_inplace        -> ops.recurrent_gdn_inplace
   _fla_chunk / _fla_recurrent  -> ops.chunk_gated_delta_rule / ops.recurrent_gated_delta_rule
-  chunk_gated_delta_rule       -> ops.chunk_gated_delta_rule_ref_api
-  recurrent_gated_delta_rule   -> fla-style gathered recurrent on HIP
   _rms_gated_forward           -> ops.rms_norm_gated
 
-and sets the feature flags the layer reads (_HAS_FLA, _USE_FLA_CHUNK,
+and sets the feature flags the layer reads (_USE_FLA_CHUNK,
 _USE_FLA_RECURRENT, _USE_GDN_VARLEN) from the same environment switches
-(FLA_CHUNK, FLA_RECURRENT, NANOVLLM_GDN_VARLEN) the reference reads.
+(FLA_CHUNK, FLA_RECURRENT, NANOVLLM_GDN_VARLEN) the reference reads
+(qwen3_5.py:74-75, :478-479).  The module's own dispatchers
+chunk_gated_delta_rule / recurrent_gated_delta_rule (qwen3_5.py:140-149,
+:230-238) stay bound: with a switch at "1" they call the rebound _fla_*
+entry point (the HIP kernels), with FLA_CHUNK=0 / FLA_RECURRENT=0 they run
+the module's own pure-torch ports, exactly as in the reference.  _HAS_FLA is
+set only when one of the two switches is on (this package then provides the
+fla entry points); with both off it keeps the module's value.
 
 With NANOVLLM_GDN_FUSED_PREFILL=1 (the default; it also needs the gate and
 conv kernels on and a conv width of 4) it further replaces the method
@@ -30,9 +35,9 @@ method makes, bit for bit), on the layer's own pools and slot ids.
 With NANOVLLM_GDN_FUSED_DECODE=1 (the default; it also needs the gate, conv
 and in-place kernels on) it replaces Qwen3_5GatedDeltaNet._gdn_padded
 (qwen3_5.py:967-1085) with one whose T == 1 branch runs the q/k decode conv
-and then ops.recurrent_decode_fused (gates, the v channels' conv and the
-in-place recurrent update in one kernel; the same results bit for bit); other
-T keep the original method.
+and then ops.recurrent_decode_fused (gates, the v channels' conv, the
+in-place recurrent update and the gated norm self.norm in one kernel; the
+same results bit for bit); other T keep the original method.
 """
 from __future__ import annotations
 
@@ -42,14 +47,9 @@ from . import ops
 
 PATCHED_NAMES = (
     "fused_g_beta", "causal_conv_silu_varlen", "conv_decode_step", "causal_conv_silu",
-    "recurrent_gdn_inplace", "_fla_chunk", "_fla_recurrent", "chunk_gated_delta_rule",
-    "recurrent_gated_delta_rule", "_rms_gated_forward",
+    "recurrent_gdn_inplace", "_fla_chunk", "_fla_recurrent", "_rms_gated_forward",
 )
-
-
-def _recurrent_ref_api(query, key, value, g, beta, initial_state=None):
-    return ops.recurrent_gated_delta_rule(query, key, value, g=g, beta=beta, initial_state=initial_state,
-                                          output_final_state=True, use_qk_l2norm_in_kernel=True)
+FLAG_NAMES = ("_HAS_FLA", "_USE_FLA_CHUNK", "_USE_FLA_RECURRENT", "_USE_GDN_VARLEN")
 
 
 def _fused_prefill_method(mod, orig):
@@ -94,9 +94,11 @@ def _fused_decode_method(orig):
         w = self.conv1d.weight.view(self.conv_dim, 4)
         kd = self.key_dim
         qk = ops.conv_decode_step(proj[:, :2 * kd], self.conv_cache[:, :2 * kd], ids, w[:2 * kd])
-        out = ops.recurrent_decode_fused(qk, proj, self.conv_cache, w, b, a, A_log, dt_bias, self.s_cache, ids,
-                                         self.num_k_heads, Hv, self.head_k_dim)
-        core = self.norm(out.reshape(n, 1, Hv, Dv), z.view(n, 1, Hv, Dv))
+        # gates + v conv + in-place update + the gated norm (self.norm's
+        # weight and eps) in one kernel
+        core = ops.recurrent_decode_fused(qk, proj, self.conv_cache, w, b, a, A_log, dt_bias, self.s_cache, ids,
+                                          self.num_k_heads, Hv, self.head_k_dim, z=z.reshape(n, Hv * Dv),
+                                          norm_weight=self.norm.weight, eps=self.norm.eps)
         return self.out_proj(core.reshape(n, 1, self.value_dim))
 
     return _gdn_padded
@@ -117,9 +119,7 @@ def _fused_prefill_enabled() -> bool:
 def install(mod) -> dict:
     """Rebind the GDN kernel entry points of a loaded qwen3_5 module.
     Returns the previous bindings (for uninstall)."""
-    prev = {name: getattr(mod, name, None) for name in PATCHED_NAMES}
-    prev.update({f: getattr(mod, f, None) for f in ("_HAS_FLA", "_USE_FLA_CHUNK", "_USE_FLA_RECURRENT",
-                                                     "_USE_GDN_VARLEN")})
+    prev = {name: getattr(mod, name, None) for name in PATCHED_NAMES + FLAG_NAMES}
     mod.fused_g_beta = ops.fused_g_beta
     mod.causal_conv_silu_varlen = ops.causal_conv_silu_varlen
     mod.conv_decode_step = ops.conv_decode_step
@@ -127,13 +127,14 @@ def install(mod) -> dict:
     mod.recurrent_gdn_inplace = ops.recurrent_gdn_inplace
     mod._fla_chunk = ops.chunk_gated_delta_rule
     mod._fla_recurrent = ops.recurrent_gated_delta_rule
-    mod.chunk_gated_delta_rule = ops.chunk_gated_delta_rule_ref_api
-    mod.recurrent_gated_delta_rule = _recurrent_ref_api
     mod._rms_gated_forward = ops.rms_norm_gated
-    mod._HAS_FLA = True
-    mod._USE_FLA_CHUNK = os.environ.get("FLA_CHUNK", "1") == "1"
-    mod._USE_FLA_RECURRENT = os.environ.get("FLA_RECURRENT", "1") == "1"
-    mod._USE_GDN_VARLEN = mod._USE_FLA_CHUNK and os.environ.get("NANOVLLM_GDN_VARLEN", "1") == "1"
+    use_chunk = os.environ.get("FLA_CHUNK", "1") == "1"
+    use_rec = os.environ.get("FLA_RECURRENT", "1") == "1"
+    if use_chunk or use_rec:
+        mod._HAS_FLA = True
+    mod._USE_FLA_CHUNK = use_chunk
+    mod._USE_FLA_RECURRENT = use_rec
+    mod._USE_GDN_VARLEN = use_chunk and os.environ.get("NANOVLLM_GDN_VARLEN", "1") == "1"
     cls = getattr(mod, "Qwen3_5GatedDeltaNet", None)
     if cls is not None and _fused_prefill_enabled() and hasattr(cls, "_gdn_prefill_varlen"):
         prev["Qwen3_5GatedDeltaNet._gdn_prefill_varlen"] = cls.__dict__.get("_gdn_prefill_varlen")

@@ -136,6 +136,7 @@ def conv_decode_step(x: torch.Tensor, state_pool: torch.Tensor, ids: torch.Tenso
     w = weight.reshape(C, K).contiguous()
     assert x.stride(1) == 1 and state_pool.stride(2) == 1
     ids64 = ids.to(torch.int64).contiguous()
+    assert ids64.shape == (n,), "one slot id per row"
     y = torch.empty(n, C, dtype=x.dtype, device=x.device)
     _lib.call("gdn_conv_decode", _lib.ptr(x), x.stride(0), _lib.ptr(state_pool), state_pool.stride(0),
               state_pool.stride(1), _lib.ptr(ids64), _lib.ptr(w), _lib.ptr(y), y.stride(0), n, C, K,
@@ -416,8 +417,8 @@ def chunk_gated_delta_rule_ref_api(query, key, value, g, beta, chunk_size=64, in
 
 
 # ---------------------------------------------------------- recurrent rule --
-def _recurrent(q, k, v, g, beta, s_in, s_out, ids, inter, scale, l2norm):
-    dev = _check_cuda(q, k, v, g, beta, s_in, s_out, ids, inter)
+def _recurrent(q, k, v, g, beta, s_in, s_out, ids, inter, scale, l2norm, src_states=None, src_accepted=None):
+    dev = _check_cuda(q, k, v, g, beta, s_in, s_out, ids, inter, src_states, src_accepted)
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
         _bf16(t, nm)
     Bsz, T, Hk, D = k.shape
@@ -438,6 +439,13 @@ def _recurrent(q, k, v, g, beta, s_in, s_out, ids, inter, scale, l2norm):
     if inter is not None:
         assert inter.is_contiguous() and inter.dtype == torch.float32
         assert inter.shape == (Bsz, T, Hv, D, D)
+    src_acc, src_T = None, 1
+    if src_accepted is not None:
+        assert src_states is not None and src_states.is_contiguous() and src_states.dtype == torch.float32
+        assert src_states.dim() == 5 and src_states.shape[0] == Bsz and src_states.shape[2:] == (Hv, D, D)
+        src_T = src_states.shape[1]
+        src_acc = src_accepted if src_accepted.dtype == torch.int64 else src_accepted.to(torch.int64)
+        assert src_acc.shape == (Bsz,) and src_acc.is_contiguous()
     out = torch.empty(Bsz, T, Hv, D, dtype=v.dtype, device=v.device)
     if scale is None:
         scale = D ** -0.5
@@ -445,7 +453,8 @@ def _recurrent(q, k, v, g, beta, s_in, s_out, ids, inter, scale, l2norm):
               k.stride(1), _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(g), _lib.ptr(beta),
               _lib.ptr(s_in), s_in.stride(0), _lib.ptr(s_out), s_out.stride(0) if s_out is not None else 0,
               _lib.ptr(ids64), _lib.ptr(inter), _lib.ptr(out), Bsz, T, Hk, Hv, D, float(scale),
-              int(bool(l2norm)), _stream(dev))
+              int(bool(l2norm)), _lib.ptr(src_states if src_acc is not None else None), _lib.ptr(src_acc),
+              src_T, _stream(dev))
     return out
 
 
@@ -462,8 +471,15 @@ def recurrent_gdn_inplace(q, k, v, g, beta, s_pool, ids):
     return _recurrent(q, k, v, g, beta, s_pool, s_pool, ids, None, None, True)
 
 
+# The decode kernel splits each head's columns over NVB workgroups when the
+# batch has few (sequence, head) tiles (NVB 1 from B * Hv >= 2048); the split
+# changes the summation order of S^T k, so whole-head and split runs differ
+# in the last bits.  Its fused norm epilogue needs whole heads.
+WHOLE_HEAD_TILES = 2048
+
+
 def recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bias, s_pool, ids, Hk, Hv, D,
-                           scale=None):
+                           scale=None, z=None, norm_weight=None, eps=1e-6, fuse_norm=None):
     """The decode step after the q/k conv, in one kernel: the gates from a, b,
     the v channels' conv1d + SiLU (their conv state rolled in place at `ids`)
     and the in-place recurrent update.  qk [B, 2*Hk*D] is conv_decode_step's
@@ -471,8 +487,14 @@ def recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bi
     [slots, C, 3] and s_pool [slots, Hv, D, D] per-layer pool views; b, a
     [B, Hv] bf16.  Returns out [B, 1, Hv, D] bf16, the same bits as
     fused_g_beta -> conv_decode_step -> recurrent_gdn_inplace
-    (nanovllm/models/qwen3_5.py:1008-1030)."""
-    dev = _check_cuda(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bias, s_pool, ids)
+    (nanovllm/models/qwen3_5.py:1008-1030).  With z ([B, Hv*D] bf16, head
+    dim contiguous) and norm_weight ([D]) `out` is the layer's gated RMSNorm
+    of it (qwen3_5.py:1083-1085), the same bits as rms_norm_gated on the core
+    output: in the same kernel when B * Hv >= WHOLE_HEAD_TILES (the kernel
+    runs whole heads then anyway), else as a second launch (fuse_norm=True
+    forces the one-kernel form, whose core output is then the whole-head
+    kernel's)."""
+    dev = _check_cuda(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bias, s_pool, ids, z, norm_weight)
     for t, nm in ((qk, "qk"), (mixed, "mixed"), (conv_pool, "conv_pool"), (b, "b"), (a, "a")):
         _bf16(t, nm)
     B, C = mixed.shape
@@ -489,6 +511,19 @@ def recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bi
     assert a_log.numel() == Hv and dt_bias.numel() == Hv
     assert _state_view_ok(s_pool, Hv, D)
     ids64 = ids.to(torch.int64).contiguous()
+    assert ids64.shape == (B,), "one slot id per row"
+    if z is not None and not (fuse_norm if fuse_norm is not None else B * Hv >= WHOLE_HEAD_TILES):
+        core = recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bias, s_pool, ids, Hk, Hv,
+                                      D, scale)
+        return rms_norm_gated(core, z.reshape(B, 1, Hv, D), norm_weight, eps)
+    nw = None
+    if z is not None:
+        _bf16(z, "z")
+        z = z.reshape(B, Hv * D)
+        if z.stride(1) != 1 or z.stride(0) % 4:
+            z = z.contiguous()
+        assert norm_weight is not None and norm_weight.numel() == D
+        nw = norm_weight.to(torch.bfloat16).contiguous()
     out = torch.empty(B, 1, Hv, D, dtype=mixed.dtype, device=mixed.device)
     if scale is None:
         scale = D ** -0.5
@@ -496,7 +531,8 @@ def recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bi
               _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_pool), conv_pool.stride(0), conv_pool.stride(1),
               _lib.ptr(w), _lib.ptr(a), _lib.ptr(b), _lib.ptr(a_log), _lib.ptr(dt_bias),
               int(a_log.dtype == torch.float32), _lib.ptr(s_pool), s_pool.stride(0), _lib.ptr(ids64),
-              _lib.ptr(out), B, Hk, Hv, D, float(scale), 1, _stream(dev))
+              _lib.ptr(out), B, Hk, Hv, D, float(scale), 1, _lib.ptr(z), z.stride(0) if z is not None else 0,
+              _lib.ptr(nw), float(eps), _stream(dev))
     return out
 
 
@@ -520,16 +556,75 @@ def recurrent_gated_delta_rule(query, key, value, g=None, beta=None, initial_sta
     return out, s_out
 
 
-def recurrent_gdn_multitoken(q, k, v, g, beta, s_pool, ids, intermediate_states=None):
+def recurrent_gdn_multitoken(q, k, v, g, beta, s_pool, ids, intermediate_states=None, src_states=None,
+                             src_accepted=None):
     """Speculative-verify decode: T draft tokens per sequence against the
     slot pool.  q/k [B, T, Hk, D], v [B, T, Hv, D], g/beta [B, T, Hv].
     With intermediate_states ([B, T, Hv, D, D] fp32) the per-token states
     are written there and the pool is left untouched (commit_states picks
     the accepted prefix); without it the pool is advanced by all T tokens.
+    src_states / src_accepted: row b starts from src_states[b,
+    src_accepted[b] - 1] where src_accepted[b] >= 1 instead of its pool row
+    (the previous verify's accepted state, not yet committed; see
+    SpecVerify).
     Returns out [B, T, Hv, D].  (No reference counterpart: spec decode is
     disabled for qwen3_5, nanovllm/config.py:84.)"""
     s_out = None if intermediate_states is not None else s_pool
-    return _recurrent(q, k, v, g, beta, s_pool, s_out, ids, intermediate_states, None, True)
+    return _recurrent(q, k, v, g, beta, s_pool, s_out, ids, intermediate_states, None, True, src_states,
+                      src_accepted)
+
+
+class SpecVerify:
+    """Speculative-verify steps of one GDN layer with the rollback folded
+    into the next step instead of a commit copy.
+
+    verify() runs the T-token kernel and keeps every per-token state in an
+    [B, T, Hv, D, D] buffer; accept(accepted) records how many of them each
+    row keeps (device int64 tensor, values 1..T: the first token of a draft
+    block is the target model's own and always kept).  The next verify()
+    starts row b from state [b, accepted[b] - 1] directly (the kernel reads it
+    where the pool row would be read, and each state is read before the step
+    overwrites it in place), so nothing runs between steps.  commit() writes
+    the accepted states into the pool, for any other user of the slots (a
+    plain decode, a prefill, or a sequence that leaves the batch).  The rows
+    keep their order across steps (ids the same); a different batch must
+    commit() first.  (No reference counterpart: spec decode is disabled for
+    qwen3_5, nanovllm/config.py:84.)"""
+
+    def __init__(self, s_pool: torch.Tensor):
+        self.s_pool = s_pool
+        self.inter = None
+        self.ids = None
+        self.accepted = None      # [B] int64 of the last verify, until the next verify or commit()
+
+    def verify(self, q, k, v, g, beta, ids):
+        Bsz, T = k.shape[:2]
+        Hv, D = v.shape[2], v.shape[3]
+        if self.accepted is not None:
+            assert self.ids is not None and torch.equal(self.ids, ids), "the batch changed: commit() first"
+        if self.inter is None or self.inter.shape != (Bsz, T, Hv, D, D):
+            assert self.accepted is None, "the draft length changed: commit() first"
+            self.inter = torch.empty(Bsz, T, Hv, D, D, dtype=torch.float32, device=v.device)
+        out = recurrent_gdn_multitoken(q, k, v, g, beta, self.s_pool, ids, self.inter,
+                                       self.inter if self.accepted is not None else None, self.accepted)
+        self.ids = ids
+        self.accepted = None      # the pool plus this step's states, until accept()
+        return out
+
+    def accept(self, accepted: torch.Tensor) -> None:
+        """accepted [B] int64 (device): tokens kept per row, 1..T."""
+        assert self.inter is not None and self.accepted is None, "accept() follows one verify()"
+        assert accepted.dtype == torch.int64 and accepted.shape == (self.inter.shape[0],)
+        assert accepted.device == self.inter.device and accepted.is_contiguous()
+        self.accepted = accepted
+
+    def commit(self) -> None:
+        """Write the accepted states into the pool rows (a no-op when
+        nothing is pending)."""
+        if self.accepted is None:
+            return
+        commit_states(self.s_pool, self.ids, self.inter, self.accepted)
+        self.accepted = None
 
 
 def commit_states(s_pool, ids, intermediate_states, accepted):
@@ -540,6 +635,7 @@ def commit_states(s_pool, ids, intermediate_states, accepted):
     assert _state_view_ok(s_pool, Hv, D) and intermediate_states.is_contiguous()
     ids64 = ids.to(torch.int64).contiguous()
     acc = accepted.to(torch.int32).contiguous()
+    assert ids64.shape == (Bsz,) and acc.shape == (Bsz,), "one slot id and one accepted length per row"
     _lib.call("gdn_state_commit", _lib.ptr(s_pool), s_pool.stride(0), _lib.ptr(ids64),
               _lib.ptr(intermediate_states), _lib.ptr(acc), Bsz, T, Hv, D, _stream(dev))
 

@@ -7,6 +7,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "gdn_mi355x.h"
@@ -56,6 +57,48 @@ def test_library_has_no_rpath_to_system_rocm(pkg):
     assert "libamdhip64.so" in out
 
 
+def test_ops_reject_short_id_lists(pkg, monkeypatch):
+    """The wrappers check the ids / accepted lengths against the batch before
+    the launch.  The device check and the launch are stubbed (CPU only): a
+    short list must fail the length check, a full one reach the launch."""
+    ops = pkg.ops
+
+    class Launched(Exception):
+        pass
+
+    def fake_call(*a, **k):
+        raise Launched()
+
+    monkeypatch.setattr(ops, "_check_cuda", lambda *ts: torch.device("cpu"))
+    monkeypatch.setattr(ops, "_stream", lambda dev: 0)
+    monkeypatch.setattr(ops._lib, "call", fake_call)
+    bf = torch.bfloat16
+    Hk = Hv = 2
+    D = 64
+    C = 2 * Hk * D + Hv * D
+    B = 4
+    x = torch.zeros(B, C, dtype=bf)
+    pool = torch.zeros(8, C, 3, dtype=bf)
+    w = torch.zeros(C, 4, dtype=bf)
+    for n_ids in (B - 1, B):
+        ids = torch.arange(n_ids)
+        exc = AssertionError if n_ids < B else Launched
+        with pytest.raises(exc):
+            ops.conv_decode_step(x, pool, ids, w)
+        s_pool = torch.zeros(8, Hv, D, D)
+        qk = torch.zeros(B, 2 * Hk * D, dtype=bf)
+        ab = torch.zeros(B, Hv, dtype=bf)
+        with pytest.raises(exc):
+            ops.recurrent_decode_fused(qk, x, pool, w, ab, ab, torch.zeros(Hv, dtype=bf), torch.zeros(Hv, dtype=bf),
+                                       s_pool, ids, Hk, Hv, D)
+        inter = torch.zeros(B, 2, Hv, D, D)
+        with pytest.raises(exc):
+            ops.commit_states(s_pool, ids, inter, torch.ones(n_ids, dtype=torch.int32))
+        if n_ids == B:
+            with pytest.raises(AssertionError):   # a short accepted list alone
+                ops.commit_states(s_pool, ids, inter, torch.ones(B - 1, dtype=torch.int32))
+
+
 def test_argument_validation_before_launch(pkg):
     """Rejected shapes return error codes without touching the device."""
     lib = pkg._lib.load()
@@ -64,7 +107,7 @@ def test_argument_validation_before_launch(pkg):
     assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, None, 0, 1, 64,
                                  1, 1, 96, 1.0, 1, None, None, 0, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_recurrent(None, 0, 0, None, 0, 0, None, 0, 0, None, None, None, 0, None, 0, None, None,
-                             None, 1, 1, 1, 1, 32, 1.0, 1, None) == _lib.GDN_ERR_UNSUPPORTED
+                             None, 1, 1, 1, 1, 32, 1.0, 1, None, None, 1, None) == _lib.GDN_ERR_UNSUPPORTED
     assert lib.gdn_rmsnorm_gated(None, 0, None, 0, None, None, 4, 1, 256, 1e-6, None) == _lib.GDN_ERR_UNSUPPORTED
     # head grouping must divide
     assert lib.gdn_chunk_prefill(None, 0, None, 0, None, 0, None, None, None, None, None, 0, None, None, 0, 1, 64,
@@ -81,13 +124,38 @@ def test_argument_validation_before_launch(pkg):
     # the fused decode step: unsupported head dim, NULL operands, grouped heads that do not divide
     fd = lib.gdn_recurrent_decode_fused
     assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
-              4, 2, 4, 96, 1.0, 1, None) == _lib.GDN_ERR_UNSUPPORTED
+              4, 2, 4, 96, 1.0, 1, None, 0, None, 1e-6, None) == _lib.GDN_ERR_UNSUPPORTED
     assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
-              4, 2, 4, 128, 1.0, 1, None) == _lib.GDN_ERR_INVALID_ARG
+              4, 2, 4, 128, 1.0, 1, None, 0, None, 1e-6, None) == _lib.GDN_ERR_INVALID_ARG
     assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
-              4, 3, 4, 128, 1.0, 1, None) == _lib.GDN_ERR_INVALID_ARG
+              4, 3, 4, 128, 1.0, 1, None, 0, None, 1e-6, None) == _lib.GDN_ERR_INVALID_ARG
     assert fd(None, 0, None, 0, None, 0, None, 0, 3, None, None, None, None, None, 0, None, 0, None, None,
-              0, 2, 4, 128, 1.0, 1, None) == _lib.GDN_OK
+              0, 2, 4, 128, 1.0, 1, None, 0, None, 1e-6, None) == _lib.GDN_OK
+    # slot strides shorter than a slot's states (rows of the pool would
+    # overlap) and short raw rows are rejected before any launch; the dummy
+    # pointers are aligned and never dereferenced
+    P = ctypes.c_void_p(1 << 20)
+    Hv, D = 4, 128
+    slot = Hv * D * D
+    rec = lambda s_in_stride, s_out_stride, src=None, idx=None: lib.gdn_recurrent(
+        P, 0, 0, P, 0, 0, P, 0, 0, P, P, P, s_in_stride, P, s_out_stride, P, None, P, 2, 1, 4, Hv, D, 1.0, 1,
+        src, idx, 4, None)
+    assert rec(slot - 4, slot) == _lib.GDN_ERR_INVALID_ARG
+    assert rec(slot, slot - 4) == _lib.GDN_ERR_INVALID_ARG
+    # the deferred-commit source: both pointers or neither
+    assert rec(slot, slot, src=P) == _lib.GDN_ERR_INVALID_ARG
+    assert rec(slot, slot, idx=P) == _lib.GDN_ERR_INVALID_ARG
+    commit = lambda stride: lib.gdn_state_commit(P, stride, P, P, P, 2, 4, Hv, D, None)
+    assert commit(slot - 4) == _lib.GDN_ERR_INVALID_ARG
+    C = 3 * Hv * D
+    fdec = lambda sx_row, s_stride, cp_slot, z=None, sz=0, nw=None: fd(
+        P, C, P, C, P, sx_row, P, cp_slot, 3, P, P, P, P, P, 0, P, s_stride, P, P, 2, Hv, Hv, D, 1.0, 1,
+        z, sz, nw, 1e-6, None)
+    assert fdec(C - 4, slot, 3 * C) == _lib.GDN_ERR_INVALID_ARG          # raw row shorter than C
+    assert fdec(C, slot - 4, 3 * C) == _lib.GDN_ERR_INVALID_ARG          # state slot stride
+    assert fdec(C, slot, 3 * C - 3) == _lib.GDN_ERR_INVALID_ARG          # conv slot stride
+    assert fdec(C, slot, 3 * C, z=P, sz=Hv * D) == _lib.GDN_ERR_INVALID_ARG       # fused norm without its weight
+    assert fdec(C, slot, 3 * C, z=P, sz=Hv * D - 4, nw=P) == _lib.GDN_ERR_INVALID_ARG  # gate rows too short
     # empty work is a no-op success
     assert lib.gdn_g_beta(None, None, None, None, 0, None, None, None, 0, 16, None) == _lib.GDN_OK
     with pytest.raises(_lib.GDNKernelError):

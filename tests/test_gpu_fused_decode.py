@@ -78,6 +78,63 @@ def test_fused_decode_against_oracle(pkg, dev):
     qk = pkg.ops.conv_decode_step(mixed[:, :2 * kd].to(dev), cp[:, :2 * kd], idd, conv_w[:2 * kd].to(dev))
     o = pkg.ops.recurrent_decode_fused(qk, mixed.to(dev), cp, conv_w.to(dev), b.to(dev), a.to(dev), A_log.to(dev),
                                        dt_bias.to(dev), sp, idd, Hk, Hv, D)
-    assert_out(o.cpu(), ro.to(BF16), "fused decode output", ulps=4)
+    assert_out(o.cpu(), ro.to(BF16), "fused decode output")
+    assert_state(sp.cpu()[ids], rs, "fused decode state")
+    assert torch.equal(cp.cpu().view(torch.int16), rpool.view(torch.int16)), "conv pool"
+
+
+@pytest.mark.parametrize("Hk,Hv,D,B,slots", CASES + [(16, 16, 128, 256, 300)], ids=lambda c: str(c))
+def test_fused_decode_norm_equals_separate_norm(pkg, dev, Hk, Hv, D, B, slots):
+    """With the gate rows and the norm weight the decode step also applies the
+    layer's gated RMSNorm (qwen3_5.py:1083-1085): bit-equal to
+    recurrent_decode_fused followed by rms_norm_gated, states and conv pool
+    as without the norm.  From B * Hv >= 2048 the norm runs in the decode
+    kernel itself (the last two cases), below it as a second launch."""
+    ops = pkg.ops
+    mixed, conv_w, A_log, dt_bias, a, b, conv_pool, s_pool, ids = (
+        t.to(dev) for t in _case(63, Hk, Hv, D, B, slots, False))
+    gen = torch.Generator().manual_seed(64)
+    z = torch.randn(B, Hv * D, generator=gen).to(BF16)
+    z[0, :D] *= 40.0                                   # gates far out on the silu tails
+    z = z.to(dev)
+    w = (1 + 0.02 * torch.randn(D, generator=gen)).to(BF16).to(dev)
+    mixed[1, 2 * Hk * D:] *= 1e-4                      # a row with a tiny mean square
+    kd = Hk * D
+    cp1, sp1 = conv_pool.clone(), s_pool.clone()
+    qk = ops.conv_decode_step(mixed[:, :2 * kd], cp1[:, :2 * kd], ids, conv_w[:2 * kd])
+    o1 = ops.recurrent_decode_fused(qk, mixed, cp1, conv_w, b, a, A_log, dt_bias, sp1, ids, Hk, Hv, D)
+    y1 = ops.rms_norm_gated(o1.view(B, Hv, D), z.view(B, Hv, D), w, 1e-6)
+    cp2, sp2 = conv_pool.clone(), s_pool.clone()
+    qk2 = ops.conv_decode_step(mixed[:, :2 * kd], cp2[:, :2 * kd], ids, conv_w[:2 * kd])
+    y2 = ops.recurrent_decode_fused(qk2, mixed, cp2, conv_w, b, a, A_log, dt_bias, sp2, ids, Hk, Hv, D,
+                                    z=z, norm_weight=w, eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(y2.view(B, Hv, D).view(torch.int16), y1.view(torch.int16)), "fused norm differs"
+    assert torch.equal(sp2, sp1), "state pool differs"
+    assert torch.equal(cp2.view(torch.int16), cp1.view(torch.int16)), "conv pool differs"
+
+
+def test_fused_decode_norm_epilogue_small_batch_vs_oracle(pkg, dev):
+    """The in-kernel norm forced at a small batch (whole heads per workgroup
+    where the plain kernel would split them): against the oracle's decode
+    chain and gated norm."""
+    Hk, Hv, D, B, slots = 2, 4, 128, 5, 8
+    mixed, conv_w, A_log, dt_bias, a, b, conv_pool, s_pool, ids = _case(65, Hk, Hv, D, B, slots, False)
+    gen = torch.Generator().manual_seed(66)
+    z = torch.randn(B, Hv * D, generator=gen).to(BF16)
+    w = (1 + 0.02 * torch.randn(D, generator=gen)).to(BF16)
+    kd = Hk * D
+    g, beta = gdn_ref.g_beta(b, a, A_log, dt_bias, None)
+    ry, rpool = gdn_ref.conv_decode(mixed, conv_pool.clone(), ids.tolist(), conv_w)
+    q, k, v = ry[:, :kd].reshape(B, 1, Hk, D), ry[:, kd:2 * kd].reshape(B, 1, Hk, D), ry[:, 2 * kd:].reshape(B, 1, Hv, D)
+    ro, rs, _ = gdn_ref.recurrent_rule(q, k, v, g.view(B, 1, Hv), beta.float().view(B, 1, Hv), s_pool[ids])
+    ref = gdn_ref.rms_norm_gated(ro.to(BF16).view(B, Hv, D), z.view(B, Hv, D), w)
+    cp, sp = conv_pool.to(dev), s_pool.to(dev)
+    idd = ids.to(dev)
+    qk = pkg.ops.conv_decode_step(mixed[:, :2 * kd].to(dev), cp[:, :2 * kd], idd, conv_w[:2 * kd].to(dev))
+    y = pkg.ops.recurrent_decode_fused(qk, mixed.to(dev), cp, conv_w.to(dev), b.to(dev), a.to(dev), A_log.to(dev),
+                                       dt_bias.to(dev), sp, idd, Hk, Hv, D, z=z.to(dev), norm_weight=w.to(dev),
+                                       fuse_norm=True)
+    assert_out(y.cpu().view(B, Hv, D), ref, "in-kernel norm output", ulps=4)
     assert_state(sp.cpu()[ids], rs, "fused decode state")
     assert torch.equal(cp.cpu().view(torch.int16), rpool.view(torch.int16)), "conv pool"

@@ -96,7 +96,7 @@ def test_fused_against_oracle(pkg, dev):
     cp, sp = conv_pool.to(dev), s_pool.to(dev)
     o = pkg.ops.conv_chunk_prefill_varlen(mixed.to(dev), cp, conv_w.to(dev), b.to(dev), a.to(dev), A_log.to(dev),
                                           dt_bias.to(dev), _cu(lens, dev), sp, ids.to(dev), Hk, Hv, D)
-    assert_out(o.cpu(), ro.to(BF16), "fused prefill output", ulps=4)
+    assert_out(o.cpu(), ro.to(BF16), "fused prefill output")
     assert_state(sp.cpu()[ids], rs, "fused prefill state")
     assert torch.equal(cp.cpu()[ids].view(torch.int16), new_conv.view(torch.int16)), "conv pool"
 

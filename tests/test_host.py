@@ -72,6 +72,74 @@ def test_install_rebinds_reference_call_sites(pkg):
     assert mod._HAS_FLA is False
 
 
+_STUB_DISPATCH = """
+def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None):
+    if _USE_FLA_CHUNK:
+        return _fla_chunk(query, key, value, g=g, beta=beta, initial_state=initial_state,
+                          output_final_state=True, use_qk_l2norm_in_kernel=True)
+    return _torch_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size, initial_state)
+
+
+def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None):
+    if _USE_FLA_RECURRENT:
+        return _fla_recurrent(query, key, value, g=g, beta=beta, initial_state=initial_state,
+                              output_final_state=True, use_qk_l2norm_in_kernel=True)
+    return _torch_recurrent_gated_delta_rule(query, key, value, g, beta, initial_state)
+
+
+def _torch_chunk_gated_delta_rule(*args):
+    return "torch chunk port"
+
+
+def _torch_recurrent_gated_delta_rule(*args):
+    return "torch recurrent port"
+"""
+
+
+def _stub_module():
+    """A module with the reference's dispatch structure for the two fla
+    entry points (module globals read at call time, qwen3_5.py:140-149,
+    :230-238) and fla absent."""
+    mod = types.ModuleType("qwen3_5_stub")
+    mod._HAS_FLA = False
+    mod._fla_chunk = mod._fla_recurrent = None
+    mod._USE_FLA_CHUNK = mod._USE_FLA_RECURRENT = mod._USE_GDN_VARLEN = False
+    exec(_STUB_DISPATCH, mod.__dict__)
+    return mod
+
+
+@pytest.mark.parametrize("fla_chunk,fla_rec", [("1", "1"), ("0", "1"), ("1", "0"), ("0", "0")])
+def test_install_keeps_fla_switch_semantics(pkg, monkeypatch, fla_chunk, fla_rec):
+    """FLA_CHUNK / FLA_RECURRENT keep the reference's meaning after install:
+    "1" routes the module's dispatcher to the HIP entry point, "0" to the
+    module's own pure-torch port."""
+    monkeypatch.setenv("FLA_CHUNK", fla_chunk)
+    monkeypatch.setenv("FLA_RECURRENT", fla_rec)
+    mod = _stub_module()
+    disp_chunk, disp_rec = mod.chunk_gated_delta_rule, mod.recurrent_gated_delta_rule
+    prev = pkg.integration.install(mod)
+    # the dispatchers themselves are never rebound
+    assert mod.chunk_gated_delta_rule is disp_chunk and mod.recurrent_gated_delta_rule is disp_rec
+    assert mod._fla_chunk is pkg.ops.chunk_gated_delta_rule
+    assert mod._fla_recurrent is pkg.ops.recurrent_gated_delta_rule
+    assert mod._USE_GDN_VARLEN == (fla_chunk == "1")
+    assert mod._HAS_FLA == (fla_chunk == "1" or fla_rec == "1")
+    x = torch.zeros(1, 2, 2, 64, dtype=torch.bfloat16)
+    g = torch.zeros(1, 2, 2)
+    if fla_chunk == "1":
+        with pytest.raises(ValueError, match="GPU only"):   # the HIP op (CPU tensors are refused)
+            mod.chunk_gated_delta_rule(x, x, x, g, g.bfloat16())
+    else:
+        assert mod.chunk_gated_delta_rule(x, x, x, g, g.bfloat16()) == "torch chunk port"
+    if fla_rec == "1":
+        with pytest.raises(ValueError, match="GPU only"):
+            mod.recurrent_gated_delta_rule(x[:, :1], x[:, :1], x[:, :1], g[:, :1], g[:, :1].bfloat16())
+    else:
+        assert mod.recurrent_gated_delta_rule(x, x, x, g, g) == "torch recurrent port"
+    pkg.integration.uninstall(mod, prev)
+    assert mod._HAS_FLA is False and mod._fla_chunk is None and mod._USE_FLA_CHUNK is False
+
+
 def test_install_replaces_varlen_prefill_method(pkg, monkeypatch):
     mod = types.ModuleType("qwen3_5_stub")
 
