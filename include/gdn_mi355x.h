@@ -31,6 +31,11 @@ extern "C" {
 #define GDN_OK 0
 #define GDN_ERR_INVALID_ARG (-1) /* shape / stride / pointer rejected */
 #define GDN_ERR_UNSUPPORTED (-2) /* valid but not built (e.g. head dim) */
+#define GDN_ERR_SCRATCH (-3)     /* needs more than the fixed scratch of an allocation-free entry point */
+
+/* Bytes of the fixed device scratch array of gdn_conv_chunk_prefill_noalloc
+ * (one per GPU, held until the process ends). */
+#define GDN_NOALLOC_SCRATCH_BYTES (128LL << 20)
 
 /* ABI version of the loaded library (GDN_ABI_VERSION). */
 int gdn_abi_version(void);
@@ -191,6 +196,28 @@ int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_sta
 /* Workspace bytes of gdn_conv_chunk_prefill; -1 on bad args. */
 int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
 
+/*
+ * gdn_conv_chunk_prefill with no workspace argument and no allocation: its
+ * records and segment scratch live in a fixed file-scope device array of
+ * GDN_NOALLOC_SCRATCH_BYTES per GPU.  No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Arguments
+ * as gdn_conv_chunk_prefill with phase = 3 (prep and state pass together) and
+ * no select_host; it calls no hipMalloc / hipFree.  A call whose workspace
+ * (gdn_conv_chunk_prefill_workspace_size) exceeds the array returns
+ * GDN_ERR_SCRATCH: 128 MiB holds ~2,200 chunk-heads of records at D = 128,
+ * e.g. ~8,000 tokens at 16 value heads (less for calls of under 4 sequences,
+ * which also reserve the segment scratch).  All calls on one GPU share the
+ * array: calls that overlap on one GPU race; calls in order on a stream are
+ * safe.  Results are the same bits as gdn_conv_chunk_prefill's.
+ */
+int gdn_conv_chunk_prefill_noalloc(const uint16_t* x, int64_t sx_row, uint16_t* conv_state, int64_t ss_seq,
+                                   int64_t ss_ch, const uint16_t* conv_w, const uint16_t* b, const uint16_t* a,
+                                   const void* A_log, const void* dt_bias, int param_is_fp32, const float* h0,
+                                   float* hT, const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
+                                   const int64_t* cu_seqlens, const int64_t* cu_seqlens_host, int max_segments,
+                                   int n_seqs, int64_t N, int Hk, int Hv, int D, float scale, int l2norm,
+                                   uint16_t* o, void* stream);
 
 /*
  * Recurrent gated delta rule for decode: T >= 1 tokens per sequence, state

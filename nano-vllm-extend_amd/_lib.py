@@ -19,6 +19,8 @@ ABI_VERSION = 2
 GDN_OK = 0
 GDN_ERR_INVALID_ARG = -1
 GDN_ERR_UNSUPPORTED = -2
+GDN_ERR_SCRATCH = -3
+NOALLOC_SCRATCH_BYTES = 128 << 20   # GDN_NOALLOC_SCRATCH_BYTES
 
 
 class GDNLibraryError(RuntimeError):
@@ -47,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "gdn_conv_chunk_prefill": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _i64, _p, _p,
                                _i32, _i32, _p, _i32, _i64, _i32, _i32, _i32, _f32, _i32, _p, _p, _i64, _p],
     "gdn_conv_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],
+    "gdn_conv_chunk_prefill_noalloc": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _i64,
+                                       _p, _p, _i32, _i32, _i64, _i32, _i32, _i32, _f32, _i32, _p, _p],
     "gdn_recurrent": [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
                       _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _p, _i32, _p],
     "gdn_recurrent_decode_fused": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32,
@@ -95,6 +99,9 @@ def check(name: str, status: int) -> None:
         raise GDNKernelError(f"{name}: invalid argument (shape / stride / alignment rejected)")
     if status == GDN_ERR_UNSUPPORTED:
         raise GDNKernelError(f"{name}: unsupported configuration (head dim must be 64 or 128, conv width 4)")
+    if status == GDN_ERR_SCRATCH:
+        raise GDNKernelError(f"{name}: the call needs more scratch than the allocation-free entry point's fixed "
+                             f"{NOALLOC_SCRATCH_BYTES >> 20} MiB array holds; use the workspace entry point")
     raise GDNKernelError(f"{name}: HIP launch failed with hipError_t {status}")
 
 

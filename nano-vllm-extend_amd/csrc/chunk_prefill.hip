@@ -53,6 +53,7 @@
 // XOR-swizzled by row (swz), so 16 lanes reading one granule column of 16
 // rows hit 16 distinct bank groups.
 #include <algorithm>
+#include <mutex>
 
 #include "gdn_common.h"
 
@@ -2029,4 +2030,76 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   return launch_chunk<64>(x, sx_row, x, sx_row, xv, sx_row, nullptr, nullptr, h0, hT, state_ids, state_stride,
                           cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
                           ws, seg_ws, &cv, phase, select_host, s);
+}
+
+// ---- the allocation-free variant of gdn_conv_chunk_prefill ----
+// For callers that cannot allocate device memory (HIP graph capture, tight
+// serving loops, harnesses that forbid hipMalloc): the records and the
+// segment scratch live in one fixed device array instead of a caller
+// workspace.  Every call on a GPU shares that GPU's array, so calls that
+// overlap on one GPU (other streams, other threads) race; calls in order on
+// one stream are safe.  Nothing in it has to start at zero: each call writes
+// every record and segment state before reading it.
+constexpr int64_t kNoAllocScratchBytes = GDN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxScratchDevices];
+
+// The device address of `scratch` on the device the stream runs on.  The
+// host-side name is only a stand-in; each device holds its own copy at its
+// own address, looked up once per device with that device current.
+int scratch_on(hipStream_t stream, uint8_t** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return e;
+  int dev = cur;
+  if (stream) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) return e;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) return GDN_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return GDN_OK;
+}
+
+}  // namespace
+
+extern "C" int gdn_conv_chunk_prefill_noalloc(const uint16_t* x, int64_t sx_row, uint16_t* conv_state,
+                                              int64_t ss_seq, int64_t ss_ch, const uint16_t* conv_w,
+                                              const uint16_t* b, const uint16_t* a, const void* A_log,
+                                              const void* dt_bias, int param_is_fp32, const float* h0, float* hT,
+                                              const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
+                                              const int64_t* cu_seqlens, const int64_t* cu_seqlens_host,
+                                              int max_segments, int n_seqs, int64_t N, int Hk, int Hv, int D,
+                                              float scale, int l2norm, uint16_t* o, void* stream) {
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (n_seqs < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
+  if (n_seqs == 0) return GDN_OK;
+  const int64_t need = gdn_conv_chunk_prefill_workspace_size(N, n_seqs, Hv, D);
+  if (need < 0) return GDN_ERR_INVALID_ARG;
+  if (need > kNoAllocScratchBytes) return GDN_ERR_SCRATCH;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* ws = nullptr;
+  const int st = scratch_on(s, &ws);
+  if (st != GDN_OK) return st;
+  return gdn_conv_chunk_prefill(x, sx_row, conv_state, ss_seq, ss_ch, conv_w, b, a, A_log, dt_bias, param_is_fp32,
+                                h0, hT, state_ids, fresh, state_stride, cu_seqlens, cu_seqlens_host, max_segments,
+                                kPhasePrep | kPhaseState, nullptr, n_seqs, N, Hk, Hv, D, scale, l2norm, o, ws,
+                                kNoAllocScratchBytes, stream);
 }

@@ -371,6 +371,50 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     return o, side_done
 
 
+def conv_chunk_prefill_varlen_noalloc(mixed: torch.Tensor, conv_state: torch.Tensor, conv_weight: torch.Tensor,
+                                      b: torch.Tensor, a: torch.Tensor, a_log: torch.Tensor, dt_bias: torch.Tensor,
+                                      cu_seqlens: torch.Tensor, state: torch.Tensor, state_ids: torch.Tensor | None,
+                                      num_k_heads: int, num_v_heads: int, head_dim: int, out: torch.Tensor,
+                                      scale: float | None = None, fresh: torch.Tensor | None = None,
+                                      cu_seqlens_cpu: torch.Tensor | None = None, max_segments: int = 0) -> None:
+    """conv_chunk_prefill_varlen through the allocation-free entry point: the
+    records live in the library's fixed per-GPU scratch array (no workspace
+    allocation), and the output goes to the caller's `out` [N, Hv, D] bf16.
+    Nothing here allocates device memory or copies: the inputs must already
+    have the layouts the kernels read (checked).  Calls that overlap on one
+    GPU race on the shared array.  Raises GDNKernelError when the call needs
+    more than the array holds."""
+    dev = _check_cuda(mixed, conv_state, conv_weight, b, a, a_log, dt_bias, cu_seqlens, state, state_ids, out, fresh)
+    Hk, Hv, D = num_k_heads, num_v_heads, head_dim
+    N, C = mixed.shape
+    for t, nm in ((mixed, "mixed"), (conv_state, "conv_state"), (a, "a"), (b, "b"), (out, "out"),
+                  (conv_weight, "conv_weight")):
+        _bf16(t, nm)
+    assert C == 2 * Hk * D + Hv * D and Hv % Hk == 0
+    assert mixed.stride(1) == 1 and mixed.stride(0) % 8 == 0
+    assert conv_weight.is_contiguous() and conv_weight.numel() == 4 * C
+    assert conv_state.stride(2) == 1 and tuple(conv_state.shape[1:]) == (C, 3)
+    assert a.is_contiguous() and b.is_contiguous() and a.shape == (N, Hv) and b.shape == (N, Hv)
+    assert a_log.dtype == dt_bias.dtype and a_log.dtype in (torch.bfloat16, torch.float32)
+    assert a_log.is_contiguous() and dt_bias.is_contiguous()
+    assert _state_view_ok(state, Hv, D), "state must be an fp32 [slots, Hv, D, D] view"
+    assert cu_seqlens.dtype == torch.int64 and cu_seqlens.is_contiguous()
+    n = cu_seqlens.shape[0] - 1
+    if state_ids is not None:
+        assert state_ids.dtype == torch.int64 and state_ids.is_contiguous() and state_ids.shape == (n,)
+    if fresh is not None:
+        assert fresh.dtype == torch.uint8 and fresh.is_contiguous() and fresh.shape == (n,)
+    assert out.shape == (N, Hv, D) and out.is_contiguous()
+    cu_host = _host_offsets(cu_seqlens_cpu, n)
+    if scale is None:
+        scale = D ** -0.5
+    _lib.call("gdn_conv_chunk_prefill_noalloc", _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_state),
+              conv_state.stride(0), conv_state.stride(1), _lib.ptr(conv_weight), _lib.ptr(b), _lib.ptr(a),
+              _lib.ptr(a_log), _lib.ptr(dt_bias), int(a_log.dtype == torch.float32), _lib.ptr(state),
+              _lib.ptr(state), _lib.ptr(state_ids), _lib.ptr(fresh), state.stride(0), _lib.ptr(cu_seqlens),
+              _host_ptr(cu_host), int(max_segments), n, N, Hk, Hv, D, float(scale), 1, _lib.ptr(out), _stream(dev))
+
+
 def chunk_gated_delta_rule(query, key, value, g=None, beta=None, scale=None, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False,
                            cu_seqlens=None, cu_seqlens_cpu=None, chunk_size=64, **kwargs):
