@@ -211,6 +211,62 @@ def prefill_bench(pkg, cfg, dev, K, W):
     return t / K, us
 
 
+def layer_bench(pkg, cfg, dev, K, W, hidden=2048):
+    """Config 1 through the whole GDN mixer (GatedDeltaNetLayer): in_proj GEMM
+    over the concatenated qkv / z / b / a weights, the layer core, out_proj
+    GEMM.  Random-init weights of a 2048 hidden size (the configs do not name
+    one).  Also times the same two GEMM shapes through torch.matmul (hipBLASLt)
+    for comparison."""
+    import math
+    gen = torch.Generator().manual_seed(11)
+    Hk, Hv, D = cfg["Hk"], cfg["Hv"], cfg["D"]
+    C = cfg["C"]
+    s = 1 / math.sqrt(hidden)
+    ws = [(torch.randn(r, hidden, generator=gen) * s).to(BF16).to(dev) for r in (C, Hv * D, Hv, Hv)]
+    w_out = (torch.randn(hidden, Hv * D, generator=gen) / math.sqrt(Hv * D)).to(BF16).to(dev)
+    layer = pkg.GatedDeltaNetLayer(*ws, w_out, Hk, Hv, D, cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
+                                   cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
+    N = cfg["N"]
+    x = torch.randn(N, hidden, generator=gen).to(BF16).to(dev)
+    n = len(cfg["lens"])
+    cu = torch.tensor([0] + torch.tensor(cfg["lens"]).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    ids = torch.arange(n, device=dev)
+    s_pool, conv_pool = cfg["h0"].to(dev), cfg["conv_state"].to(dev)
+    lens = cfg["lens"]
+
+    def step():
+        layer.forward(x, cu, max(lens), ids, conv_pool, s_pool, lens_q=lens)
+
+    for _ in range(W):
+        step()
+    t = timed_steps(step, K)
+    timer = EventTimer()
+    layer.timer = timer
+    for _ in range(min(K, 20)):
+        step()
+    torch.cuda.synchronize()
+    layer.timer = None
+    layer.core.timer = None
+    us = timer.avg_us()
+    # the same GEMM shapes through torch.matmul (hipBLASLt)
+    y_in = torch.empty(N, layer.n_in, dtype=BF16, device=dev)
+    core_out = torch.randn(N, Hv * D, generator=gen).to(BF16).to(dev)
+    y_out = torch.empty(N, hidden, dtype=BF16, device=dev)
+    ref = EventTimer()
+    for _ in range(3):
+        torch.matmul(x, layer.w_in.t(), out=y_in)
+        torch.matmul(core_out, layer.w_out.t(), out=y_out)
+    for _ in range(10):
+        ref.start("in_proj_hipblaslt")
+        torch.matmul(x, layer.w_in.t(), out=y_in)
+        ref.stop("in_proj_hipblaslt")
+        ref.start("out_proj_hipblaslt")
+        torch.matmul(core_out, layer.w_out.t(), out=y_out)
+        ref.stop("out_proj_hipblaslt")
+    torch.cuda.synchronize()
+    return t / K, us, ref.avg_us(), layer.n_in, hidden
+
+
 def decode_bench(pkg, cfg, dev, K, W):
     core = pkg.GatedDeltaNetCore(cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
                                  cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
@@ -359,7 +415,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="1,2,3,4")
+    ap.add_argument("--configs", default="1,2,3,4,5",
+                    help="1-4: BASELINE configs; 5: config 1 through the whole mixer with its projections")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB K times (the reference kernel for "
@@ -409,6 +466,18 @@ def main():
                 "kernel_us": round(chunk_us, 2), "algorithmic_flop_per_launch": flops}
     kernels1 = {k: round(v, 2) for k, v in k1.items()}
 
+    if 5 in configs:
+        t5, k5, r5, n_in, hidden = layer_bench(pkg, cfg1, dev, max(2, K // 4), 2)
+        fl_in = 2.0 * N1 * n_in * hidden
+        fl_out = 2.0 * N1 * hidden * cfg1["Hv"] * cfg1["D"]
+        extra["layer_with_projections_config1"] = {
+            "tokens_per_s": round(N1 / t5, 1), "ms_per_step": round(t5 * 1e3, 4), "hidden": hidden,
+            "kernels_us": {k: round(v, 2) for k, v in k5.items()},
+            "in_proj_TFLOPs": round(fl_in / (k5["in_proj"] * 1e-6) / 1e12, 1),
+            "out_proj_TFLOPs": round(fl_out / (k5["out_proj"] * 1e-6) / 1e12, 1),
+            "hipblaslt_same_shapes_us": {k: round(v, 2) for k, v in r5.items()},
+            "note": "in_proj = one GEMM over the concatenated qkv/z/b/a weights [N, 2048] x [8224, 2048]^T; "
+                    "out_proj [N, 2048] x [2048, 2048]^T; random-init weights"}
     if 2 in configs:
         c2 = make_decode()
         t2, t2g, k2, rec_us = decode_bench(pkg, c2, dev, K, W)

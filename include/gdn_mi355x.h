@@ -297,6 +297,27 @@ int gdn_state_commit(float* pool, int64_t slot_stride, const int64_t* ids, const
                      const int32_t* accepted, int B, int T, int Hv, int D, void* stream);
 
 /*
+ * The layer's projections: C = A B^T, bf16 operands, fp32 accumulation, bf16
+ * result.  Replaces F.linear in ColumnParallelLinear / RowParallelLinear
+ * (nanovllm/layers/linear.py:56-75, :133-158) at the GDN layer's in_proj_qkv,
+ * in_proj_z, in_proj_b, in_proj_a (nanovllm/models/qwen3_5.py:929-939,
+ * :1008-1010; one call over the four weights concatenated) and out_proj
+ * (:964, :1086).
+ *   A [M, K] row stride lda; B [N, K] (the nn.Linear weight) row stride ldb;
+ *   C [M, N] row stride ldc.  K a multiple of 64; lda, ldb multiples of 8 and
+ *   A, B 16-byte aligned (C rows go out in 16-byte pieces when ldc is a
+ *   multiple of 8 and C 16-byte aligned, else element by element).
+ *   g, beta, A_log, dt_bias, param_is_fp32, gate_col, Hv (g == NULL: none):
+ *   the columns [gate_col, gate_col + Hv) of C are the b projection and
+ *   [gate_col + Hv, gate_col + 2 Hv) the a projection; from their bf16 values
+ *   beta [M, Hv] bf16 and g [M, Hv] fp32 are also written, as gdn_g_beta
+ *   computes them (fused_g_beta, qwen3_5.py:345-360).
+ */
+int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, uint16_t* C, int64_t ldc, int M,
+                  int N, int K, float* g, uint16_t* beta, const void* A_log, const void* dt_bias, int param_is_fp32,
+                  int gate_col, int Hv, void* stream);
+
+/*
  * Gated RMSNorm on the value head dim.  Replaces Qwen3_5RMSNormGated /
  * _rms_gated_forward (nanovllm/models/qwen3_5.py:121-131, :697-709):
  *   y = bf16( float(bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))) * silu(float(z)) )

@@ -2,7 +2,8 @@
 
 The GDN kernels of the Qwen3.5 hybrid model -- varlen / decode / padded
 causal conv + SiLU, fused g/beta, chunked gated delta rule, recurrent
-decode (single- and multi-token), gated RMSNorm -- as hand-written HIP for
+decode (single- and multi-token), gated RMSNorm, the projection GEMMs -- as
+hand-written HIP for
 gfx950 behind the C ABI of include/gdn_mi355x.h, with Python wrappers that
 keep the reference's call signatures (ops), a host mirror of the layer
 dispatch (gdn_layer), the slot-pool bookkeeping (state_pool) and the hook
@@ -19,10 +20,11 @@ from .ops import (  # noqa: F401
     commit_states,
     conv_decode_step,
     fused_g_beta,
+    linear,
     recurrent_gated_delta_rule,
     recurrent_gdn_inplace,
     recurrent_gdn_multitoken,
     rms_norm_gated,
 )
-from .gdn_layer import GatedDeltaNetCore, Switches  # noqa: F401
+from .gdn_layer import GatedDeltaNetCore, GatedDeltaNetLayer, Switches  # noqa: F401
 from .state_pool import LinearStatePool, allocate_state_pools, reset_linear_states, varlen_meta  # noqa: F401

@@ -20,8 +20,20 @@
 
 namespace {
 
-__device__ __forceinline__ void store_nt(float* p, const float4& v) {
-  __builtin_nontemporal_store(gdn::f32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<gdn::f32x4_t*>(p));
+// State tiles move through raw buffer loads and stores: the tile base in the
+// descriptor (uniform over the workgroup), the lane's offset in one VGPR and
+// the pass's offset as an immediate, so the NP row passes need no address
+// registers of their own.  The range is left open (offsets stay inside the
+// D x D tile); stores are non-temporal (cache policy bit nt).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const float* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0), 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float4 tile_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ void tile_st_nt(__amdgpu_buffer_rsrc_t r, int voff, int soff, const float4& v) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, soff, 2);
 }
 
 // Inputs of the fused decode step (one token per sequence): the gates from
@@ -60,24 +72,24 @@ struct SrcIn {
   int T_src;
 };
 
-template <int D, int NVB, bool kFused>
-__global__ __launch_bounds__(256) void recurrent_kernel(
+template <int D, int NVB, int NW, bool kFused>
+__global__ __launch_bounds__(64 * NW) void recurrent_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, const uint16_t* __restrict__ k,
     int64_t sk_b, int64_t sk_t, const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t,
     const float* __restrict__ g, const uint16_t* __restrict__ beta, const float* s_in,
     int64_t s_in_stride, float* s_out, int64_t s_out_stride, const int64_t* __restrict__ ids,
     float* __restrict__ inter, uint16_t* __restrict__ o, int B, int T, int Hk, int Hv,
     float scale, int l2norm, DecodeIn din, NormIn nin, SrcIn src) {
-  constexpr int VB = D / NVB;     // state columns per workgroup
-  constexpr int CPR = VB / 4;     // float4 column groups per row
-  constexpr int RPP = 256 / CPR;  // rows per pass of the workgroup
+  constexpr int VB = D / NVB;       // state columns per workgroup
+  constexpr int CPR = VB / 4;       // float4 column groups per row
+  constexpr int RPP = 64 * NW / CPR;  // rows per pass of the workgroup
   constexpr int NP = D / RPP;     // passes (float4 registers per thread)
   static_assert(CPR <= 64 && 64 % CPR == 0 && NP >= 1, "tile shape");
 
   __shared__ float sq[2][D];
   __shared__ float sk[2][D];
   __shared__ float skq[2];
-  __shared__ float red[2][4][2][VB];
+  __shared__ float red[2][NW][2][VB];
 
   const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(B) * Hv * NVB);
   if (wi < 0) return;
@@ -94,12 +106,17 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
 
   const int64_t row = ids ? ids[b] : b;
   const int64_t acc = src.acc ? src.acc[b] : 0;
-  const float* sin = acc >= 1 ? src.src + ((static_cast<int64_t>(b) * src.T_src + acc - 1) * Hv + h) * D * D + col
-                              : s_in + row * s_in_stride + static_cast<int64_t>(h) * D * D + col;
+  const float* sin = acc >= 1 ? src.src + ((static_cast<int64_t>(b) * src.T_src + acc - 1) * Hv + h) * D * D
+                              : s_in + row * s_in_stride + static_cast<int64_t>(h) * D * D;
+  // byte offset of this lane's float4 in the tile, and of row pass j
+  const int voff = (r0 * D + col) * 4;
+  constexpr int kPass = RPP * D * 4;
   float4 S[NP];
+  {
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(sin);
 #pragma unroll
-  for (int j = 0; j < NP; ++j)
-    S[j] = *reinterpret_cast<const float4*>(sin + static_cast<int64_t>(r0 + RPP * j) * D);
+    for (int j = 0; j < NP; ++j) S[j] = tile_ld(r, voff, j * kPass);
+  }
 
   for (int t = 0; t < T; ++t) {
     const int buf = t & 1;
@@ -219,10 +236,12 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
     float delta[4], out[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float kvt = red[buf][0][0][c4 * 4 + i] + red[buf][1][0][c4 * 4 + i] +
-                        red[buf][2][0][c4 * 4 + i] + red[buf][3][0][c4 * 4 + i];
-      const float qvt = red[buf][0][1][c4 * 4 + i] + red[buf][1][1][c4 * 4 + i] +
-                        red[buf][2][1][c4 * 4 + i] + red[buf][3][1][c4 * 4 + i];
+      float kvt = red[buf][0][0][c4 * 4 + i], qvt = red[buf][0][1][c4 * 4 + i];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) {
+        kvt += red[buf][w][0][c4 * 4 + i];
+        qvt += red[buf][w][1][c4 * 4 + i];
+      }
       delta[i] = (vv[i] - kvt) * bt;
       out[i] = qvt + delta[i] * kq;
     }
@@ -232,9 +251,10 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
       S[j].x += kr * delta[0]; S[j].y += kr * delta[1]; S[j].z += kr * delta[2]; S[j].w += kr * delta[3];
     }
     if (inter) {
-      float* ip = inter + (static_cast<int64_t>(b) * T + t) * Hv * D * D + static_cast<int64_t>(h) * D * D + col;
+      const __amdgpu_buffer_rsrc_t r =
+          tile_rsrc(inter + ((static_cast<int64_t>(b) * T + t) * Hv + h) * static_cast<int64_t>(D) * D);
 #pragma unroll
-      for (int j = 0; j < NP; ++j) store_nt(ip + static_cast<int64_t>(r0 + RPP * j) * D, S[j]);
+      for (int j = 0; j < NP; ++j) tile_st_nt(r, voff, j * kPass, S[j]);
     }
     if (r0 == 0) {
       uint2 u;
@@ -275,9 +295,9 @@ __global__ __launch_bounds__(256) void recurrent_kernel(
   }
 
   if (s_out) {
-    float* sout = s_out + row * s_out_stride + static_cast<int64_t>(h) * D * D + col;
+    const __amdgpu_buffer_rsrc_t r = tile_rsrc(s_out + row * s_out_stride + static_cast<int64_t>(h) * D * D);
 #pragma unroll
-    for (int j = 0; j < NP; ++j) store_nt(sout + static_cast<int64_t>(r0 + RPP * j) * D, S[j]);
+    for (int j = 0; j < NP; ++j) tile_st_nt(r, voff, j * kPass, S[j]);
   }
 }
 
@@ -298,7 +318,7 @@ __global__ __launch_bounds__(256) void state_commit_kernel(float* __restrict__ p
   for (int i = threadIdx.x; i < D * D / 4; i += 256) dst[i] = src[i];
 }
 
-template <int D, int NVB>
+template <int D, int NVB, int NW = 4>
 int launch_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k, int64_t sk_b,
                      int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t, const float* g,
                      const uint16_t* beta, const float* s_in, int64_t s_in_stride, float* s_out,
@@ -308,11 +328,11 @@ int launch_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16
   const int64_t work = static_cast<int64_t>(B) * Hv * NVB;
   const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
   if (din.xv)
-    recurrent_kernel<D, NVB, true><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
+    recurrent_kernel<D, NVB, NW, true><<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, stream>>>(
         q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
         ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
   else
-    recurrent_kernel<D, NVB, false><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, stream>>>(
+    recurrent_kernel<D, NVB, NW, false><<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, stream>>>(
         q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
         ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
   return gdn_launch_status();

@@ -411,3 +411,68 @@ class GatedDeltaNetCore:
 
         core = self.prefill_padded(pad(mixed), pad(z), pad(b), pad(a), lens, ids, conv_cache, s_cache)
         return core.reshape(n, T, self.value_dim)[mask]
+
+
+class GatedDeltaNetLayer:
+    """The whole GDN mixer of one layer, projections included
+    (Qwen3_5GatedDeltaNet, nanovllm/models/qwen3_5.py:786-1087, tp = 1):
+
+      hidden [N, hidden] --in_proj--> mixed | z | b | a --core--> [N, Hv, D]
+      --out_proj--> [N, hidden]
+
+    in_proj is one GEMM over the four projection weights concatenated
+    (in_proj_qkv [C, hidden], in_proj_z [Hv*D, hidden], in_proj_b [Hv, hidden],
+    in_proj_a [Hv, hidden], :811-822), whose output rows hold mixed, z, b and a
+    side by side; the core reads them as strided views (the fused prefill and
+    decode kernels take the raw b and a and compute g / beta themselves).
+    out_proj [hidden, Hv*D] (:838-839) runs on the gated norm's output.  Both
+    GEMMs are ops.linear (bf16 matrix cores, fp32 accumulation)."""
+
+    def __init__(self, w_qkv, w_z, w_b, w_a, w_out, num_k_heads: int, num_v_heads: int, head_dim: int,
+                 conv_weight, A_log, dt_bias, norm_weight, eps: float = 1e-6, switches: Switches | None = None):
+        self.core = GatedDeltaNetCore(num_k_heads, num_v_heads, head_dim, conv_weight, A_log, dt_bias, norm_weight,
+                                      eps=eps, switches=switches)
+        c = self.core
+        assert w_qkv.shape[0] == c.conv_dim and w_z.shape[0] == c.value_dim
+        assert w_b.shape[0] == num_v_heads and w_a.shape[0] == num_v_heads
+        self.hidden = w_qkv.shape[1]
+        self.w_in = torch.cat([w_qkv, w_z, w_b, w_a], dim=0).contiguous()
+        self.w_out = w_out.contiguous()
+        assert self.w_out.shape == (self.hidden, c.value_dim)
+        self.timer = None
+
+    @property
+    def n_in(self) -> int:
+        return self.w_in.shape[0]
+
+    def _timed(self, name):
+        t = self.timer
+        if t is None:
+            return contextlib.nullcontext()
+
+        @contextlib.contextmanager
+        def cm():
+            t.start(name)
+            yield
+            t.stop(name)
+
+        return cm()
+
+    def project_in(self, hidden):
+        """hidden [N, hidden] -> (mixed, z, b, a) as column views of one
+        [N, C + Hv*D + 2 Hv] bf16 buffer."""
+        c = self.core
+        with self._timed("in_proj"):
+            y = ops.linear(hidden, self.w_in)
+        C, V, Hv = c.conv_dim, c.value_dim, c.Hv
+        return y[:, :C], y[:, C:C + V], y[:, C + V:C + V + Hv], y[:, C + V + Hv:]
+
+    def forward(self, hidden, cu_seqlens_q, max_seqlen_q, ids, conv_cache, s_cache, lens_q=None):
+        """Qwen3_5GatedDeltaNet.forward for one varlen step (qwen3_5.py:864-920):
+        hidden [N, hidden] bf16 -> [N, hidden] bf16."""
+        mixed, z, b, a = self.project_in(hidden)
+        self.core.timer = self.timer
+        core = self.core.forward(mixed, z, b.contiguous(), a.contiguous(), cu_seqlens_q, max_seqlen_q, ids,
+                                 conv_cache, s_cache, lens_q=lens_q)
+        with self._timed("out_proj"):
+            return ops.linear(core, self.w_out)

@@ -684,6 +684,56 @@ def commit_states(s_pool, ids, intermediate_states, accepted):
               _lib.ptr(intermediate_states), _lib.ptr(acc), Bsz, T, Hv, D, _stream(dev))
 
 
+# ------------------------------------------------------------- projections --
+def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+           gates: dict | None = None) -> torch.Tensor:
+    """F.linear(x, weight) without bias on the bf16 matrix cores (fp32
+    accumulation): x [..., K] bf16 (last dim contiguous), weight [N, K] bf16
+    (nn.Linear layout).  Returns [..., N] bf16 (or writes `out`, a [M, N]
+    view with contiguous rows).  gates: {"gate_col", "A_log", "dt_bias"}
+    (and the Hv of A_log): the columns [gate_col, gate_col + Hv) are the b
+    projection and the next Hv the a projection; beta (bf16) and g (fp32)
+    [M, Hv] of them are also computed and returned as (y, g, beta), equal to
+    fused_g_beta on those columns.
+    Reference: ColumnParallelLinear / RowParallelLinear.forward,
+    nanovllm/layers/linear.py:74-75, :154-158 (tp = 1)."""
+    dev = _check_cuda(x, weight, out)
+    _bf16(x, "x")
+    _bf16(weight, "weight")
+    K = x.shape[-1]
+    N = weight.shape[0]
+    assert weight.shape[1] == K
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w = weight if (weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0) \
+        else weight.contiguous()
+    M = x2.shape[0]
+    if out is None:
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    else:
+        _bf16(out, "out")
+        assert out.shape == (M, N) and out.stride(1) == 1
+        y = out
+    g = beta = None
+    a_log = dt_bias = None
+    gate_col = Hv = 0
+    if gates is not None:
+        a_log, dt_bias = gates["A_log"], gates["dt_bias"]
+        if a_log.dtype != dt_bias.dtype or a_log.dtype not in (torch.bfloat16, torch.float32):
+            a_log, dt_bias = a_log.float(), dt_bias.float()
+        a_log, dt_bias = a_log.contiguous(), dt_bias.contiguous()
+        Hv = a_log.numel()
+        gate_col = int(gates["gate_col"])
+        g = torch.empty(M, Hv, dtype=torch.float32, device=x.device)
+        beta = torch.empty(M, Hv, dtype=torch.bfloat16, device=x.device)
+    _lib.call("gdn_gemm_bf16", _lib.ptr(x2), x2.stride(0), _lib.ptr(w), w.stride(0), _lib.ptr(y), y.stride(0),
+              M, N, K, _lib.ptr(g), _lib.ptr(beta), _lib.ptr(a_log), _lib.ptr(dt_bias),
+              int(a_log is not None and a_log.dtype == torch.float32), gate_col, Hv, _stream(dev))
+    y = y.view(*x.shape[:-1], N) if out is None else y
+    return y if gates is None else (y, g, beta)
+
+
 # -------------------------------------------------------------- gated norm --
 def rms_norm_gated(hidden_states: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor,
                    eps: float) -> torch.Tensor:

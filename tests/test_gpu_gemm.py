@@ -1,0 +1,79 @@
+"""GPU parity of the projection GEMM (gdn_gemm_bf16): C = A B^T with bf16
+operands and fp32 accumulation against an fp32 CPU matmul of the same bf16
+values, on the GDN layer's projection shapes (in_proj over the concatenated
+qkv / z / b / a weights, out_proj) and ragged edges; the fused gate epilogue
+against fused_g_beta on the b / a columns."""
+import math
+
+import pytest
+import torch
+
+from helpers import BF16, bf16_step
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(c, ref, scale, tag):
+    """Each element within one bf16 step of the fp32 reference plus the fp32
+    summation-order slack 2^-16 (|A| |B|^T) (the reference and the kernel add
+    the K products in different orders; near-zero results carry that absolute
+    error), and elements that are not the rounded reference rare."""
+    c, ref = c.float().cpu(), ref.float()
+    d = (c - ref).abs()
+    bound = bf16_step(ref) + scale * 2.0 ** -16
+    assert bool((d <= bound).all()), f"{tag}: max |diff| / bound {float((d / bound).max()):.2f}"
+    flips = (c != ref.to(BF16).float()).float().mean().item()
+    assert flips < 2e-2, f"{tag}: {flips:.2e} of elements are not the rounded reference"
+
+
+def _ref(a, w):
+    return a.float() @ w.float().t(), a.float().abs() @ w.float().abs().t()
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 200, 128), (1, 8224, 2048), (17, 2048, 2048),
+                                   (1000, 2080, 512), (4111, 333, 192)])
+def test_gemm_against_fp32_matmul(pkg, dev, M, N, K):
+    gen = torch.Generator().manual_seed(M * 7 + N)
+    a = torch.randn(M, K, generator=gen).to(BF16)
+    w = (torch.randn(N, K, generator=gen) / math.sqrt(K)).to(BF16)
+    ref, sc = _ref(a, w)
+    c = pkg.ops.linear(a.to(dev), w.to(dev))
+    _check(c, ref, sc, f"gemm {M}x{N}x{K}")
+
+
+def test_gemm_strided_operands_and_out(pkg, dev):
+    """Row strides larger than K (views of wider buffers) and an output view."""
+    gen = torch.Generator().manual_seed(5)
+    M, N, K = 333, 264, 256
+    abuf = torch.randn(M, K + 64, generator=gen).to(BF16)
+    wbuf = (torch.randn(N, K + 128, generator=gen) / 16).to(BF16)
+    a, w = abuf[:, 32:32 + K], wbuf[:, :K]
+    out = torch.zeros(M, N + 40, dtype=BF16, device=dev)
+    pkg.ops.linear(abuf.to(dev)[:, 32:32 + K], wbuf.to(dev)[:, :K], out=out[:, 8:8 + N])
+    _check(out[:, 8:8 + N], *_ref(a, w), "strided gemm")
+    assert torch.equal(out[:, :8].cpu(), torch.zeros(M, 8, dtype=BF16))
+    assert torch.equal(out[:, 8 + N:].cpu(), torch.zeros(M, 32, dtype=BF16))
+
+
+def test_in_proj_with_gate_epilogue(pkg, dev):
+    """The layer's in_proj over [W_qkv; W_z; W_b; W_a] (config 1 widths, a
+    2048 hidden size): the projections, and g / beta from the b and a columns
+    equal to fused_g_beta on them."""
+    gen = torch.Generator().manual_seed(6)
+    Hk = Hv = 16
+    D, hidden = 128, 2048
+    C = 2 * Hk * D + Hv * D
+    N = C + Hv * D + 2 * Hv
+    M = 777
+    x = torch.randn(M, hidden, generator=gen).to(BF16)
+    w = (torch.randn(N, hidden, generator=gen) / math.sqrt(hidden)).to(BF16)
+    A_log = (torch.rand(Hv, generator=gen) * math.log(16)).to(BF16)
+    dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(BF16)
+    y, g, beta = pkg.ops.linear(x.to(dev), w.to(dev), gates={"gate_col": C + Hv * D, "A_log": A_log.to(dev),
+                                                             "dt_bias": dt_bias.to(dev)})
+    _check(y, *_ref(x, w), "in_proj")
+    b = y[:, C + Hv * D:C + Hv * D + Hv].contiguous()
+    a = y[:, C + Hv * D + Hv:].contiguous()
+    g2, beta2 = pkg.ops.fused_g_beta(b, a, A_log.to(dev), dt_bias.to(dev), None)
+    torch.cuda.synchronize()
+    assert torch.equal(g, g2) and torch.equal(beta.view(torch.int16), beta2.view(torch.int16))
