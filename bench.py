@@ -42,6 +42,15 @@ BF16_PEAK_TFLOPS = 2500.0       # MI355X dense bf16 MFMA
 BF16 = torch.bfloat16
 
 
+def prefill_compulsory_bytes(cfg) -> int:
+    """HBM bytes the fused prefill call cannot avoid: the conv input rows
+    (bf16 [N, C]), the b / a gate inputs (bf16 [N, Hv] each), the output
+    (bf16 [N, Hv*D]), each sequence's state read and written (fp32
+    [Hv, D, D]) and its conv state read and written (bf16 [C, 3])."""
+    N, C, Hv, D, n = cfg["N"], cfg["C"], cfg["Hv"], cfg["D"], len(cfg["lens"])
+    return N * (2 * C + 4 * Hv + 2 * Hv * D) + n * (2 * 4 * Hv * D * D + 2 * 2 * C * 3)
+
+
 def chunk_flops(n_tokens: int, Hv: int, D: int, C: int = 64) -> float:
     """Algorithmic chunk-prefill FLOPs per call: N*Hv*[2C(3D+2D) + 6D^2 + (2/3)C^2]
     (full QK^T/KK^T tiles, W, U, intra-chunk O, three state GEMMs, the solve)."""
@@ -377,6 +386,50 @@ def spec_bench(pkg, cfg, dev, K, W):
     return t / K, us
 
 
+def standalone_kernels(pkg, cfg, dev, K, W):
+    """The kernels the fused prefill replaces, each launched on its own at
+    config 1's shapes (the path the unfused switches select): the gates, the
+    varlen conv, the padded conv (sequences padded to the longest), the gated
+    norm.  Returns {kernel: (average us over K launches, compulsory bytes)}."""
+    N, C, Hv, D = cfg["N"], cfg["C"], cfg["Hv"], cfg["D"]
+    lens = cfg["lens"]
+    n, T = len(lens), max(lens)
+    x, z, a, b = (cfg[k].to(dev) for k in ("x", "z", "a", "b"))
+    A_log, dt_bias, w = cfg["A_log"].to(dev), cfg["dt_bias"].to(dev), cfg["conv_w"].to(dev)
+    lens32 = torch.tensor(lens, dtype=torch.int32, device=dev)
+    starts = torch.tensor([0] + torch.tensor(lens).cumsum(0)[:-1].tolist(), dtype=torch.int32, device=dev)
+    st_v = torch.zeros(n, C, 3, dtype=BF16, device=dev)
+    xp = torch.zeros(n, C, T, dtype=BF16, device=dev)
+    for i, (s0, l) in enumerate(zip(starts.tolist(), lens)):
+        xp[i, :, :l] = x[s0:s0 + l].t()
+    st_p = torch.zeros(n, C, 3, dtype=BF16, device=dev)
+    endp = lens32 - 1
+    core = torch.randn(N, Hv, D, device=dev).to(BF16)
+    zz = z.view(N, Hv, D)
+    nw = cfg["norm_w"].to(dev)
+    kd = cfg["Hk"] * D
+    launches = {
+        "g_beta_kernel": (lambda: pkg.ops.fused_g_beta(b, a, A_log, dt_bias, None), N * Hv * (2 + 2 + 4 + 2)),
+        "conv_varlen_kernel": (lambda: pkg.ops.causal_conv_silu_varlen_parts(x, st_v, w, lens32, starts, kd),
+                               2 * N * C * 2),
+        "conv_padded_kernel": (lambda: pkg.ops.causal_conv_silu(xp, st_p, w, endp), 2 * n * C * T * 2),
+        "rmsnorm_gated_kernel": (lambda: pkg.ops.rms_norm_gated(core, zz, nw, 1e-6), 3 * N * Hv * D * 2),
+    }
+    out = {}
+    for name, (fn, nbytes) in launches.items():
+        for _ in range(W):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(K):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = (1e3 * e0.elapsed_time(e1) / K, nbytes)
+    return out
+
+
 def cpu_baseline(cfg, n_seq: int, threads: int):
     """CPU oracle (fp32 torch restatement of the reference path) on the first
     n_seq sequences of config 1: 1 warm-up on a 256-token slice, median of 3."""
@@ -421,6 +474,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB K times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
+    ap.add_argument("--standalone-kernels", action="store_true",
+                    help="only time the gate, varlen-conv, padded-conv and gated-norm kernels on their own at "
+                         "config 1's shapes, K launches each")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the GDN path shards by value head / by sequence with no "
@@ -445,6 +501,12 @@ def main():
     pkg._lib.load()
     dev = torch.device("cuda:0")
     K, W = args.steps, args.warmup
+    if args.standalone_kernels:
+        res = standalone_kernels(pkg, make_prefill(1, None), dev, K, W)
+        print(json.dumps({"standalone_kernels_config1": {
+            k: {"us": round(t, 2), "compulsory_bytes": nb, "GBps": round(nb / (t * 1e-6) / 1e9, 1),
+                "hbm_frac": round(nb / (t * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)} for k, (t, nb) in res.items()}}))
+        return
     configs = {int(c) for c in args.configs.split(",") if c}
     extra = {}
 
@@ -455,8 +517,11 @@ def main():
     chunk_us = k1["conv_chunk_prefill" if fused else "chunk_prefill"]
     flops = chunk_flops(N1, cfg1["Hv"], cfg1["D"])
     achieved = flops / (chunk_us * 1e-6) / 1e12
+    floor1 = prefill_compulsory_bytes(cfg1)
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                "hbm_floor_frac": round(floor1 / (chunk_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                "compulsory_bytes_per_launch": floor1,
                 "traffic": _profiled_traffic("conv_chunk_prefill_config1" if fused else "chunk_prefill_config1"),
                 "kernel": ("gates + conv1d/SiLU + chunk rule = chunk_prep_kernel<128, true> + "
                            "chunk_state_kernel<128, true> (one launch pair per call; the time includes the conv and "
@@ -500,12 +565,18 @@ def main():
         K3 = max(2, K // 4)
         t3, k3 = prefill_bench(pkg, c3, dev, K3, 1)
         f3 = chunk_flops(c3["N"], c3["Hv"], c3["D"])
-        a3 = f3 / (k3["conv_chunk_prefill" if "conv_chunk_prefill" in k3 else "chunk_prefill"] * 1e-6) / 1e12
+        us3 = k3["conv_chunk_prefill" if "conv_chunk_prefill" in k3 else "chunk_prefill"]
+        a3 = f3 / (us3 * 1e-6) / 1e12
+        floor3 = prefill_compulsory_bytes(c3)
         extra["long_prefill_config3"] = {
             "tokens_per_s": round(c3["N"] / t3, 1), "ms_per_step": round(t3 * 1e3, 3), "steps": K3,
             "kernels_us": {k: round(v, 2) for k, v in k3.items()},
             "roofline": {"bound": "mfma", "achieved": round(a3, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(a3 / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+                         "frac": round(a3 / BF16_PEAK_TFLOPS, 4),
+                         "hbm_floor_frac": round(floor3 / (us3 * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                         "compulsory_bytes_per_launch": floor3,
+                         "traffic": _profiled_traffic("conv_chunk_prefill_config3"), "kernel_us": round(us3, 2),
+                         "algorithmic_flop_per_launch": f3}}
         del c3
     if 4 in configs:
         c4 = make_spec()
@@ -515,7 +586,11 @@ def main():
         extra["spec_verify_config4"] = {
             "ms_per_step": round(t4 * 1e3, 4), "kernels_us": {k: round(v, 2) for k, v in k4.items()},
             "roofline": {"bound": "hbm", "achieved": round(g4, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(g4 / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "frac": round(g4 / HBM_PEAK_GBPS, 4),
+                         "traffic": _profiled_traffic("recurrent_multitoken_config4"),
+                         "kernel": "recurrent_kernel multi-token form (reads the accepted state, writes T "
+                                   "intermediate states per row)",
+                         "kernel_us": round(k4["recurrent_multitoken"], 2),
                          "algorithmic_bytes_per_launch": rb}}
         del c4
 
