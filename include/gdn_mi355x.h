@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 2
+#define GDN_ABI_VERSION 3
 
 #define GDN_OK 0
 #define GDN_ERR_INVALID_ARG (-1) /* shape / stride / pointer rejected */
@@ -332,12 +332,13 @@ int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16_t* z, int6
  * The gated norm over some token ranges only (the same arithmetic):
  * ranges int64 [3 * n_ranges] on the device, (first token, token count,
  * selected tokens before this range) each; n_sel_tok = all selected tokens.
- * x, z, y as gdn_rmsnorm_gated (y rows at the tokens' own positions).  No
- * reference counterpart: it lets the norm of the sequences whose state pass
- * ends early run while the longest ones are still in the state kernel.
+ * x, z, y as gdn_rmsnorm_gated (y rows at the tokens' own positions), n_tok
+ * rows each: a range token outside [0, n_tok) is skipped.  No reference
+ * counterpart: it lets the norm of the sequences whose state pass ends early
+ * run while the longest ones are still in the state kernel.
  */
 int gdn_rmsnorm_gated_ranges(const uint16_t* x, int64_t sx_tok, const uint16_t* z, int64_t sz_tok,
-                             const uint16_t* w, uint16_t* y, const int64_t* ranges, int n_ranges,
+                             const uint16_t* w, uint16_t* y, int64_t n_tok, const int64_t* ranges, int n_ranges,
                              int64_t n_sel_tok, int H, int D, float eps, void* stream);
 
 #ifdef __cplusplus

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = Path(os.environ.get("GDN_MI355X_LIB", Path(__file__).resolve().parent / "lib" / "libgdn_mi355x.so"))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 GDN_OK = 0
 GDN_ERR_INVALID_ARG = -1
@@ -59,7 +59,7 @@ SIGNATURES: dict[str, list] = {
     "gdn_state_commit": [_p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _p],
     "gdn_gemm_bf16": [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _i32, _i32, _p],
     "gdn_rmsnorm_gated": [_p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p],
-    "gdn_rmsnorm_gated_ranges": [_p, _i64, _p, _i64, _p, _p, _p, _i32, _i64, _i32, _i32, _f32, _p],
+    "gdn_rmsnorm_gated_ranges": [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i32, _i64, _i32, _i32, _f32, _p],
 }
 
 # entry points whose return type is not int (status)

@@ -16,23 +16,30 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ w,
                                                             uint16_t* __restrict__ y,
                                                             int64_t rows, int H, float eps,
-                                                            const int64_t* __restrict__ ranges, int n_ranges) {
+                                                            const int64_t* __restrict__ ranges, int n_ranges,
+                                                            int64_t n_tok) {
   constexpr int kLanes = D / 8;                 // lanes per row
   constexpr int kRowsPerBlock = 256 / kLanes;
   const int lane = threadIdx.x % kLanes;
   const int64_t r_sel = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
-  const bool active = r_sel < rows;
+  bool active = r_sel < rows;
   int64_t tok = active ? r_sel / H : 0;
   const int h = active ? static_cast<int>(r_sel % H) : 0;
   if (ranges && active) {
-    // token ranges (start, count, tokens before it): the t-th selected token
+    // token ranges (start, count, tokens before it): the t-th selected token;
+    // a token that no range holds, or that falls outside the n_tok rows, is
+    // skipped
+    bool found = false;
     for (int i = 0; i < n_ranges; ++i) {
       const int64_t start = ranges[3 * i], cnt = ranges[3 * i + 1], before = ranges[3 * i + 2];
-      if (tok < before + cnt) {
+      if (tok >= before && tok < before + cnt) {
         tok = start + (tok - before);
+        found = true;
         break;
       }
     }
+    active = found && tok >= 0 && tok < n_tok;
+    if (!active) tok = 0;
   }
   const int64_t row = tok * H + h;
 
@@ -90,19 +97,19 @@ extern "C" int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16
   if (D == 128) {
     const int64_t nb = (rows + 15) / 16;
     rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                     nullptr, 0);
+                                                                                     nullptr, 0, n_tok);
   } else {
     const int64_t nb = (rows + 31) / 32;
     rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                    nullptr, 0);
+                                                                                    nullptr, 0, n_tok);
   }
   return gdn_launch_status();
 }
 
 extern "C" int gdn_rmsnorm_gated_ranges(const uint16_t* x, int64_t sx_tok, const uint16_t* z, int64_t sz_tok,
-                                        const uint16_t* w, uint16_t* y, const int64_t* ranges, int n_ranges,
-                                        int64_t n_sel_tok, int H, int D, float eps, void* stream) {
-  if (n_sel_tok < 0 || H <= 0 || n_ranges < 0) return GDN_ERR_INVALID_ARG;
+                                        const uint16_t* w, uint16_t* y, int64_t n_tok, const int64_t* ranges,
+                                        int n_ranges, int64_t n_sel_tok, int H, int D, float eps, void* stream) {
+  if (n_sel_tok < 0 || n_tok < 0 || n_sel_tok > n_tok || H <= 0 || n_ranges < 0) return GDN_ERR_INVALID_ARG;
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
   if (n_sel_tok == 0) return GDN_OK;
   if (!x || !z || !w || !y || !ranges || n_ranges == 0) return GDN_ERR_INVALID_ARG;
@@ -115,11 +122,11 @@ extern "C" int gdn_rmsnorm_gated_ranges(const uint16_t* x, int64_t sx_tok, const
   if (D == 128) {
     const int64_t nb = (rows + 15) / 16;
     rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                     ranges, n_ranges);
+                                                                                     ranges, n_ranges, n_tok);
   } else {
     const int64_t nb = (rows + 31) / 32;
     rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                    ranges, n_ranges);
+                                                                                    ranges, n_ranges, n_tok);
   }
   return gdn_launch_status();
 }

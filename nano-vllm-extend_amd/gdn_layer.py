@@ -276,16 +276,19 @@ class GatedDeltaNetCore:
         side = self._side_stream(dev)
         cur = torch.cuda.current_stream(dev)
         keep = []
+        # The side stream's norm reads the output and the range tables: both are
+        # allocated, and the tables copied, on the current stream before the
+        # prep launch, whose completion the side stream waits for.
+        y = torch.empty(N, Hv, D, dtype=torch.bfloat16, device=dev)
+        zz = z.view(N, Hv, D)
+        r_e = r_early.to(dev, non_blocking=True)
+        r_l = r_late.to(dev, non_blocking=True)
         with self._timed("conv_chunk_prefill"):
             o, side_done = ops.conv_chunk_prefill_varlen(mixed, conv_cache, self.conv_w, b, a, self.A_log,
                                                          self.dt_bias, cu64_gpu, s_cache, ids, Hk, Hv, D,
                                                          fresh=fresh, cu_seqlens_cpu=cu64_cpu, late=late,
                                                          side_stream=side, keep=keep)
             cur.wait_event(side_done)   # (the long sequences' state pass is the longer one)
-        y = torch.empty(N, Hv, D, dtype=torch.bfloat16, device=dev)
-        zz = z.view(N, Hv, D)
-        r_e = r_early.to(dev, non_blocking=True)
-        r_l = r_late.to(dev, non_blocking=True)
         with torch.cuda.stream(side):
             ops.rms_norm_gated_ranges(o, zz, self.norm_w, self.eps, y, r_e, n_early)
         with self._timed("rmsnorm_gated"):

@@ -777,8 +777,8 @@ def rms_norm_gated_ranges(hidden_states: torch.Tensor, gate: torch.Tensor, weigh
     assert gate.stride(2) == 1 and gate.stride(1) == D
     w = weight.to(torch.bfloat16).contiguous()
     _lib.call("gdn_rmsnorm_gated_ranges", _lib.ptr(hidden_states), hidden_states.stride(0), _lib.ptr(gate),
-              gate.stride(0), _lib.ptr(w), _lib.ptr(out), _lib.ptr(ranges), ranges.numel() // 3, n_sel_tok, H, D,
-              float(eps), _stream(dev))
+              gate.stride(0), _lib.ptr(w), _lib.ptr(out), N, _lib.ptr(ranges), ranges.numel() // 3, n_sel_tok, H,
+              D, float(eps), _stream(dev))
 
 
 class Qwen3_5RMSNormGated(torch.nn.Module):

@@ -357,3 +357,24 @@ def test_rmsnorm_gated_token_ranges(pkg, dev):
         mask[st:st + cnt] = True
     assert torch.equal(out.cpu()[mask].view(torch.int16), full.cpu()[mask].view(torch.int16))
     assert torch.all(out.cpu()[~mask] == 7.0)
+
+
+def test_rmsnorm_gated_token_ranges_bounded(pkg, dev):
+    """Range entries that point past the rows are skipped by the kernel's own
+    bounds (the in-range tokens still normalised exactly), and a range table
+    larger than the rows is refused on the host."""
+    gen = _gen(62)
+    N, H, D = 64, 2, 128
+    x = torch.randn(N, H, D, generator=gen).to(BF16).to(dev)
+    z = torch.randn(N, H, D, generator=gen).to(BF16).to(dev)
+    w = (1 + 0.02 * torch.randn(D, generator=gen)).to(BF16).to(dev)
+    full = pkg.ops.rms_norm_gated(x, z, w, 1e-6)
+    # (first token, count, before): tokens 60..63 valid, 64..67 past the rows
+    rows = torch.tensor([60, 8, 0], device=dev)
+    out = torch.full((N, H, D), 7.0, dtype=BF16, device=dev)
+    pkg.ops.rms_norm_gated_ranges(x, z, w, 1e-6, out, rows, 8)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu()[60:].view(torch.int16), full.cpu()[60:].view(torch.int16))
+    assert torch.all(out.cpu()[:60] == 7.0)
+    with pytest.raises(pkg._lib.GDNKernelError):
+        pkg.ops.rms_norm_gated_ranges(x, z, w, 1e-6, out, rows, N + 1)
