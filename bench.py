@@ -305,7 +305,8 @@ def decode_bench(pkg, cfg, dev, K, W):
     torch.cuda.current_stream().wait_stream(s)
     g.replay()
     t_graph = timed_steps(g.replay, K)
-    return t / K, t_graph / K, timer.avg_us(), recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z)
+    rec_us, pass_us = recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z)
+    return t / K, t_graph / K, timer.avg_us(), rec_us, pass_us
 
 
 def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, R=20):
@@ -313,7 +314,10 @@ def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, 
     launches between one event pair (an event pair around each launch adds a
     few microseconds to what it measures).  Launches alternate the batch's
     slots with the pool's other slots, so no launch finds its states cached
-    from the one before (the pool is larger than the last-level cache)."""
+    from the one before (the pool is larger than the last-level cache).
+    Also times, the same way, the state tile pass: the same state tiles read
+    and written back in place with no arithmetic (the ceiling of this access
+    pattern).  Returns (kernel us, tile pass us)."""
     B, Hk, Hv, D = x.shape[0], cfg["Hk"], cfg["Hv"], cfg["D"]
     kd = Hk * D
     used = set(ids.tolist())
@@ -336,6 +340,12 @@ def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, 
 
         def launch(sl):
             pkg.ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_pool, sl)
+    return _burst_us(launch, sets, R), _burst_us(lambda sl: pkg.ops.state_tile_pass(s_pool, sl), sets, R)
+
+
+def _burst_us(launch, sets, R):
+    """Average duration of R back-to-back launches over the slot sets in turn,
+    between one event pair (after an untimed launch)."""
     launch(sets[-1])
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -545,7 +555,7 @@ def main():
                     "out_proj [N, 2048] x [2048, 2048]^T; random-init weights"}
     if 2 in configs:
         c2 = make_decode()
-        t2, t2g, k2, rec_us = decode_bench(pkg, c2, dev, K, W)
+        t2, t2g, k2, rec_us, pass_us = decode_bench(pkg, c2, dev, K, W)
         state_bytes = 2 * c2["B"] * c2["Hv"] * c2["D"] * c2["D"] * 4
         gbps = state_bytes / (rec_us * 1e-6) / 1e9
         extra["decode_config2"] = {
@@ -558,7 +568,14 @@ def main():
                                    "conv with its state roll, state update)", "kernel_us": round(rec_us, 2),
                          "timing": "20 back-to-back launches between one event pair, alternating two disjoint "
                                    "slot sets of the pool",
-                         "algorithmic_bytes_per_launch": state_bytes}}
+                         "algorithmic_bytes_per_launch": state_bytes,
+                         "inplace_tile_ceiling": {
+                             "kernel_us": round(pass_us, 2),
+                             "GBps": round(state_bytes / (pass_us * 1e-6) / 1e9, 1),
+                             "kernel_frac_of_ceiling": round(pass_us / rec_us, 4),
+                             "what": "gdn_state_tile_pass: the same state tiles read and written back in place "
+                                     "with the decode kernel's layout, launch shape and cache policy, no "
+                                     "arithmetic, timed the same way"}}}
         del c2
     if 3 in configs:
         c3 = make_prefill(4, [65536], h0_std=0.1, conv_std=1.0)

@@ -297,6 +297,17 @@ int gdn_state_commit(float* pool, int64_t slot_stride, const int64_t* ids, const
                      const int32_t* accepted, int B, int T, int Hv, int D, void* stream);
 
 /*
+ * Measurement pass, no counterpart in the reference: every state tile
+ * pool[ids[b], h] (D x D fp32) is read into registers and written back
+ * unchanged, with the one-token decode kernel's tile layout, launch shape and
+ * cache policy -- the decode step's state traffic without its arithmetic.
+ * The pool's contents are left as they were (duplicate ids write identical
+ * values).  slot_stride >= Hv*D*D.
+ */
+int gdn_state_tile_pass(float* pool, int64_t slot_stride, const int64_t* ids, int B, int Hv, int D,
+                        void* stream);
+
+/*
  * The layer's projections: C = A B^T, bf16 operands, fp32 accumulation, bf16
  * result.  Replaces F.linear in ColumnParallelLinear / RowParallelLinear
  * (nanovllm/layers/linear.py:56-75, :133-158) at the GDN layer's in_proj_qkv,

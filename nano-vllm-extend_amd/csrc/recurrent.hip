@@ -318,6 +318,31 @@ __global__ __launch_bounds__(256) void state_commit_kernel(float* __restrict__ p
   for (int i = threadIdx.x; i < D * D / 4; i += 256) dst[i] = src[i];
 }
 
+// Measurement pass: each selected state tile read into registers and written
+// back unchanged, with the decode kernel's layout (NVB = 1, 4 waves), cache
+// policy and barrier between the loads and the stores: one decode step's
+// state traffic without its arithmetic.
+template <int D>
+__global__ __launch_bounds__(256) void state_tile_pass_kernel(float* pool, int64_t slot_stride,
+                                                              const int64_t* __restrict__ ids, int B, int Hv) {
+  constexpr int CPR = D / 4;
+  constexpr int RPP = 256 / CPR;
+  constexpr int NP = D / RPP;
+  constexpr int kPass = RPP * D * 4;
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(B) * Hv);
+  if (wi < 0) return;
+  const int h = static_cast<int>(wi % Hv);
+  const int b = static_cast<int>(wi / Hv);
+  const __amdgpu_buffer_rsrc_t r = tile_rsrc(pool + ids[b] * slot_stride + static_cast<int64_t>(h) * D * D);
+  const int voff = ((threadIdx.x / CPR) * D + (threadIdx.x % CPR) * 4) * 4;
+  float4 S[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) S[j] = tile_ld(r, voff, j * kPass);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NP; ++j) tile_st_nt(r, voff, j * kPass, S[j]);
+}
+
 template <int D, int NVB, int NW = 4>
 int launch_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k, int64_t sk_b,
                      int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t, const float* g,
@@ -445,4 +470,20 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
   if (nvb == 2) return launch_recurrent<64, 2>(GDN_REC_ARGS);
   return launch_recurrent<64, 4>(GDN_REC_ARGS);
 #undef GDN_REC_ARGS
+}
+
+extern "C" int gdn_state_tile_pass(float* pool, int64_t slot_stride, const int64_t* ids, int B, int Hv, int D,
+                                   void* stream) {
+  if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
+  if (B < 0 || Hv <= 0 || slot_stride % 4 || slot_stride < static_cast<int64_t>(Hv) * D * D) return GDN_ERR_INVALID_ARG;
+  if (B == 0) return GDN_OK;
+  if (!pool || !ids || reinterpret_cast<uintptr_t>(pool) % 16) return GDN_ERR_INVALID_ARG;
+  const int64_t work = static_cast<int64_t>(B) * Hv;
+  const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 128)
+    state_tile_pass_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(pool, slot_stride, ids, B, Hv);
+  else
+    state_tile_pass_kernel<64><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(pool, slot_stride, ids, B, Hv);
+  return gdn_launch_status();
 }

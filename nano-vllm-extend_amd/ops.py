@@ -685,6 +685,18 @@ def commit_states(s_pool, ids, intermediate_states, accepted):
 
 
 # ------------------------------------------------------------- projections --
+def state_tile_pass(s_pool: torch.Tensor, ids: torch.Tensor) -> None:
+    """Measurement pass (no reference counterpart): reads every state tile
+    s_pool[ids[b], h] and writes it back unchanged, with the one-token decode
+    kernel's tile layout and cache policy -- that step's state traffic without
+    its arithmetic.  s_pool [slots, Hv, D, D] fp32 (any slot stride)."""
+    dev = _check_cuda(s_pool, ids)
+    assert _state_view_ok(s_pool, s_pool.shape[1], s_pool.shape[-1])
+    ids64 = ids.to(torch.int64).contiguous()
+    _lib.call("gdn_state_tile_pass", _lib.ptr(s_pool), s_pool.stride(0), _lib.ptr(ids64), ids64.numel(),
+              s_pool.shape[1], s_pool.shape[-1], _stream(dev))
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
            gates: dict | None = None) -> torch.Tensor:
     """F.linear(x, weight) without bias on the bf16 matrix cores (fp32

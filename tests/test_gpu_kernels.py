@@ -378,3 +378,17 @@ def test_rmsnorm_gated_token_ranges_bounded(pkg, dev):
     assert torch.all(out.cpu()[:60] == 7.0)
     with pytest.raises(pkg._lib.GDNKernelError):
         pkg.ops.rms_norm_gated_ranges(x, z, w, 1e-6, out, rows, N + 1)
+
+
+def test_state_tile_pass_leaves_pool_unchanged(pkg, dev):
+    """The measurement pass reads and writes back the selected state tiles of a
+    per-layer pool view: every bit of the pool (other layers, other slots,
+    duplicated ids included) is as before."""
+    gen = _gen(63)
+    slots, L, Hv, D = 12, 3, 4, 128
+    pool = torch.randn(slots, L, Hv, D, D, generator=gen).to(dev)
+    before = pool.clone()
+    ids = torch.tensor([5, 0, 11, 5], device=dev)
+    pkg.ops.state_tile_pass(pool[:, 1], ids)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.cpu().view(torch.int32), before.cpu().view(torch.int32))
