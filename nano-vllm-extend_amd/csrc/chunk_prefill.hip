@@ -356,12 +356,14 @@ __device__ __forceinline__ void conv_load(ConvRaw<D>& R, const ConvIn& cv, int p
   constexpr int SEG = D / 8;
   const int c8 = tid % SEG, t0 = ConvRaw<D>::RPT * (tid / SEG);
   const int ch = conv_part_channel(cv, part, kh, h, D) + 8 * c8;
+  // chunk rows t >= lo keep row tok0 + t >= 0 (the clamp in 32 bits)
+  const int lo = tok0 < 3 ? -static_cast<int>(tok0) : -3;
 #pragma unroll
   for (int i = 0; i < ConvRaw<D>::RPT + 3; ++i) {
     // rows past the sequence end re-read its last row (outputs dropped); rows
     // before the first chunk's start are replaced by the state
     const int t = t0 - 3 + i;
-    const int64_t row = max<int64_t>(tok0 + min(t, len - 1), 0);
+    const int64_t row = tok0 + max(min(t, len - 1), lo);
     R.x[i] = *reinterpret_cast<const uint4*>(cv.x + row * cv.sx + ch);
   }
 }
