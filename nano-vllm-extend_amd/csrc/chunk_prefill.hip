@@ -14,9 +14,9 @@
 //   chunk_prep_kernel: one workgroup per (chunk, value head), all chunks in
 //     parallel.  Everything that needs only the chunk's own q, k, g, beta:
 //     the row norms, K K^T, Q K^T, the triangular inverse T (fp32), and it
-//     writes a 51 KiB record: -T' = -T diag(beta e^G / |k|), T'' = T diag(beta)
-//     and A as fp16 tiles, the per-token scales, and the q rows and K^T as
-//     fp16 operand fragments.  The fused variant first computes the gates
+//     writes a 57 KiB record: -T' = -T diag(beta e^G / |k|), T'' = T diag(beta),
+//     A and A's fp16 rounding residual as fp16 tiles, the per-token scales,
+//     and the q rows and K^T as fp16 operand fragments.  The fused variant first computes the gates
 //     and the conv1d + SiLU of the chunk's q and k channels from the raw rows.
 //   chunk_state_kernel: one workgroup per (sequence, value head, block of 64
 //     value columns), persistent over the sequence's chunks.  Producer waves
@@ -27,11 +27,13 @@
 //     their 128 x 32 slice of S in registers.
 //
 // Numerics.  Every state-path product runs on the fp16 matrix cores
-// (v_mfma_f32_32x32x16_f16, fp32 accumulation) with one pass: fp16 keeps 11
-// significant bits, and a CPU simulation of this scheme against an fp64
-// recurrence gives output mean-rel ~3e-4 and state rel ~2.6e-4 at the
-// slow decays of trained checkpoints (bf16 single-pass operands give
-// ~2e-3).  K is L2-normalised (in fp32) before its fp16 conversion, so its
+// (v_mfma_f32_32x32x16_f16, fp32 accumulation): fp16 keeps 11 significant
+// bits, and a CPU simulation of one pass against an fp64 recurrence gives
+// state rel ~2.6e-4 at the slow decays of trained checkpoints (bf16
+// single-pass operands give ~2e-3).  The output's intra-chunk product A Vn,
+// which dominated the one-pass output error (mean-rel ~3e-4), runs as three
+// products Vh A + Vl A + Vh A_lo over the operands' fp16 roundings and
+// residuals (~1e-5).  K is L2-normalised (in fp32) before its fp16 conversion, so its
 // operands lie in [-1, 1]; raw q, v and T, S, Vn must stay below the fp16
 // maximum (65504), far above any trained model's range (1/||q|| is applied
 // to the output rows in fp32).  q k^T and k k^T of the

@@ -684,7 +684,6 @@ def commit_states(s_pool, ids, intermediate_states, accepted):
               _lib.ptr(intermediate_states), _lib.ptr(acc), Bsz, T, Hv, D, _stream(dev))
 
 
-# ------------------------------------------------------------- projections --
 def state_tile_pass(s_pool: torch.Tensor, ids: torch.Tensor) -> None:
     """Measurement pass (no reference counterpart): reads every state tile
     s_pool[ids[b], h] and writes it back unchanged, with the one-token decode
@@ -697,6 +696,7 @@ def state_tile_pass(s_pool: torch.Tensor, ids: torch.Tensor) -> None:
               s_pool.shape[1], s_pool.shape[-1], _stream(dev))
 
 
+# ------------------------------------------------------------- projections --
 def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
            gates: dict | None = None) -> torch.Tensor:
     """F.linear(x, weight) without bias on the bf16 matrix cores (fp32
