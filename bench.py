@@ -399,8 +399,10 @@ def spec_bench(pkg, cfg, dev, K, W):
 def standalone_kernels(pkg, cfg, dev, K, W):
     """The kernels the fused prefill replaces, each launched on its own at
     config 1's shapes (the path the unfused switches select): the gates, the
-    varlen conv, the padded conv (sequences padded to the longest), the gated
-    norm.  Returns {kernel: (average us over K launches, compulsory bytes)}."""
+    varlen conv, the padded conv (sequences padded to the longest; input both
+    [n, C, T] contiguous and the reference's [n, T, C] rows seen as [n, C, T]),
+    the gated norm.  Returns {kernel: (average us over K launches, compulsory
+    bytes)}."""
     N, C, Hv, D = cfg["N"], cfg["C"], cfg["Hv"], cfg["D"]
     lens = cfg["lens"]
     n, T = len(lens), max(lens)
@@ -413,6 +415,11 @@ def standalone_kernels(pkg, cfg, dev, K, W):
     for i, (s0, l) in enumerate(zip(starts.tolist(), lens)):
         xp[i, :, :l] = x[s0:s0 + l].t()
     st_p = torch.zeros(n, C, 3, dtype=BF16, device=dev)
+    # the reference's own padded layout: [n, T, C] rows seen as [n, C, T] (channel stride 1)
+    xt = torch.zeros(n, T, C, dtype=BF16, device=dev)
+    for i, (s0, l) in enumerate(zip(starts.tolist(), lens)):
+        xt[i, :l] = x[s0:s0 + l]
+    st_t = torch.zeros(n, C, 3, dtype=BF16, device=dev)
     endp = lens32 - 1
     core = torch.randn(N, Hv, D, device=dev).to(BF16)
     zz = z.view(N, Hv, D)
@@ -423,6 +430,8 @@ def standalone_kernels(pkg, cfg, dev, K, W):
         "conv_varlen_kernel": (lambda: pkg.ops.causal_conv_silu_varlen_parts(x, st_v, w, lens32, starts, kd),
                                2 * N * C * 2),
         "conv_padded_kernel": (lambda: pkg.ops.causal_conv_silu(xp, st_p, w, endp), 2 * n * C * T * 2),
+        "conv_padded_kernel (channel-stride-1 input)": (lambda: pkg.ops.causal_conv_silu(xt.transpose(1, 2), st_t, w, endp),
+                                                        2 * n * C * T * 2),
         "rmsnorm_gated_kernel": (lambda: pkg.ops.rms_norm_gated(core, zz, nw, 1e-6), 3 * N * Hv * D * 2),
     }
     out = {}

@@ -127,20 +127,35 @@ def test_conv_decode_strided_pool_view(pkg, dev):
     assert torch.equal(full_d.cpu(), exp)
 
 
-def test_conv_padded(pkg, dev):
+@pytest.mark.parametrize("layout,n,C,T", [
+    ("chan", 5, 6144, 100),     # [n, T, C] rows seen as [n, C, T] (the reference's layout)
+    ("chan", 3, 200, 128),      # partial channel tile, 16-byte output stores
+    ("tok", 3, 192, 128),       # [n, C, T] contiguous
+    ("tok", 4, 96, 70),         # T not a multiple of 8 or of the 64-token tile
+    ("generic", 3, 100, 66),    # strides that allow no 16-byte loads
+])
+def test_conv_padded(pkg, dev, layout, n, C, T):
+    """The padded conv (a6) against the oracle for each input layout the kernel
+    loads differently, with end positions at, inside and before the tokens."""
     gen = _gen(16)
-    n, C, T = 5, 6144, 100
-    xm = torch.randn(n, T, C, generator=gen).to(BF16)
-    x = xm.transpose(1, 2)                       # [n, C, T], channel stride 1
+    if layout == "chan":
+        xm = torch.randn(n, T, C, generator=gen).to(BF16)
+        x, xd = xm.transpose(1, 2), xm.to(dev).transpose(1, 2)       # [n, C, T], channel stride 1
+    elif layout == "tok":
+        x = torch.randn(n, C, T, generator=gen).to(BF16)
+        xd = x.to(dev)
+    else:
+        big = torch.randn(n, 2 * C + 1, T + 3, generator=gen).to(BF16)
+        x = big[:, 1::2, 3:]                                        # channel stride 2 (T + 3), token stride 1
+        xd = big.to(dev)[:, 1::2, 3:]
     state = torch.randn(n, C, 3, generator=gen).to(BF16)
     w = (torch.randn(C, 4, generator=gen) * 0.5).to(BF16)
-    endp = [100, 2, -1, 0, 57]
+    endp = ([T, 2, -1, 0, min(57, T)] * 2)[:n]
     ry, rstate = gdn_ref.conv_padded(x, state, w, endp)
     sd = state.to(dev)
-    y = pkg.ops.causal_conv_silu(xm.to(dev).transpose(1, 2), sd, w.to(dev),
-                                 torch.tensor(endp, dtype=torch.int32, device=dev))
+    y = pkg.ops.causal_conv_silu(xd, sd, w.to(dev), torch.tensor(endp, dtype=torch.int32, device=dev))
     assert y.shape == (n, C, T) and y.is_contiguous()
-    assert_out(y.cpu(), ry, "conv padded")
+    assert_out(y.cpu(), ry, f"conv padded {layout}")
     assert torch.equal(sd.cpu(), rstate)
 
 
