@@ -13,13 +13,14 @@
 // k values of one row of A (lane % 32) and of one row of B, so every operand
 // read is one 16-byte LDS read.
 //
-// Tiling: a workgroup of 8 waves computes a 256 x 256 tile of C, K in steps of
-// 64.  Per step the A and B tiles (2 x 32 KiB) go global -> registers -> LDS,
-// double-buffered (128 KiB of LDS): the loads of step s + 1 are issued before
-// the products of step s and written to the other buffer after them, one
-// workgroup barrier per step.  Wave w owns rows 128 (w / 4) .. + 127 and
-// columns 64 (w % 4) .. + 63: 4 x 2 accumulator tiles of 32 x 32 (128 fp32
-// registers), 32 products per step.  LDS rows are 128 bytes with their eight
+// Tiling: a workgroup of 8 waves computes a BM x 256 tile of C (BM = 256, or
+// 192 where that fills the last wave of tiles better), K in steps of 64.  Per
+// step the A and B tiles (BM and 256 rows of 128 bytes) go global -> registers
+// -> LDS, double-buffered (128 KiB of LDS at BM = 256): the loads of step s + 1
+// are issued before the products of step s and written to the other buffer
+// after them, one workgroup barrier per step.  Wave w owns rows BM / 2 (w / 4)
+// .. + BM / 2 - 1 and columns 64 (w % 4) .. + 63: BM / 64 x 2 accumulator tiles
+// of 32 x 32 (at BM = 256: 128 fp32 registers, 32 products per step).  LDS rows are 128 bytes with their eight
 // 16-byte granules XOR-swizzled by (row % 8), so the 8 lanes of each LDS read
 // phase hit 8 distinct granules (all 32 banks).
 //
@@ -39,9 +40,10 @@
 
 namespace {
 
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBN = 256, kBK = 64;  // row tile BM is a template argument: 256 or 192
 constexpr int kGemmThreads = 512;
 constexpr int kGroupM = 4;  // row blocks per tile group
+constexpr int kCUs = 256;   // MI355X compute units: 8 XCDs x 32
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -72,24 +74,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base) {
 // thread; granule id = tid + 512 j: row id / 8, granule id % 8 (8 lanes per
 // 128-byte row).  Rows past M (N) re-read the last row; their results are
 // not stored.
+template <int MI>
 struct StepRegs {
-  u32x4_t a[4], b[4];
+  u32x4_t a[MI], b[4];
 };
 
-__device__ __forceinline__ void load_step(StepRegs& R, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
-                                          const int (&aoff)[4], const int (&boff)[4], int kbyte) {
+template <int MI>
+__device__ __forceinline__ void load_step(StepRegs<MI>& R, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                          const int (&aoff)[MI], const int (&boff)[4], int kbyte) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[j], kbyte, 0);
+  for (int j = 0; j < MI; ++j) R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[j], kbyte, 0);
 #pragma unroll
   for (int j = 0; j < 4; ++j) R.b[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, boff[j], kbyte, 0);
 }
 
-__device__ __forceinline__ void store_step(const StepRegs& R, uint8_t* la, uint8_t* lb, int tid) {
+template <int MI>
+__device__ __forceinline__ void store_step(const StepRegs<MI>& R, uint8_t* la, uint8_t* lb, int tid) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int id = tid + kGemmThreads * j;
     const int off = sw_off(id >> 3, id & 7);
-    *reinterpret_cast<u32x4_t*>(la + off) = R.a[j];
+    if (j < MI) *reinterpret_cast<u32x4_t*>(la + off) = R.a[j];
     *reinterpret_cast<u32x4_t*>(lb + off) = R.b[j];
   }
 }
@@ -101,19 +106,22 @@ __device__ __forceinline__ f32x16_t zero16() {
   return z;
 }
 
-// grid = 8 * ceil(tiles / 8); block = 512.
+// grid = 8 * ceil(tiles / 8); block = 512.  BM / 64 granules of A per thread
+// per step (MI), MI x 2 accumulator tiles per wave.
+template <int BM>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                    const uint16_t* __restrict__ B, int64_t ldb,
                                                                    uint16_t* __restrict__ C, int64_t ldc, int M,
                                                                    int N, int K, GemmGates gt) {
-  // 2 stages x (A, B) tiles of 256 rows x 128 bytes = 128 KiB; the epilogue
-  // reuses it as one [256][256] bf16 tile
-  __shared__ __align__(16) uint8_t smem[4 * kBM * 128];
-  // stage s: A tile at s * 64 KiB, B tile 32 KiB after it
-  auto lds_a = [&](int st) { return smem + st * 2 * kBM * 128; };
-  auto lds_b = [&](int st) { return smem + st * 2 * kBM * 128 + kBM * 128; };
+  constexpr int MI = BM / 64;
+  // 2 stages x (A, B) tiles of BM and 256 rows x 128 bytes (128 KiB for BM =
+  // 256, 112 KiB for 192); the epilogue reuses it as one [BM][256] bf16 tile
+  __shared__ __align__(16) uint8_t smem[2 * (BM + kBN) * 128];
+  // stage s: A tile at s * (BM + 256) * 128 bytes, B tile BM * 128 bytes after it
+  auto lds_a = [&](int st) { return smem + st * (BM + kBN) * 128; };
+  auto lds_b = [&](int st) { return smem + st * (BM + kBN) * 128 + BM * 128; };
 
-  const int mb_n = (M + kBM - 1) / kBM, nb_n = (N + kBN - 1) / kBN;
+  const int mb_n = (M + BM - 1) / BM, nb_n = (N + kBN - 1) / kBN;
   const int64_t tiles = static_cast<int64_t>(mb_n) * nb_n;
   const int64_t L = gdn::xcd_remap(blockIdx.x, tiles);
   if (L < 0) return;
@@ -123,7 +131,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
   const int gm = static_cast<int>(min<int64_t>(kGroupM, mb_n - grp * kGroupM));
   const int mb = static_cast<int>(grp * kGroupM + in_grp % gm);
   const int nb = static_cast<int>(in_grp / gm);
-  const int m0 = mb * kBM, n0 = nb * kBN;
+  const int m0 = mb * BM, n0 = nb * kBN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -131,20 +139,20 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
   const int wm = wave >> 2, wn = wave & 3;
   const int li = lane & 31, lg = lane >> 5;
 
-  // per-thread global byte offsets of its 4 + 4 granules (row clamped)
+  // per-thread global byte offsets of its MI + 4 granules (row clamped)
   const __amdgpu_buffer_rsrc_t ra = rsrc_of(A), rb = rsrc_of(B);
-  int aoff[4], boff[4];
+  int aoff[MI], boff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int id = tid + kGemmThreads * j;
     const int r = id >> 3, c = id & 7;
-    aoff[j] = static_cast<int>((min(m0 + r, M - 1) * lda + 8 * c) * 2);
+    if (j < MI) aoff[j] = static_cast<int>((min(m0 + r, M - 1) * lda + 8 * c) * 2);
     boff[j] = static_cast<int>((min(n0 + r, N - 1) * ldb + 8 * c) * 2);
   }
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
 
@@ -157,21 +165,21 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
   auto products = [&](const uint8_t* la, const uint8_t* lb) {
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      gdn::s16x8_t af[4], bf[2];
+      gdn::s16x8_t af[MI], bf[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const gdn::s16x8_t*>(la + sw_off(128 * wm + 32 * i + li, 2 * ks + lg));
+      for (int i = 0; i < MI; ++i)
+        af[i] = *reinterpret_cast<const gdn::s16x8_t*>(la + sw_off((BM / 2) * wm + 32 * i + li, 2 * ks + lg));
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         bf[j] = *reinterpret_cast<const gdn::s16x8_t*>(lb + sw_off(64 * wn + 32 * j + li, 2 * ks + lg));
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(af[i], bf[j], acc[i][j]);
     }
   };
   auto kb = [&](int st) { return min(st, nk - 1) * kBK * 2; };
-  StepRegs R0, R1;
+  StepRegs<MI> R0, R1;
   load_step(R0, ra, rb, aoff, boff, kb(0));
   gdn::keep_loads_here();
   load_step(R1, ra, rb, aoff, boff, kb(1));
@@ -195,12 +203,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
   __syncthreads();  // the staged tile reuses the buffers; no loads left to keep in flight
 
   // ---- epilogue: bf16 tile through LDS, 16-byte row pieces out ----
-  // wave (wm, wn) stages its 128 x 64 tile at rows 128 wm .., columns 64 wn ..
-  // of a [256][256] bf16 tile (512-byte rows, granules swizzled by row % 32)
+  // wave (wm, wn) stages its BM / 2 x 64 tile at rows BM / 2 wm .., columns
+  // 64 wn .. of a [BM][256] bf16 tile (512-byte rows, granules swizzled by row % 32)
   uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
   auto c_off = [](int r, int c8) { return r * 256 + (((c8) ^ (r & 31)) << 3); };
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int col = 64 * wn + 32 * j + li;
@@ -208,14 +216,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = 128 * wm + 32 * i + 8 * q + 4 * lg + r;
+          const int row = (BM / 2) * wm + 32 * i + 8 * q + 4 * lg + r;
           ct[c_off(row, col >> 3) + (col & 7)] = gdn::f2bf(acc[i][j][4 * q + r]);
         }
     }
   gdn::lds_barrier();
-  // 256 rows x 32 granules = 8192 granules, 16 per thread
+  // BM rows x 32 granules, BM / 16 per thread
 #pragma unroll 4
-  for (int e = tid; e < kBM * (kBN / 8); e += kGemmThreads) {
+  for (int e = tid; e < BM * (kBN / 8); e += kGemmThreads) {
     const int row = e >> 5, c8 = e & 31;
     const int m = m0 + row, n = n0 + 8 * c8;
     if (m >= M || n >= N) continue;
@@ -263,9 +271,22 @@ extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, 
     return GDN_ERR_INVALID_ARG;
   if (g && (!beta || !A_log || !dt_bias || Hv <= 0 || gate_col < 0 || gate_col + 2 * Hv > N)) return GDN_ERR_INVALID_ARG;
   const GemmGates gt{g, beta, A_log, dt_bias, param_is_fp32 ? 1 : 0, gate_col, Hv};
-  const int64_t tiles = static_cast<int64_t>((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  // Row tile: one workgroup per CU, so a launch runs in ceil(tiles / CUs)
+  // waves of tiles, each taking time in proportion to the tile's rows.  The
+  // 192-row tile is taken when its waves x rows is smaller (a short last
+  // wave of 256-row tiles, e.g. 536 tiles = 2.09 waves -> 712 = 2.78).
+  const int64_t nbn = (N + kBN - 1) / kBN;
+  const int64_t t256 = ((M + 255) / 256) * nbn, t192 = ((M + 191) / 192) * nbn;
+  const int64_t w256 = (t256 + kCUs - 1) / kCUs, w192 = (t192 + kCUs - 1) / kCUs;
+  const bool small = w192 * 192 < w256 * 256;
+  const int64_t tiles = small ? t192 : t256;
   const int64_t grid = gdn::kNumXcd * ((tiles + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  gemm_tn_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kGemmThreads), 0, static_cast<hipStream_t>(stream)>>>(
-      A, lda, B, ldb, C, ldc, M, N, K, gt);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (small)
+    gemm_tn_kernel<192><<<dim3(static_cast<unsigned>(grid)), dim3(kGemmThreads), 0, st>>>(A, lda, B, ldb, C, ldc,
+                                                                                         M, N, K, gt);
+  else
+    gemm_tn_kernel<256><<<dim3(static_cast<unsigned>(grid)), dim3(kGemmThreads), 0, st>>>(A, lda, B, ldb, C, ldc,
+                                                                                         M, N, K, gt);
   return gdn_launch_status();
 }

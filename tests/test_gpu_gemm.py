@@ -30,8 +30,14 @@ def _ref(a, w):
     return a.float() @ w.float().t(), a.float().abs() @ w.float().abs().t()
 
 
+# The row tile is 256, or 192 when ceil(tiles / 256 CUs) x rows is smaller
+# with it: every shape below one wave of tiles, and (17000, 2048) = 712 tiles of
+# 192 rows (3 waves) against 536 of 256 (3 waves), take 192; (8190, 2047) is
+# exactly 256 tiles of 256 rows (344 of 192) and (17000, 8224) ties at 9 waves,
+# so both take 256.
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 200, 128), (1, 8224, 2048), (17, 2048, 2048),
-                                   (1000, 2080, 512), (4111, 333, 192)])
+                                   (1000, 2080, 512), (4111, 333, 192), (17000, 2048, 256), (8190, 2047, 128),
+                                   (17000, 8224, 128)])
 def test_gemm_against_fp32_matmul(pkg, dev, M, N, K):
     gen = torch.Generator().manual_seed(M * 7 + N)
     a = torch.randn(M, K, generator=gen).to(BF16)
@@ -55,16 +61,17 @@ def test_gemm_strided_operands_and_out(pkg, dev):
     assert torch.equal(out[:, 8 + N:].cpu(), torch.zeros(M, 32, dtype=BF16))
 
 
-def test_in_proj_with_gate_epilogue(pkg, dev):
+@pytest.mark.parametrize("M", [777, 1790])
+def test_in_proj_with_gate_epilogue(pkg, dev, M):
     """The layer's in_proj over [W_qkv; W_z; W_b; W_a] (config 1 widths, a
     2048 hidden size): the projections, and g / beta from the b and a columns
-    equal to fused_g_beta on them."""
+    equal to fused_g_beta on them.  M = 777 runs 192-row tiles, M = 1790 (231
+    tiles of 256 rows, 330 of 192) 256-row tiles."""
     gen = torch.Generator().manual_seed(6)
     Hk = Hv = 16
     D, hidden = 128, 2048
     C = 2 * Hk * D + Hv * D
     N = C + Hv * D + 2 * Hv
-    M = 777
     x = torch.randn(M, hidden, generator=gen).to(BF16)
     w = (torch.randn(N, hidden, generator=gen) / math.sqrt(hidden)).to(BF16)
     A_log = (torch.rand(Hv, generator=gen) * math.log(16)).to(BF16)
