@@ -10,38 +10,45 @@
 //
 // Both operands are K-contiguous, which is the layout the matrix-core
 // fragments want: a 32x32x16 bf16 product takes from each lane 8 consecutive
-// k values of one row of A (lane % 32) and of one row of B, so every operand
-// read is one 16-byte LDS read.
+// k values of one row of each operand, so every operand read is one 16-byte
+// LDS read.
 //
-// Tiling: a workgroup of 8 waves computes a BM x 256 tile of C (BM = 256, or
-// 192 where that fills the last wave of tiles better), K in steps of 64.  Per
-// step the A and B tiles (BM and 256 rows of 128 bytes) go global -> registers
-// -> LDS, double-buffered (128 KiB of LDS at BM = 256): the loads of step s + 1
-// are issued before the products of step s and written to the other buffer
-// after them, one workgroup barrier per step.  Wave w owns rows BM / 2 (w / 4)
-// .. + BM / 2 - 1 and columns 64 (w % 4) .. + 63: BM / 64 x 2 accumulator tiles
-// of 32 x 32 (at BM = 256: 128 fp32 registers, 32 products per step).  LDS rows are 128 bytes with their eight
-// 16-byte granules XOR-swizzled by (row % 8), so the 8 lanes of each LDS read
-// phase hit 8 distinct granules (all 32 banks).
+// Tiling: a workgroup of 4 waves (one per SIMD, one workgroup per CU)
+// computes a BM x 256 tile of C (BM = 256, or 192 where that fills the last
+// wave of tiles better), K in steps of 64.  Wave (wm, wn) owns rows BM / 2 wm
+// .. and columns 128 wn ..: BM / 64 x 4 accumulator tiles of 32 x 32 (256
+// registers at BM = 256, kept in AGPRs), 64 products per step.
+//
+// Operand path: global -> LDS directly (buffer_load ... lds, no registers),
+// two stages of BM + 256 rows x 128 bytes (128 KiB at BM = 256).  The loads
+// of step s + 1 are spread one per product over the first half of step s (a
+// burst stalls the waves on the shared address unit).  Operand fragments
+// are read one 16-deep sub-step ahead of their products, interleaved one read
+// per product.  One workgroup barrier per step, placed before the last
+// sub-step's products so the next stage's first reads overlap them.  LDS
+// rows have their eight 16-byte granules XOR-swizzled by (row / 2) % 8, which
+// makes the fragment reads free of bank conflicts (measured: zero).
 //
 // Tile order: consecutive workgroups run on different XCDs (workgroup b on
 // XCD b % 8); the tiles are renumbered so that each XCD walks a contiguous
 // range in groups of 4 row blocks x all column blocks, and the tiles resident
 // on one XCD at a time share A row blocks and B column blocks in its L2.
 //
-// Epilogue: the accumulators are rounded to bf16 and staged through LDS so
-// each row goes out in 16-byte pieces.  With gate outputs (GemmGates) the
-// columns [gate_col, gate_col + Hv) are the b projection and [gate_col + Hv,
-// gate_col + 2 Hv) the a projection: besides their bf16 values, beta =
-// sigmoid(b) (bf16) and g = -exp(A_log) softplus(a + dt_bias) (fp32) are
-// written from the bf16-rounded values with the gate kernel's arithmetic
-// (gdn::gate_beta, gdn::gate_g), so they equal gdn_g_beta applied to C.
+// Epilogue: the products take B as the first operand, so they are tiles of
+// C^T and each lane holds runs of 4 consecutive columns of one row; a lane
+// swap (v_permlane32_swap) makes them runs of 8, stored as 16-byte pieces
+// straight from the registers.  With gate outputs (GemmGates) the columns
+// [gate_col, gate_col + Hv) are the b projection and [gate_col + Hv, gate_col
+// + 2 Hv) the a projection: besides their bf16 values, beta = sigmoid(b)
+// (bf16) and g = -exp(A_log) softplus(a + dt_bias) (fp32) are written from the
+// bf16-rounded values with the gate kernel's arithmetic (gdn::gate_beta,
+// gdn::gate_g), so they equal gdn_g_beta applied to C.
 #include "gdn_common.h"
 
 namespace {
 
 constexpr int kBN = 256, kBK = 64;  // row tile BM is a template argument: 256 or 192
-constexpr int kGemmThreads = 512;
+constexpr int kGemmThreads = 256;
 constexpr int kGroupM = 4;  // row blocks per tile group
 constexpr int kCUs = 256;   // MI355X compute units: 8 XCDs x 32
 
@@ -58,8 +65,12 @@ struct GemmGates {
   int Hv;
 };
 
-// byte offset of granule c (16 bytes) of row r in a 128-byte-row LDS tile
-__device__ __forceinline__ int sw_off(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// Byte offset of granule c (16 bytes) of row r in a 128-byte-row LDS tile.
+// Granules are XOR-swizzled by (r / 2) % 8: a 16-byte read serves 16 lanes
+// at a time from 256 bytes of banks (two rows), and the 16 lanes of a
+// fragment read (16 consecutive rows, one granule) then hit 16 distinct
+// 16-byte bank groups.
+__device__ __forceinline__ int sw_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
 __device__ __forceinline__ f32x16_t mfma_bf16(const gdn::s16x8_t& a, const gdn::s16x8_t& b, const f32x16_t& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gdn::bf16x8_t, a),
@@ -70,33 +81,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), 0x7fffffff, 0x00020000);
 }
 
-// Global -> register loads of one K step: 4 granules of A and 4 of B per
-// thread; granule id = tid + 512 j: row id / 8, granule id % 8 (8 lanes per
-// 128-byte row).  Rows past M (N) re-read the last row; their results are
-// not stored.
-template <int MI>
-struct StepRegs {
-  u32x4_t a[MI], b[4];
-};
+// Direct-to-LDS loads: one buffer_load_dwordx4 ... lds moves 64 lanes x 16
+// bytes into the 1 KiB of LDS at M0 + 16 lane.  A stage holds the A tile (BM
+// rows) then the B tile (256 rows), 128 bytes a row: 1 KiB block b is tile rows
+// 8 b' .. 8 b' + 7 (b' = b for A, b - BM / 8 for B; BM / 8 is even).  Lane l
+// fills row 8 b' + l / 8, slot l % 8, which under the swizzle holds the row's
+// global granule (l % 8) ^ (4 (b % 2) + l / 16).  Wave w loads blocks w,
+// w + 4, w + 8, ...
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int MI>
-__device__ __forceinline__ void load_step(StepRegs<MI>& R, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
-                                          const int (&aoff)[MI], const int (&boff)[4], int kbyte) {
-#pragma unroll
-  for (int j = 0; j < MI; ++j) R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[j], kbyte, 0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) R.b[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, boff[j], kbyte, 0);
-}
-
-template <int MI>
-__device__ __forceinline__ void store_step(const StepRegs<MI>& R, uint8_t* la, uint8_t* lb, int tid) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int id = tid + kGemmThreads * j;
-    const int off = sw_off(id >> 3, id & 7);
-    if (j < MI) *reinterpret_cast<u32x4_t*>(la + off) = R.a[j];
-    *reinterpret_cast<u32x4_t*>(lb + off) = R.b[j];
-  }
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint8_t* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
 }
 
 __device__ __forceinline__ f32x16_t zero16() {
@@ -106,20 +101,22 @@ __device__ __forceinline__ f32x16_t zero16() {
   return z;
 }
 
-// grid = 8 * ceil(tiles / 8); block = 512.  BM / 64 granules of A per thread
-// per step (MI), MI x 2 accumulator tiles per wave.
+// grid = 8 * ceil(tiles / 8); block = 256 (4 waves, 2 x 2 over the tile).
+// Wave (wm, wn) owns rows BM / 2 wm .. and columns 128 wn ..: MI x 4
+// accumulator tiles of 32 x 32 (MI = BM / 64).
 template <int BM>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                    const uint16_t* __restrict__ B, int64_t ldb,
                                                                    uint16_t* __restrict__ C, int64_t ldc, int M,
                                                                    int N, int K, GemmGates gt) {
   constexpr int MI = BM / 64;
-  // 2 stages x (A, B) tiles of BM and 256 rows x 128 bytes (128 KiB for BM =
-  // 256, 112 KiB for 192); the epilogue reuses it as one [BM][256] bf16 tile
-  __shared__ __align__(16) uint8_t smem[2 * (BM + kBN) * 128];
-  // stage s: A tile at s * (BM + 256) * 128 bytes, B tile BM * 128 bytes after it
-  auto lds_a = [&](int st) { return smem + st * (BM + kBN) * 128; };
-  auto lds_b = [&](int st) { return smem + st * (BM + kBN) * 128 + BM * 128; };
+  constexpr int kStage = (BM + kBN) * 128;  // bytes per stage: 64 KiB at BM = 256, 56 KiB at 192
+  constexpr int kPer = (BM + kBN) / 32;     // 1 KiB blocks per wave per stage
+  constexpr int kAPer = BM / 32;            // of which A blocks (the first kAPer)
+  // two stages as two objects, so the compiler sees that products from one
+  // do not read what the loads into the other write
+  __shared__ __align__(16) uint8_t st0[kStage];
+  __shared__ __align__(16) uint8_t st1[kStage];
 
   const int mb_n = (M + BM - 1) / BM, nb_n = (N + kBN - 1) / kBN;
   const int64_t tiles = static_cast<int64_t>(mb_n) * nb_n;
@@ -136,118 +133,182 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, lg = lane >> 5;
 
-  // per-thread global byte offsets of its MI + 4 granules (row clamped)
+  // per-lane global byte offsets of the wave's kPer blocks (rows clamped:
+  // rows past M (N) re-read the last row; their results are not stored)
   const __amdgpu_buffer_rsrc_t ra = rsrc_of(A), rb = rsrc_of(B);
-  int aoff[MI], boff[4];
+  int goff[kPer];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int id = tid + kGemmThreads * j;
-    const int r = id >> 3, c = id & 7;
-    if (j < MI) aoff[j] = static_cast<int>((min(m0 + r, M - 1) * lda + 8 * c) * 2);
-    boff[j] = static_cast<int>((min(n0 + r, N - 1) * ldb + 8 * c) * 2);
+  for (int i = 0; i < kPer; ++i) {
+    const int b = wave + 4 * i;
+    const int gcol = 8 * ((lane & 7) ^ (((b & 1) << 2) | (lane >> 4)));
+    if (i < kAPer) {
+      goff[i] = static_cast<int>((min(m0 + 8 * b + (lane >> 3), M - 1) * lda + gcol) * 2);
+    } else {
+      goff[i] = static_cast<int>((min(n0 + 8 * (b - BM / 8) + (lane >> 3), N - 1) * ldb + gcol) * 2);
+    }
   }
+  const int nk = K / kBK;
+  // the wave's blocks i0 .. i0 + n - 1 of step `step` (clamped to the last
+  // step: the loads after the last step repeat it into the unused stage)
+  auto issue = [&](uint8_t* st, int step, int i0, int n) {
+    const int kbyte = min(step, nk - 1) * kBK * 2;
+#pragma unroll
+    for (int i = i0; i < i0 + n; ++i) dma16(i < kAPer ? ra : rb, st + (wave + 4 * i) * 1024, goff[i], kbyte);
+  };
 
-  f32x16_t acc[MI][2];
+  f32x16_t acc[MI][4];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+    for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
 
-  // Step s's tiles are loaded into register set s % 2 two steps ahead (so a
-  // load has two steps of products to arrive), written to LDS buffer s % 2
-  // at the end of step s - 1, and read there in step s.  Every path issues
-  // the same loads (indices past the last step repeat it) so the compiler's
-  // load counters stay exact; the loop runs two steps per trip.
-  const int nk = K / kBK;
-  auto products = [&](const uint8_t* la, const uint8_t* lb) {
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      gdn::s16x8_t af[MI], bf[2];
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-        af[i] = *reinterpret_cast<const gdn::s16x8_t*>(la + sw_off((BM / 2) * wm + 32 * i + li, 2 * ks + lg));
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const gdn::s16x8_t*>(lb + sw_off(64 * wn + 32 * j + li, 2 * ks + lg));
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16(af[i], bf[j], acc[i][j]);
-    }
+  // Operand fragments of one 16-deep sub-step: MI of A, 4 of B (one 16-byte
+  // LDS read each).  Fragments are read one sub-step ahead of their
+  // products, so each read has 16 products' time (512 cycles) to arrive.
+  struct Frag {
+    gdn::s16x8_t a[MI], b[4];
   };
-  auto kb = [&](int st) { return min(st, nk - 1) * kBK * 2; };
-  StepRegs<MI> R0, R1;
-  load_step(R0, ra, rb, aoff, boff, kb(0));
-  gdn::keep_loads_here();
-  load_step(R1, ra, rb, aoff, boff, kb(1));
-  gdn::keep_loads_here();
-  store_step(R0, lds_a(0), lds_b(0), tid);
-  gdn::lds_barrier();
+  auto read_frag = [&](const uint8_t* st, int ks, Frag& f) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+      f.a[i] = *reinterpret_cast<const gdn::s16x8_t*>(st + sw_off((BM / 2) * wm + 32 * i + li, 2 * ks + lg));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      f.b[j] = *reinterpret_cast<const gdn::s16x8_t*>(st + BM * 128 + sw_off(128 * wn + 32 * j + li, 2 * ks + lg));
+  };
+  // B as the first operand: the product is the tile of C^T, so each lane's
+  // four consecutive accumulator registers are four consecutive columns of
+  // one row of C (stored as one 8-byte piece)
+  auto mfmas = [&](const Frag& f) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(f.b[j], f.a[i], acc[i][j]);
+  };
+  // One sub-step's products with the next sub-step's reads between them.
+  auto overlap = [&](const Frag& f, const uint8_t* st, int ks, Frag& nf) {
+    read_frag(st, ks, nf);
+    mfmas(f);
+#pragma unroll
+    for (int r = 0; r < MI + 4; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, MI * 4 - (MI + 4), 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // The same with half of the wave's loads of step `ld` into `dst` as well
+  // (kPer / 2 = MI + 4 of them, one after each of the first products).  A
+  // burst of loads stalls the wave (the address unit takes 1 KiB per 16
+  // cycles, and four waves share it), so they are spread over the products.
+  auto overlap_ld = [&](const Frag& f, const uint8_t* st, int ks, Frag& nf, uint8_t* dst, int ld, int i0) {
+    read_frag(st, ks, nf);
+    issue(dst, ld, i0, kPer / 2);
+    mfmas(f);
+#pragma unroll
+    for (int r = 0; r < MI + 4; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, MI * 4 - (MI + 4), 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Step s (4 sub-steps) is multiplied from stage s % 2 while step s + 1 is
+  // loaded into the other stage (during its first two sub-steps).  The barrier comes once the step's last
+  // fragments are read (before their products): it waits for the wave's own
+  // loads first, so after it the next stage is complete for every wave and
+  // no wave reads the current stage any more (the loads of step s + 2 may
+  // overwrite it).  The next step's first fragments are read behind the last
+  // sub-step's products (no branch on the accumulators' path: a branch there
+  // makes the compiler copy them and spill).
+  Frag f0, f1;
+  auto step = [&](uint8_t* cur, uint8_t* nxt, int s) {
+    overlap_ld(f0, cur, 1, f1, nxt, s + 1, 0);
+    overlap_ld(f1, cur, 2, f0, nxt, s + 1, kPer / 2);
+    overlap(f0, cur, 3, f1);
+    __syncthreads();
+    overlap(f1, nxt, 0, f0);  // after the last step these reads go unused
+  };
+  issue(st0, 0, 0, kPer);
+  __syncthreads();
+  read_frag(st0, 0, f0);
   int s = 0;
   for (; s + 1 < nk; s += 2) {
-    load_step(R0, ra, rb, aoff, boff, kb(s + 2));     // step s + 2 (set 0 was written out)
-    gdn::keep_loads_here();
-    products(lds_a(0), lds_b(0));                      // step s
-    store_step(R1, lds_a(1), lds_b(1), tid);           // step s + 1
-    gdn::lds_barrier();
-    load_step(R1, ra, rb, aoff, boff, kb(s + 3));     // step s + 3
-    gdn::keep_loads_here();
-    products(lds_a(1), lds_b(1));                      // step s + 1
-    if (s + 2 < nk) store_step(R0, lds_a(0), lds_b(0), tid);  // step s + 2
-    gdn::lds_barrier();
+    step(st0, st1, s);
+    step(st1, st0, s + 1);
   }
-  if (s < nk) products(lds_a(0), lds_b(0));            // the last step when nk is odd
-  __syncthreads();  // the staged tile reuses the buffers; no loads left to keep in flight
-
-  // ---- epilogue: bf16 tile through LDS, 16-byte row pieces out ----
-  // wave (wm, wn) stages its BM / 2 x 64 tile at rows BM / 2 wm .., columns
-  // 64 wn .. of a [BM][256] bf16 tile (512-byte rows, granules swizzled by row % 32)
-  uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
-  auto c_off = [](int r, int c8) { return r * 256 + (((c8) ^ (r & 31)) << 3); };
+  if (s < nk) step(st0, st1, s);  // the last step when nk is odd
+  // ---- epilogue: straight from the accumulators ----
+  // acc[i][j] register 4 q + r of lane (li, lg) is C[row][col + r] with row =
+  // m0 + BM / 2 wm + 32 i + li, col = n0 + 128 wn + 32 j + 8 q + 4 lg.  One
+  // swap between lanes l and l + 32 (v_permlane32_swap: the upper half of the
+  // first operand with the lower half of the second) leaves lane (li, lg)
+  // columns 16 p + 8 lg .. + 7 of pair p = (q 2p, q 2p + 1) in bf16: one
+  // 16-byte store per pair, two lanes filling 32 bytes of a row.
+  const bool vec = ldc % 8 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0;
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+  for (int i = 0; i < MI; ++i) {
+    const int m = m0 + (BM / 2) * wm + 32 * i + li;
+    const bool row_ok = m < M;  // (no early exit: the gate loop below spans every lane)
+    uint16_t* crow = C + static_cast<int64_t>(row_ok ? m : 0) * ldc;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = 64 * wn + 32 * j + li;
+    for (int j = 0; j < 4; ++j) {
+      const int cb = n0 + 128 * wn + 32 * j;  // wave-uniform
+      if (cb >= N) continue;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = (BM / 2) * wm + 32 * i + 8 * q + 4 * lg + r;
-          ct[c_off(row, col >> 3) + (col & 7)] = gdn::f2bf(acc[i][j][4 * q + r]);
-        }
-    }
-  gdn::lds_barrier();
-  // BM rows x 32 granules, BM / 16 per thread
-#pragma unroll 4
-  for (int e = tid; e < BM * (kBN / 8); e += kGemmThreads) {
-    const int row = e >> 5, c8 = e & 31;
-    const int m = m0 + row, n = n0 + 8 * c8;
-    if (m >= M || n >= N) continue;
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ct + c_off(row, c8));
-    uint16_t* cp = C + static_cast<int64_t>(m) * ldc + n;
-    if (n + 8 <= N && ldc % 8 == 0) {
-      *reinterpret_cast<u32x4_t*>(cp) = v;
-    } else {
-      const uint16_t* vs = reinterpret_cast<const uint16_t*>(&v);
-      for (int t = 0; t < min(8, N - n); ++t) cp[t] = vs[t];
-    }
-    if (gt.g && n + 8 > gt.gate_col && n < gt.gate_col + 2 * gt.Hv) {
-      const uint16_t* vs = reinterpret_cast<const uint16_t*>(&v);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int col = n + t - gt.gate_col;
-        if (col < 0 || col >= 2 * gt.Hv || n + t >= N) continue;
-        if (col < gt.Hv) {
-          gt.beta[static_cast<int64_t>(m) * gt.Hv + col] = gdn::gate_beta(gdn::bf2f(vs[t]));
+      for (int p = 0; p < 2; ++p) {
+        const int q = 2 * p;
+        const auto lo = __builtin_amdgcn_permlane32_swap(gdn::f2bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                                         gdn::f2bf2(acc[i][j][4 * q + 4], acc[i][j][4 * q + 5]),
+                                                         false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(gdn::f2bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]),
+                                                         gdn::f2bf2(acc[i][j][4 * q + 6], acc[i][j][4 * q + 7]),
+                                                         false, false);
+        const uint32_t w[4] = {lo[0], hi[0], lo[1], hi[1]};  // columns n .. n + 7
+        const int n = cb + 16 * p + 8 * lg;
+        if (!row_ok) {
+        } else if (vec && n + 8 <= N) {
+          *reinterpret_cast<uint4*>(crow + n) = make_uint4(w[0], w[1], w[2], w[3]);
         } else {
-          const int h = col - gt.Hv;
-          gt.g[static_cast<int64_t>(m) * gt.Hv + h] =
-              gdn::gate_g(gdn::bf2f(vs[t]), gdn::load_param(gt.A_log, h, gt.param_f32),
-                          gdn::load_param(gt.dt_bias, h, gt.param_f32));
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            if (n + t < N) crow[n + t] = static_cast<uint16_t>(w[t / 2] >> (16 * (t % 2)));
+        }
+      }
+      // Gate outputs from the bf16-rounded b and a columns of this 32-column
+      // block.  The block's values go through the wave's own 8 KiB of the
+      // stage the last step no longer reads (wave-local, in order), and a
+      // rolled loop computes beta and g (unrolled over the registers, the gate
+      // arithmetic would not fit beside the accumulators).
+      if (gt.g && cb + 32 > gt.gate_col && cb < gt.gate_col + 2 * gt.Hv) {
+        uint16_t* gs = reinterpret_cast<uint16_t*>(nk % 2 ? st0 : st1) + wave * (BM / 2) * 32;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = gdn::f2bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+          const uint32_t hi = gdn::f2bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          *reinterpret_cast<uint2*>(gs + 32 * (32 * i + li) + 8 * q + 4 * lg) = make_uint2(lo, hi);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll 1
+        for (int e = lane; e < 32 * 32; e += 64) {
+          const int r = e >> 5, c = e & 31;
+          const int mm = m - li + r, n = cb + c, col = n - gt.gate_col;
+          if (mm >= M || n >= N || col < 0 || col >= 2 * gt.Hv) continue;
+          const float v = gdn::bf2f(gs[32 * (32 * i + r) + c]);
+          if (col < gt.Hv) {
+            gt.beta[static_cast<int64_t>(mm) * gt.Hv + col] = gdn::gate_beta(v);
+          } else {
+            const int h = col - gt.Hv;
+            gt.g[static_cast<int64_t>(mm) * gt.Hv + h] =
+                gdn::gate_g(v, gdn::load_param(gt.A_log, h, gt.param_f32), gdn::load_param(gt.dt_bias, h, gt.param_f32));
+          }
         }
       }
     }

@@ -47,18 +47,21 @@ def test_gemm_against_fp32_matmul(pkg, dev, M, N, K):
     _check(c, ref, sc, f"gemm {M}x{N}x{K}")
 
 
-def test_gemm_strided_operands_and_out(pkg, dev):
-    """Row strides larger than K (views of wider buffers) and an output view."""
+@pytest.mark.parametrize("pad,off", [(40, 8), (41, 3)])
+def test_gemm_strided_operands_and_out(pkg, dev, pad, off):
+    """Row strides larger than K (views of wider buffers) and an output view;
+    pad 41 / offset 3 gives an output row stride that is not a multiple of 4
+    and rows at 2-byte alignment (element-by-element stores)."""
     gen = torch.Generator().manual_seed(5)
     M, N, K = 333, 264, 256
     abuf = torch.randn(M, K + 64, generator=gen).to(BF16)
     wbuf = (torch.randn(N, K + 128, generator=gen) / 16).to(BF16)
     a, w = abuf[:, 32:32 + K], wbuf[:, :K]
-    out = torch.zeros(M, N + 40, dtype=BF16, device=dev)
-    pkg.ops.linear(abuf.to(dev)[:, 32:32 + K], wbuf.to(dev)[:, :K], out=out[:, 8:8 + N])
-    _check(out[:, 8:8 + N], *_ref(a, w), "strided gemm")
-    assert torch.equal(out[:, :8].cpu(), torch.zeros(M, 8, dtype=BF16))
-    assert torch.equal(out[:, 8 + N:].cpu(), torch.zeros(M, 32, dtype=BF16))
+    out = torch.zeros(M, N + pad, dtype=BF16, device=dev)
+    pkg.ops.linear(abuf.to(dev)[:, 32:32 + K], wbuf.to(dev)[:, :K], out=out[:, off:off + N])
+    _check(out[:, off:off + N], *_ref(a, w), "strided gemm")
+    assert torch.equal(out[:, :off].cpu(), torch.zeros(M, off, dtype=BF16))
+    assert torch.equal(out[:, off + N:].cpu(), torch.zeros(M, pad - off, dtype=BF16))
 
 
 @pytest.mark.parametrize("M", [777, 1790])
