@@ -47,7 +47,7 @@
 
 namespace {
 
-constexpr int kBN = 256, kBK = 64;  // row tile BM is a template argument: 256 or 192
+constexpr int kBK = 64;  // the tile (BM x BN) is a template argument
 constexpr int kGemmThreads = 256;
 constexpr int kGroupM = 4;  // row blocks per tile group
 constexpr int kCUs = 256;   // MI355X compute units: 8 XCDs x 32
@@ -102,23 +102,26 @@ __device__ __forceinline__ f32x16_t zero16() {
 }
 
 // grid = 8 * ceil(tiles / 8); block = 256 (4 waves, 2 x 2 over the tile).
-// Wave (wm, wn) owns rows BM / 2 wm .. and columns 128 wn ..: MI x 4
-// accumulator tiles of 32 x 32 (MI = BM / 64).
-template <int BM>
-__global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
+// Wave (wm, wn) owns rows BM / 2 wm .. and columns BN / 2 wn ..: MI x NJ
+// accumulator tiles of 32 x 32 (MI = BM / 64, NJ = BN / 64).  kMinWG
+// workgroups per CU bound the registers (1: 512 per lane, AGPRs included).
+template <int BM, int BN, int kMinWG>
+__global__ __launch_bounds__(kGemmThreads, kMinWG) void gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                    const uint16_t* __restrict__ B, int64_t ldb,
                                                                    uint16_t* __restrict__ C, int64_t ldc, int M,
                                                                    int N, int K, GemmGates gt) {
-  constexpr int MI = BM / 64;
-  constexpr int kStage = (BM + kBN) * 128;  // bytes per stage: 64 KiB at BM = 256, 56 KiB at 192
-  constexpr int kPer = (BM + kBN) / 32;     // 1 KiB blocks per wave per stage
-  constexpr int kAPer = BM / 32;            // of which A blocks (the first kAPer)
+  constexpr int MI = BM / 64, NJ = BN / 64;
+  constexpr int kStage = (BM + BN) * 128;  // bytes per stage: 64 KiB at 256 x 256
+  constexpr int kPer = (BM + BN) / 32;     // 1 KiB blocks per wave per stage (= 2 (MI + NJ))
+  constexpr int kAPer = BM / 32;           // of which A blocks (the first kAPer)
+  constexpr int kReads = MI + NJ, kProds = MI * NJ;  // fragment reads, products per sub-step
+  constexpr int kPair = kReads < kProds ? kReads : kProds;
   // two stages as two objects, so the compiler sees that products from one
   // do not read what the loads into the other write
   __shared__ __align__(16) uint8_t st0[kStage];
   __shared__ __align__(16) uint8_t st1[kStage];
 
-  const int mb_n = (M + BM - 1) / BM, nb_n = (N + kBN - 1) / kBN;
+  const int mb_n = (M + BM - 1) / BM, nb_n = (N + BN - 1) / BN;
   const int64_t tiles = static_cast<int64_t>(mb_n) * nb_n;
   const int64_t L = gdn::xcd_remap(blockIdx.x, tiles);
   if (L < 0) return;
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
   const int gm = static_cast<int>(min<int64_t>(kGroupM, mb_n - grp * kGroupM));
   const int mb = static_cast<int>(grp * kGroupM + in_grp % gm);
   const int nb = static_cast<int>(in_grp / gm);
-  const int m0 = mb * BM, n0 = nb * kBN;
+  const int m0 = mb * BM, n0 = nb * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -159,25 +162,26 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
     for (int i = i0; i < i0 + n; ++i) dma16(i < kAPer ? ra : rb, st + (wave + 4 * i) * 1024, goff[i], kbyte);
   };
 
-  f32x16_t acc[MI][4];
+  f32x16_t acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
+    for (int j = 0; j < NJ; ++j) acc[i][j] = zero16();
 
-  // Operand fragments of one 16-deep sub-step: MI of A, 4 of B (one 16-byte
+  // Operand fragments of one 16-deep sub-step: MI of A, NJ of B (one 16-byte
   // LDS read each).  Fragments are read one sub-step ahead of their
-  // products, so each read has 16 products' time (512 cycles) to arrive.
+  // products, so each read has a sub-step of products (512 cycles at 256 x
+  // 256) to arrive.
   struct Frag {
-    gdn::s16x8_t a[MI], b[4];
+    gdn::s16x8_t a[MI], b[NJ];
   };
   auto read_frag = [&](const uint8_t* st, int ks, Frag& f) {
 #pragma unroll
     for (int i = 0; i < MI; ++i)
       f.a[i] = *reinterpret_cast<const gdn::s16x8_t*>(st + sw_off((BM / 2) * wm + 32 * i + li, 2 * ks + lg));
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      f.b[j] = *reinterpret_cast<const gdn::s16x8_t*>(st + BM * 128 + sw_off(128 * wn + 32 * j + li, 2 * ks + lg));
+    for (int j = 0; j < NJ; ++j)
+      f.b[j] = *reinterpret_cast<const gdn::s16x8_t*>(st + BM * 128 + sw_off((BN / 2) * wn + 32 * j + li, 2 * ks + lg));
   };
   // B as the first operand: the product is the tile of C^T, so each lane's
   // four consecutive accumulator registers are four consecutive columns of
@@ -186,22 +190,23 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(f.b[j], f.a[i], acc[i][j]);
+      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma_bf16(f.b[j], f.a[i], acc[i][j]);
   };
   // One sub-step's products with the next sub-step's reads between them.
   auto overlap = [&](const Frag& f, const uint8_t* st, int ks, Frag& nf) {
     read_frag(st, ks, nf);
     mfmas(f);
 #pragma unroll
-    for (int r = 0; r < MI + 4; ++r) {
+    for (int r = 0; r < kPair; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, MI * 4 - (MI + 4), 0);
+    if (kProds > kPair) __builtin_amdgcn_sched_group_barrier(0x008, kProds - kPair, 0);
+    if (kReads > kPair) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPair, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
   // The same with half of the wave's loads of step `ld` into `dst` as well
-  // (kPer / 2 = MI + 4 of them, one after each of the first products).  A
+  // (kPer / 2 = MI + NJ of them, one after each of the first products).  A
   // burst of loads stalls the wave (the address unit takes 1 KiB per 16
   // cycles, and four waves share it), so they are spread over the products.
   auto overlap_ld = [&](const Frag& f, const uint8_t* st, int ks, Frag& nf, uint8_t* dst, int ld, int i0) {
@@ -209,12 +214,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
     issue(dst, ld, i0, kPer / 2);
     mfmas(f);
 #pragma unroll
-    for (int r = 0; r < MI + 4; ++r) {
+    for (int r = 0; r < kPair; ++r) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one product
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, MI * 4 - (MI + 4), 0);
+    if (kProds > kPair) __builtin_amdgcn_sched_group_barrier(0x008, kProds - kPair, 0);
+    if (kReads > kPair) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPair, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, kReads - kPair, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -245,7 +254,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
   if (s < nk) step(st0, st1, s);  // the last step when nk is odd
   // ---- epilogue: straight from the accumulators ----
   // acc[i][j] register 4 q + r of lane (li, lg) is C[row][col + r] with row =
-  // m0 + BM / 2 wm + 32 i + li, col = n0 + 128 wn + 32 j + 8 q + 4 lg.  One
+  // m0 + BM / 2 wm + 32 i + li, col = n0 + BN / 2 wn + 32 j + 8 q + 4 lg.  One
   // swap between lanes l and l + 32 (v_permlane32_swap: the upper half of the
   // first operand with the lower half of the second) leaves lane (li, lg)
   // columns 16 p + 8 lg .. + 7 of pair p = (q 2p, q 2p + 1) in bf16: one
@@ -257,8 +266,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_tn_kernel(const uint16_t
     const bool row_ok = m < M;  // (no early exit: the gate loop below spans every lane)
     uint16_t* crow = C + static_cast<int64_t>(row_ok ? m : 0) * ldc;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int cb = n0 + 128 * wn + 32 * j;  // wave-uniform
+    for (int j = 0; j < NJ; ++j) {
+      const int cb = n0 + (BN / 2) * wn + 32 * j;  // wave-uniform
       if (cb >= N) continue;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
@@ -332,22 +341,26 @@ extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, 
     return GDN_ERR_INVALID_ARG;
   if (g && (!beta || !A_log || !dt_bias || Hv <= 0 || gate_col < 0 || gate_col + 2 * Hv > N)) return GDN_ERR_INVALID_ARG;
   const GemmGates gt{g, beta, A_log, dt_bias, param_is_fp32 ? 1 : 0, gate_col, Hv};
-  // Row tile: one workgroup per CU, so a launch runs in ceil(tiles / CUs)
-  // waves of tiles, each taking time in proportion to the tile's rows.  The
-  // 192-row tile is taken when its waves x rows is smaller (a short last
-  // wave of 256-row tiles, e.g. 536 tiles = 2.09 waves -> 712 = 2.78).
-  const int64_t nbn = (N + kBN - 1) / kBN;
-  const int64_t t256 = ((M + 255) / 256) * nbn, t192 = ((M + 191) / 192) * nbn;
+  // Tile: 256 x 256 with one workgroup per CU, so a launch runs in
+  // ceil(tiles / CUs) waves of tiles, each taking time in proportion to the
+  // tile's rows.  192 x 256 is taken when its waves x rows is smaller (a
+  // short last wave of 256-row tiles, e.g. 536 tiles = 2.09 waves -> 712 =
+  // 2.78).  When 256 x 256 tiles would not fill half of the CUs (small M:
+  // decode batches), 64 x 128 tiles, two or more workgroups per CU, spread
+  // the work over the whole chip.
+  const int64_t nb256 = (N + 255) / 256;
+  const int64_t t256 = ((M + 255) / 256) * nb256, t192 = ((M + 191) / 192) * nb256;
   const int64_t w256 = (t256 + kCUs - 1) / kCUs, w192 = (t192 + kCUs - 1) / kCUs;
-  const bool small = w192 * 192 < w256 * 256;
-  const int64_t tiles = small ? t192 : t256;
+  const int cfg = t256 < kCUs / 2 ? 2 : (w192 * 192 < w256 * 256 ? 1 : 0);
+  const int64_t tiles = cfg == 2 ? ((M + 63) / 64) * ((N + 127) / 128) : cfg == 1 ? t192 : t256;
   const int64_t grid = gdn::kNumXcd * ((tiles + gdn::kNumXcd - 1) / gdn::kNumXcd);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  if (small)
-    gemm_tn_kernel<192><<<dim3(static_cast<unsigned>(grid)), dim3(kGemmThreads), 0, st>>>(A, lda, B, ldb, C, ldc,
-                                                                                         M, N, K, gt);
+  const dim3 g3(static_cast<unsigned>(grid)), b3(kGemmThreads);
+  if (cfg == 2)
+    gemm_tn_kernel<64, 128, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+  else if (cfg == 1)
+    gemm_tn_kernel<192, 256, 1><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
   else
-    gemm_tn_kernel<256><<<dim3(static_cast<unsigned>(grid)), dim3(kGemmThreads), 0, st>>>(A, lda, B, ldb, C, ldc,
-                                                                                         M, N, K, gt);
+    gemm_tn_kernel<256, 256, 1><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
   return gdn_launch_status();
 }

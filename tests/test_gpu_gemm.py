@@ -30,11 +30,12 @@ def _ref(a, w):
     return a.float() @ w.float().t(), a.float().abs() @ w.float().abs().t()
 
 
-# The row tile is 256, or 192 when ceil(tiles / 256 CUs) x rows is smaller
-# with it: every shape below one wave of tiles, and (17000, 2048) = 712 tiles of
-# 192 rows (3 waves) against 536 of 256 (3 waves), take 192; (8190, 2047) is
-# exactly 256 tiles of 256 rows (344 of 192) and (17000, 8224) ties at 9 waves,
-# so both take 256.
+# The tile is 256 x 256, or 192 x 256 when ceil(tiles / 256 CUs) x rows is
+# smaller with it, or 64 x 128 when fewer than 128 tiles of 256 x 256 would
+# run.  64 x 128: the first six shapes (up to 36 tiles of 256 x 256);
+# 192 x 256: (17000, 2048) = 712 tiles of 192 rows (3 waves) against 536 of 256
+# (3 waves); 256 x 256: (8190, 2047) is exactly 256 tiles of 256 rows (344 of
+# 192) and (17000, 8224) ties at 9 waves.
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 200, 128), (1, 8224, 2048), (17, 2048, 2048),
                                    (1000, 2080, 512), (4111, 333, 192), (17000, 2048, 256), (8190, 2047, 128),
                                    (17000, 8224, 128)])
@@ -64,12 +65,13 @@ def test_gemm_strided_operands_and_out(pkg, dev, pad, off):
     assert torch.equal(out[:, off + N:].cpu(), torch.zeros(M, pad - off, dtype=BF16))
 
 
-@pytest.mark.parametrize("M", [777, 1790])
+@pytest.mark.parametrize("M", [100, 777, 1790])
 def test_in_proj_with_gate_epilogue(pkg, dev, M):
     """The layer's in_proj over [W_qkv; W_z; W_b; W_a] (config 1 widths, a
     2048 hidden size): the projections, and g / beta from the b and a columns
-    equal to fused_g_beta on them.  M = 777 runs 192-row tiles, M = 1790 (231
-    tiles of 256 rows, 330 of 192) 256-row tiles."""
+    equal to fused_g_beta on them.  M = 100 runs 64 x 128 tiles, M = 777
+    192 x 256 tiles, M = 1790 (231 tiles of 256 rows, 330 of 192) 256 x 256
+    tiles."""
     gen = torch.Generator().manual_seed(6)
     Hk = Hv = 16
     D, hidden = 128, 2048
