@@ -276,6 +276,70 @@ def layer_bench(pkg, cfg, dev, K, W, hidden=2048):
     return t / K, us, ref.avg_us(), layer.n_in, hidden
 
 
+def layer_decode_bench(pkg, cfg, dev, K, W, hidden=2048):
+    """Config 2 (256 one-token rows, slots of a 512-slot pool) through the
+    whole GDN mixer (GatedDeltaNetLayer, decode path): in_proj GEMM, the fused
+    decode kernel with its gated norm, out_proj GEMM.  Random-init weights of
+    a 2048 hidden size.  Also times the same two GEMM shapes through
+    torch.matmul (hipBLASLt)."""
+    import math
+    gen = torch.Generator().manual_seed(12)
+    Hk, Hv, D, C, B = cfg["Hk"], cfg["Hv"], cfg["D"], cfg["C"], cfg["B"]
+    s = 1 / math.sqrt(hidden)
+    ws = [(torch.randn(r, hidden, generator=gen) * s).to(BF16).to(dev) for r in (C, Hv * D, Hv, Hv)]
+    w_out = (torch.randn(hidden, Hv * D, generator=gen) / math.sqrt(Hv * D)).to(BF16).to(dev)
+    layer = pkg.GatedDeltaNetLayer(*ws, w_out, Hk, Hv, D, cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
+                                   cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
+    x = torch.randn(B, hidden, generator=gen).to(BF16).to(dev)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=dev)
+    ids = cfg["ids"].to(dev)
+    s_pool, conv_pool = cfg["s_pool"].to(dev), cfg["conv_pool"].to(dev)
+    lens = [1] * B
+
+    def step():
+        layer.forward(x, cu, 1, ids, conv_pool, s_pool, lens_q=lens)
+
+    for _ in range(W):
+        step()
+    t = timed_steps(step, K)
+    # the same step replayed from a captured HIP graph (how the engine runs decode)
+    g = torch.cuda.CUDAGraph()
+    gs = torch.cuda.Stream()
+    gs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(gs):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=gs):
+            step()
+    torch.cuda.current_stream().wait_stream(gs)
+    g.replay()
+    t_graph = timed_steps(g.replay, K)
+    timer = EventTimer()
+    layer.timer = timer
+    for _ in range(min(K, 20)):
+        step()
+    torch.cuda.synchronize()
+    layer.timer = None
+    layer.core.timer = None
+    us = timer.avg_us()
+    y_in = torch.empty(B, layer.n_in, dtype=BF16, device=dev)
+    core_out = torch.randn(B, Hv * D, generator=gen).to(BF16).to(dev)
+    y_out = torch.empty(B, hidden, dtype=BF16, device=dev)
+    ref = EventTimer()
+    for _ in range(3):
+        torch.matmul(x, layer.w_in.t(), out=y_in)
+        torch.matmul(core_out, layer.w_out.t(), out=y_out)
+    for _ in range(10):
+        ref.start("in_proj_hipblaslt")
+        torch.matmul(x, layer.w_in.t(), out=y_in)
+        ref.stop("in_proj_hipblaslt")
+        ref.start("out_proj_hipblaslt")
+        torch.matmul(core_out, layer.w_out.t(), out=y_out)
+        ref.stop("out_proj_hipblaslt")
+    torch.cuda.synchronize()
+    return t / K, t_graph / K, us, ref.avg_us(), layer.n_in
+
+
 def decode_bench(pkg, cfg, dev, K, W):
     core = pkg.GatedDeltaNetCore(cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
                                  cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
@@ -396,6 +460,54 @@ def spec_bench(pkg, cfg, dev, K, W):
     return t / K, us
 
 
+def gemm_shapes(pkg, dev, R=10):
+    """gdn_gemm_bf16 (ops.linear) against torch.matmul (hipBLASLt) on the
+    mixer's projection shapes (hidden 2048, config 1's 17,001 tokens and a
+    decode batch of 256) and a square 8192^3: an event pair around R
+    back-to-back launches, three times for each side in turn after about a
+    second of untimed launches (the clock settles under load), the median
+    kept; random operands."""
+    out = {}
+    gen = torch.Generator().manual_seed(13)
+    shapes = [(17001, 8224, 2048, "in_proj_config1"), (17001, 2048, 2048, "out_proj_config1"),
+              (256, 8224, 2048, "in_proj_decode256"), (256, 2048, 2048, "out_proj_decode256"),
+              (8192, 8192, 8192, "square_8192")]
+    ops_ = {}
+    for M, N, K, tag in shapes:
+        a = torch.randn(M, K, generator=gen).to(BF16).to(dev)
+        w = (torch.randn(N, K, generator=gen) / math.sqrt(K)).to(BF16).to(dev)
+        c = torch.empty(M, N, dtype=BF16, device=dev)
+        ops_[tag] = (lambda a=a, w=w, c=c: pkg.ops.linear(a, w, out=c),
+                     lambda a=a, w=w, c=c: torch.matmul(a, w.t(), out=c))
+    t_end = time.time() + 1.0
+    while time.time() < t_end:
+        for ours, _ in ops_.values():
+            ours()
+        torch.cuda.synchronize()
+
+    def t(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(R):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / R * 1e3
+    for M, N, K, tag in shapes:
+        ours, lib = ops_[tag]
+        ts, th = [], []
+        for _ in range(3):
+            ts.append(t(ours))
+            th.append(t(lib))
+        us, us_h = statistics.median(ts), statistics.median(th)
+        fl = 2.0 * M * N * K
+        out[tag] = {"M": M, "N": N, "K": K, "us": round(us, 1), "TFLOPs": round(fl / us / 1e6, 1),
+                    "hipblaslt_us": round(us_h, 1), "hipblaslt_TFLOPs": round(fl / us_h / 1e6, 1)}
+    return out
+
+
 def standalone_kernels(pkg, cfg, dev, K, W):
     """The kernels the fused prefill replaces, each launched on its own at
     config 1's shapes (the path the unfused switches select): the gates, the
@@ -493,6 +605,8 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB K times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
+    ap.add_argument("--gemm-shapes", action="store_true",
+                    help="time the projection GEMM against hipBLASLt on the mixer's shapes and exit")
     ap.add_argument("--standalone-kernels", action="store_true",
                     help="only time the gate, varlen-conv, padded-conv and gated-norm kernels on their own at "
                          "config 1's shapes, K launches each")
@@ -520,6 +634,9 @@ def main():
     pkg._lib.load()
     dev = torch.device("cuda:0")
     K, W = args.steps, args.warmup
+    if args.gemm_shapes:
+        print(json.dumps({"gemm_shapes": gemm_shapes(pkg, dev)}))
+        return
     if args.standalone_kernels:
         res = standalone_kernels(pkg, make_prefill(1, None), dev, K, W)
         print(json.dumps({"standalone_kernels_config1": {
@@ -562,6 +679,20 @@ def main():
             "hipblaslt_same_shapes_us": {k: round(v, 2) for k, v in r5.items()},
             "note": "in_proj = one GEMM over the concatenated qkv/z/b/a weights [N, 2048] x [8224, 2048]^T; "
                     "out_proj [N, 2048] x [2048, 2048]^T; random-init weights"}
+        c2l = make_decode()
+        t6, t6g, k6, r6, n_in6 = layer_decode_bench(pkg, c2l, dev, max(2, K // 4), 2)
+        B6 = c2l["B"]
+        extra["layer_with_projections_decode_config2"] = {
+            "tokens_per_s": round(B6 / t6, 1), "ms_per_step": round(t6 * 1e3, 4),
+            "tokens_per_s_graph": round(B6 / t6g, 1), "ms_per_step_graph": round(t6g * 1e3, 4), "hidden": hidden,
+            "kernels_us": {k: round(v, 2) for k, v in k6.items()},
+            "in_proj_TFLOPs": round(2.0 * B6 * n_in6 * hidden / (k6["in_proj"] * 1e-6) / 1e12, 1),
+            "out_proj_TFLOPs": round(2.0 * B6 * hidden * c2l["Hv"] * c2l["D"] / (k6["out_proj"] * 1e-6) / 1e12, 1),
+            "hipblaslt_same_shapes_us": {k: round(v, 2) for k, v in r6.items()},
+            "note": "config 2's 256 one-token rows through the mixer, eager and replayed from a HIP graph; "
+                    "kernels_us from an event pair around each launch (eager: includes launch gaps at this "
+                    "size): in_proj [256, 2048] x [8224, 2048]^T, q/k conv, fused decode kernel, out_proj "
+                    "[256, 2048] x [2048, 2048]^T; random-init weights"}
     if 2 in configs:
         c2 = make_decode()
         t2, t2g, k2, rec_us, pass_us = decode_bench(pkg, c2, dev, K, W)
