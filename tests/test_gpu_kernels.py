@@ -128,15 +128,19 @@ def test_conv_decode_strided_pool_view(pkg, dev):
 
 
 @pytest.mark.parametrize("layout,n,C,T", [
-    ("chan", 5, 6144, 100),     # [n, T, C] rows seen as [n, C, T] (the reference's layout)
-    ("chan", 3, 200, 128),      # partial channel tile, 16-byte output stores
-    ("tok", 3, 192, 128),       # [n, C, T] contiguous
-    ("tok", 4, 96, 70),         # T not a multiple of 8 or of the 64-token tile
-    ("generic", 3, 100, 66),    # strides that allow no 16-byte loads
+    ("chan", 5, 6144, 100),     # [n, T, C] rows seen as [n, C, T] (the reference's layout); 4-byte stores
+    ("chan", 3, 200, 128),      # partial channel tile, 16-byte loads and stores
+    ("chan", 2, 100, 50),       # C not a multiple of 8: the element-wise kernel
+    ("tok", 3, 192, 128),       # [n, C, T] contiguous: 16-byte accesses
+    ("tok", 4, 96, 70),         # T not a multiple of 8: 4-byte accesses, a partial last group
+    ("tok", 2, 136, 600),       # many 8-token groups per channel (halo from the previous group)
+    ("tok_odd", 3, 100, 66),    # token stride 1, odd sequence stride: 2-byte accesses
+    ("strided", 2, 72, 90),     # neither stride 1: the element-wise kernel
 ])
 def test_conv_padded(pkg, dev, layout, n, C, T):
-    """The padded conv (a6) against the oracle for each input layout the kernel
-    loads differently, with end positions at, inside and before the tokens."""
+    """The padded conv (a6) against the oracle for each input layout the
+    kernels load differently, with end positions at, inside and before the
+    tokens."""
     gen = _gen(16)
     if layout == "chan":
         xm = torch.randn(n, T, C, generator=gen).to(BF16)
@@ -144,10 +148,14 @@ def test_conv_padded(pkg, dev, layout, n, C, T):
     elif layout == "tok":
         x = torch.randn(n, C, T, generator=gen).to(BF16)
         xd = x.to(dev)
-    else:
+    elif layout == "tok_odd":
         big = torch.randn(n, 2 * C + 1, T + 3, generator=gen).to(BF16)
         x = big[:, 1::2, 3:]                                        # channel stride 2 (T + 3), token stride 1
         xd = big.to(dev)[:, 1::2, 3:]
+    else:
+        big = torch.randn(n, 2 * C, 2 * T, generator=gen).to(BF16)
+        x = big[:, ::2, ::2]                                        # channel stride 4 T, token stride 2
+        xd = big.to(dev)[:, ::2, ::2]
     state = torch.randn(n, C, 3, generator=gen).to(BF16)
     w = (torch.randn(C, 4, generator=gen) * 0.5).to(BF16)
     endp = ([T, 2, -1, 0, min(57, T)] * 2)[:n]
