@@ -15,7 +15,8 @@
 //
 // Tiling: a workgroup of 4 waves (one per SIMD, one workgroup per CU)
 // computes a BM x 256 tile of C (BM = 256, or 192 where that fills the last
-// wave of tiles better), K in steps of 64.  Wave (wm, wn) owns rows BM / 2 wm
+// wave of tiles better; 64 x 128 or 64 x 64, several workgroups per CU, for
+// small M), K in steps of 64.  Wave (wm, wn) owns rows BM / 2 wm
 // .. and columns 128 wn ..: BM / 64 x 4 accumulator tiles of 32 x 32 (256
 // registers at BM = 256, kept in AGPRs), 64 products per step.
 //
@@ -347,16 +348,19 @@ extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, 
   // short last wave of 256-row tiles, e.g. 536 tiles = 2.09 waves -> 712 =
   // 2.78).  When 256 x 256 tiles would not fill half of the CUs (small M:
   // decode batches), 64 x 128 tiles, two or more workgroups per CU, spread
-  // the work over the whole chip.
+  // the work over the whole chip; 64 x 64 when even those would not.
   const int64_t nb256 = (N + 255) / 256;
   const int64_t t256 = ((M + 255) / 256) * nb256, t192 = ((M + 191) / 192) * nb256;
   const int64_t w256 = (t256 + kCUs - 1) / kCUs, w192 = (t192 + kCUs - 1) / kCUs;
-  const int cfg = t256 < kCUs / 2 ? 2 : (w192 * 192 < w256 * 256 ? 1 : 0);
-  const int64_t tiles = cfg == 2 ? ((M + 63) / 64) * ((N + 127) / 128) : cfg == 1 ? t192 : t256;
+  const int64_t t64x128 = ((M + 63) / 64) * ((N + 127) / 128);
+  const int cfg = t256 >= kCUs / 2 ? (w192 * 192 < w256 * 256 ? 1 : 0) : t64x128 >= kCUs / 2 ? 2 : 3;
+  const int64_t tiles = cfg == 3 ? ((M + 63) / 64) * ((N + 63) / 64) : cfg == 2 ? t64x128 : cfg == 1 ? t192 : t256;
   const int64_t grid = gdn::kNumXcd * ((tiles + gdn::kNumXcd - 1) / gdn::kNumXcd);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 g3(static_cast<unsigned>(grid)), b3(kGemmThreads);
-  if (cfg == 2)
+  if (cfg == 3)
+    gemm_tn_kernel<64, 64, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+  else if (cfg == 2)
     gemm_tn_kernel<64, 128, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
   else if (cfg == 1)
     gemm_tn_kernel<192, 256, 1><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);

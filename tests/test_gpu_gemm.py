@@ -32,11 +32,13 @@ def _ref(a, w):
 
 # The tile is 256 x 256, or 192 x 256 when ceil(tiles / 256 CUs) x rows is
 # smaller with it, or 64 x 128 when fewer than 128 tiles of 256 x 256 would
-# run.  64 x 128: the first six shapes (up to 36 tiles of 256 x 256);
+# run, or 64 x 64 when fewer than 128 of 64 x 128 would.  64 x 64: (256, 256),
+# (300, 200), (1, 8224), (17, 2048), (256, 2048) (the decode out_proj);
+# 64 x 128: (1000, 2080), (4111, 333);
 # 192 x 256: (17000, 2048) = 712 tiles of 192 rows (3 waves) against 536 of 256
 # (3 waves); 256 x 256: (8190, 2047) is exactly 256 tiles of 256 rows (344 of
 # 192) and (17000, 8224) ties at 9 waves.
-@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 200, 128), (1, 8224, 2048), (17, 2048, 2048),
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 200, 128), (1, 8224, 2048), (17, 2048, 2048), (256, 2048, 2048),
                                    (1000, 2080, 512), (4111, 333, 192), (17000, 2048, 256), (8190, 2047, 128),
                                    (17000, 8224, 128)])
 def test_gemm_against_fp32_matmul(pkg, dev, M, N, K):
