@@ -563,7 +563,8 @@ def standalone_kernels(pkg, cfg, dev, K, W):
 
 def cpu_baseline(cfg, n_seq: int, threads: int):
     """CPU oracle (fp32 torch restatement of the reference path) on the first
-    n_seq sequences of config 1: 1 warm-up on a 256-token slice, median of 3."""
+    n_seq sequences of config 1 (the bench passes all of them: the whole
+    workload): 1 warm-up on a 256-token slice, median of 3."""
     from oracle import gdn_ref
 
     torch.set_num_threads(threads)
@@ -589,7 +590,8 @@ def cpu_baseline(cfg, n_seq: int, threads: int):
     except OSError:
         pass
     return {"value": N / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"config 1 GDN core (g/beta+conv+chunk rule+gated norm) on its first {n_seq} sequences "
+            "sample": f"config 1 GDN core (g/beta+conv+chunk rule+gated norm) on {n_seq} of its "
+                      f"{len(cfg['lens'])} sequences "
                       f"({N} tokens, lens {lens}), fp32 torch oracle, median of 3 reps ({t:.2f} s each), "
                       f"os.cpu_count()={os.cpu_count()}, cpu='{cpu_name}'"}
 
@@ -753,7 +755,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(cfg1, 3, threads=min(16, os.cpu_count() or 1))
+        cpu = cpu_baseline(cfg1, len(cfg1["lens"]), threads=min(16, os.cpu_count() or 1))
 
     out = {
         "metric": METRIC, "value": round(N1 / t1, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
