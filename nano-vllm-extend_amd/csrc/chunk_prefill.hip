@@ -220,10 +220,13 @@ __device__ bool locate_chunk(const int64_t* __restrict__ cu, int n_seqs, int64_t
 // lane (n, g) has a 1 at slot e iff 16 h + 8 g + e == col(n), with col(n) = n
 // (natural) or qswap(n) (so output column n receives input column qswap(n)).
 __device__ __forceinline__ s16x8_t ident_frag(int h, int coln, int g) {
-  s16x8_t f;
+  // the slot e = coln - 16 h - 8 g, if in [0, 8): bf16 1.0 in half e & 1 of word e >> 1
+  const uint32_t e = static_cast<uint32_t>(coln - 16 * h - 8 * g);
+  const uint32_t one = e < 8 ? (0x3f80u << (16 * (e & 1))) : 0u;
+  u32x4_t w;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) f[e] = (16 * h + 8 * g + e == coln) ? static_cast<short>(0x3f80) : static_cast<short>(0);
-  return f;
+  for (int k = 0; k < 4; ++k) w[k] = (e >> 1) == static_cast<uint32_t>(k) ? one : 0u;
+  return __builtin_bit_cast(s16x8_t, w);
 }
 
 __device__ __forceinline__ f32x16_t mfma32_bf16(const s16x8_t& a, const s16x8_t& b, const f32x16_t& c) {
@@ -322,20 +325,19 @@ struct ConvIn {
 };
 
 // Fused variant, phase 1: causal conv (width 4) + SiLU of the chunk's q and k
-// rows (the v channels' conv runs in the state kernel).  Each output row needs the 3 raw rows before it: inside the chunk
-// and the previous chunk they are rows of x, before a sequence's first token
-// they are the conv state's taps.  Thread (16-byte channel segment c8, rows
-// t0 .. t0 + RPT - 1) loads its RPT + 3 raw rows of a part (q, k or v) and the
-// part's taps, and writes q -> Qc and k -> Kr (bf16 rows in LDS, zero past the
-// sequence end), the k rows' sums of squares -> ssk (in the plain path's
-// summation order).
-// The loads of a part are unconditional (rows clamped into x) so that the
-// three parts' loads can be in flight together; the few lanes whose window
-// starts before the sequence replace those rows with the conv state after the
-// loads have landed.
+// rows (the v channels' conv runs in the state kernel).  Each output row needs
+// the 3 raw rows before it: inside the chunk and the previous chunk they are
+// rows of x, before a sequence's first token they are the conv state's taps.
+// Waves 0-1 compute q, waves 2-3 k.  Thread (16-byte channel segment c8, rows
+// t0 .. t0 + RPT - 1 of its part) loads its RPT + 3 raw rows and the part's
+// taps, and writes q -> Qc, k -> Kr (bf16 rows in LDS, zero past the sequence
+// end).
+// The loads are unconditional (rows clamped into x) so that they can all be
+// in flight together; the few lanes whose window starts before the sequence
+// replace those rows with the conv state after the loads have landed.
 template <int D>
 struct ConvRaw {
-  static constexpr int RPT = kC * (D / 8) / 256;  // rows per thread
+  static constexpr int RPT = kC * (D / 8) / 128;  // rows per thread (128 threads per part)
   uint4 x[RPT + 3];                               // raw rows t0 - 3 .. t0 + RPT - 1
 };
 
@@ -407,8 +409,8 @@ __device__ __forceinline__ float bf_elem(const uint4& u, int e) {
 
 template <int D>
 __device__ __forceinline__ void conv_compute(const ConvRaw<D>& R, const ConvIn& cv, int part, uint16_t (*Qc)[D + 8],
-                                             uint16_t (*Kr)[D + 8], float* ssk, int64_t tok0, int len, int kh,
-                                             int h, int Hv, int tid) {
+                                             uint16_t (*Kr)[D + 8], int64_t tok0, int len, int kh, int h, int Hv,
+                                             int tid) {
   constexpr int SEG = D / 8;
   constexpr int RPT = ConvRaw<D>::RPT;
   const int c8 = tid % SEG, t0 = RPT * (tid / SEG);
@@ -445,39 +447,23 @@ __device__ __forceinline__ void conv_compute(const ConvRaw<D>& R, const ConvIn& 
   for (int rr = 0; rr < RPT; ++rr) {
     const int t = t0 + rr;
     u32x4_t out = {yp[rr][0], yp[rr][1], yp[rr][2], yp[rr][3]};
-    if (t >= len) out = u32x4_t{0u, 0u, 0u, 0u};
-    if (part == 0) {
-      *reinterpret_cast<u32x4_t*>(&Qc[t][8 * c8]) = out;
-    } else {
-      *reinterpret_cast<u32x4_t*>(&Kr[t][8 * c8]) = out;
-      const s16x8_t kv8 = __builtin_bit_cast(s16x8_t, out);
-      float ks = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
-        ks += kf * kf;
-      }
-#pragma unroll
-      for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
-      if (c8 == 0) ssk[t] = ks;
-    }
+    if (len < kC && t >= len) out = u32x4_t{0u, 0u, 0u, 0u};  // only a sequence's last chunk
+    *reinterpret_cast<u32x4_t*>(part == 0 ? &Qc[t][8 * c8] : &Kr[t][8 * c8]) = out;
   }
 }
 
-// The two parts with two register sets: q and k in flight together.
+// Waves 0-1 compute the q part, waves 2-3 the k part (wave-uniform).
 template <int D>
 __device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)[D + 8], uint16_t (*Kr)[D + 8],
-                                                float* ssk, int64_t tok0, int len, bool first, int r, int kh,
-                                                int h, int Hv, int tid) {
-  ConvRaw<D> R0, R1;
-  conv_load<D>(R0, cv, 0, tok0, len, kh, h, tid);
+                                                int64_t tok0, int len, bool first, int r, int kh, int h, int Hv,
+                                                int tid) {
+  const int part = __builtin_amdgcn_readfirstlane(tid >> 7);
+  const int ptid = tid & 127;
+  ConvRaw<D> R;
+  conv_load<D>(R, cv, part, tok0, len, kh, h, ptid);
   gdn::keep_loads_here();
-  conv_load<D>(R1, cv, 1, tok0, len, kh, h, tid);
-  gdn::keep_loads_here();
-  conv_state_halo<D>(R0, cv, 0, first, r, kh, h, tid);
-  conv_compute<D>(R0, cv, 0, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
-  conv_state_halo<D>(R1, cv, 1, first, r, kh, h, tid);
-  conv_compute<D>(R1, cv, 1, Qc, Kr, ssk, tok0, len, kh, h, Hv, tid);
+  conv_state_halo<D>(R, cv, part, first, r, kh, h, ptid);
+  conv_compute<D>(R, cv, part, Qc, Kr, tok0, len, kh, h, Hv, ptid);
 }
 
 // grid = 8 * ceil(nc_bound * Hv / 8); block = 256.  One workgroup per
@@ -528,24 +514,16 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
   s16x8_t qv[KTD];
   auto q_rows = [&]() {
     const int t = 16 * wave + lr;
-    float qs = 0.f;
+    if constexpr (kConv) {
 #pragma unroll
-    for (int kk = 0; kk < KTD; ++kk) {
-      if constexpr (kConv) {
-        qv[kk] = *reinterpret_cast<const s16x8_t*>(&Qc[t][32 * kk + 8 * lg]);
-      } else {
+      for (int kk = 0; kk < KTD; ++kk) qv[kk] = *reinterpret_cast<const s16x8_t*>(&Qc[t][32 * kk + 8 * lg]);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KTD; ++kk) {
         qv[kk] = *reinterpret_cast<const s16x8_t*>(qh + (tok0 + min(t, len - 1)) * sq + 8 * lg + 32 * kk);
         if (t >= len) qv[kk] = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float qf = gdn::bf2f(static_cast<uint16_t>(qv[kk][i]));
-        qs += qf * qf;
-      }
     }
-    qs += __shfl_xor(qs, 16, 64);
-    qs += __shfl_xor(qs, 32, 64);
-    if (lg == 0) sm.ssq[t] = qs;
   };
   if constexpr (!kConv) q_rows();
   // gate inputs of token tok0 + lane (used by wave 0), loaded ahead of the
@@ -565,7 +543,7 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
   }
   gdn::keep_loads_here();
   if constexpr (kConv) {
-    conv_chunk_rows<D>(cv, Qc, sm.u.Kr, sm.ssk, tok0, len, jc == 0, r, kh, h, Hv, tid);
+    conv_chunk_rows<D>(cv, Qc, sm.u.Kr, tok0, len, jc == 0, r, kh, h, Hv, tid);
   } else {
 #pragma unroll
     for (int j = 0; j < NSEG1; ++j) {
@@ -575,15 +553,6 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
       s16x8_t kv8 = *reinterpret_cast<const s16x8_t*>(kh_ + row * sk + c8 * 8);
       if (t >= len) kv8 = s16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
       *reinterpret_cast<s16x8_t*>(&sm.u.Kr[t][c8 * 8]) = kv8;
-      float ks = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float kf = gdn::bf2f(static_cast<uint16_t>(kv8[i]));
-        ks += kf * kf;
-      }
-#pragma unroll
-      for (int m = SEG / 2; m >= 1; m >>= 1) ks += __shfl_xor(ks, m, 64);
-      if (c8 == 0) sm.ssk[t] = ks;
     }
   }
   if (wave == 0) {
@@ -608,6 +577,29 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
   if constexpr (kConv) {
     __syncthreads();  // the conv's q rows are in LDS
     q_rows();
+  }
+  __syncthreads();
+
+  // ---- the rows' sums of squares: the diagonals of the Gram tiles K K^T and
+  //      Q Q^T of wave w's 16 rows (the bf16 products are exact; the matrix
+  //      core sums them in fp32).  A row's A and B operand fragments are the
+  //      same registers, so Q Q^T needs no LDS read.  C lane (column lr, rows
+  //      4 lg + i) holds the diagonal element (lr, lr) at lg = lr / 4,
+  //      i = lr % 4. ----
+  {
+    const int t = 16 * wave + lr;
+    f32x4_t gk = {0.f, 0.f, 0.f, 0.f}, gq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KTD; ++kk) {
+      const s16x8_t k8 = *reinterpret_cast<const s16x8_t*>(&sm.u.Kr[t][32 * kk + 8 * lg]);
+      gk = gdn::mfma16x16x32(k8, k8, gk);
+      gq = gdn::mfma16x16x32(qv[kk], qv[kk], gq);
+    }
+    if (lg == (lr >> 2)) {
+      const int i = lr & 3;
+      sm.ssk[t] = i == 0 ? gk[0] : i == 1 ? gk[1] : i == 2 ? gk[2] : gk[3];
+      sm.ssq[t] = i == 0 ? gq[0] : i == 1 ? gq[1] : i == 2 ? gq[2] : gq[3];
+    }
   }
   __syncthreads();
 
