@@ -675,10 +675,18 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     const int s = 16 * nt + lr;
     const float rks = sm.rk[s];
     const float Gs = sm.G[s];
+    // rows t = 16 mt + 4 lg + i: four consecutive tokens, one 16-byte read per vector
+    const int t0 = 16 * mt + 4 * lg;
+    const float4 btv = *reinterpret_cast<const float4*>(&sm.bt[t0]);
+    const float4 rkv = *reinterpret_cast<const float4*>(&sm.rk[t0]);
+    const float4 gv = *reinterpret_cast<const float4*>(&sm.G[t0]);
+    const float bt4[4] = {btv.x, btv.y, btv.z, btv.w}, rk4[4] = {rkv.x, rkv.y, rkv.z, rkv.w};
+    const float g4[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = 16 * mt + 4 * lg + i;
-      sm.Lp[j][4 * lg + i][lr] = s < t ? acc[i] * sm.bt[t] * sm.rk[t] * rks * __expf(sm.G[t] - Gs) : 0.f;
+      const float l = acc[i] * bt4[i] * rk4[i] * rks * __expf(g4[i] - Gs);
+      // below the diagonal tile every s < t; on it the strict lower triangle
+      sm.Lp[j][4 * lg + i][lr] = (mt != nt || s < t0 + i) ? l : 0.f;
     }
   }
   __syncthreads();
@@ -717,19 +725,24 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     const float Gt = sm.G[t];
 #pragma unroll 1
     for (int ns = 0; ns <= (mt | 1); ++ns) {  // wave-uniform trip count
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      float a[4] = {0.f, 0.f, 0.f, 0.f};       // tiles above the diagonal stay zero
       if (ns <= mt) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < KTD; ++kk) {
           const s16x8_t a8 = *reinterpret_cast<const s16x8_t*>(&sm.u.Kr[16 * ns + lr][32 * kk + 8 * lg]);
           acc = gdn::mfma16x16x32(a8, qv[kk], acc);
         }
-      }
-      float a[4];
+        // keys s = 16 ns + 4 lg + i: four consecutive tokens
+        const int s0 = 16 * ns + 4 * lg;
+        const float4 rkv = *reinterpret_cast<const float4*>(&sm.rk[s0]);
+        const float4 gv = *reinterpret_cast<const float4*>(&sm.G[s0]);
+        const float rk4[4] = {rkv.x, rkv.y, rkv.z, rkv.w}, g4[4] = {gv.x, gv.y, gv.z, gv.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int s = 16 * ns + 4 * lg + i;
-        a[i] = (s <= t && t < len) ? acc[i] * qscale * sm.rk[s] * __expf(Gt - sm.G[s]) : 0.f;
+        for (int i = 0; i < 4; ++i) {
+          const float av = acc[i] * qscale * rk4[i] * __expf(Gt - g4[i]);
+          a[i] = ((ns < mt || s0 + i <= t) && t < len) ? av : 0.f;
+        }
       }
       // tokens 16 ns + 4 lg .. + 3 sit at the positions of quad qswap
       const int pos = qswap(16 * ns + 4 * lg);

@@ -9,6 +9,8 @@ CPU or eager fallback: a CPU tensor or a missing library raises.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib
@@ -35,6 +37,54 @@ def _bf16(t: torch.Tensor, name: str) -> None:
 
 def _stream(dev: torch.device) -> int:
     return _lib.stream_handle(dev)
+
+
+# ------------------------------------------------------- fp16 operand range --
+# The chunk kernels run their state-path products on fp16 matrix cores: the
+# raw k and v rows (after the conv), Q', the block inverses, A, the state S
+# and Vn = U - W S become fp16 operands, so each must stay below the fp16
+# maximum.  Q' and A are bounded by the L2 norm (|Q'| <= scale, |A| <= scale);
+# the inputs a caller controls are checked here on request.
+FP16_MAX = 65504.0
+
+
+def range_check_enabled() -> bool:
+    """NANOVLLM_GDN_CHECK_RANGE=1 turns on the input range check of the
+    prefill wrappers (a device reduction and a host sync per call)."""
+    return os.environ.get("NANOVLLM_GDN_CHECK_RANGE", "0") == "1"
+
+
+def fp16_range_violation(rows: torch.Tensor | None = None, conv_weight: torch.Tensor | None = None,
+                         states: torch.Tensor | None = None) -> str | None:
+    """Why a prefill call's inputs could leave the fp16 operand range, or None.
+
+    rows: the rows that feed the kernels -- raw q|k|v rows when conv_weight
+    [C, 4] is given (the conv output of channel c is at most
+    sum_i |w[c, i]| * max |x| in magnitude, SiLU not increasing it), else the
+    q, k, v rows themselves; states: the initial states that will be read.
+    Non-finite values count as violations.  Works on any device."""
+    if rows is not None and rows.numel():
+        m = rows.detach().float().abs().amax()
+        if not torch.isfinite(m):
+            return "non-finite input rows"
+        bound = float(m)
+        if conv_weight is not None:
+            gain = float(conv_weight.detach().float().reshape(conv_weight.shape[0], -1).abs().sum(1).amax())
+            bound *= gain
+        if bound >= FP16_MAX:
+            return (f"input rows reach {bound:.4g} after the conv" if conv_weight is not None
+                    else f"input rows reach {bound:.4g}") + f" (fp16 operands must stay below {FP16_MAX:g})"
+    if states is not None and states.numel():
+        m = float(states.detach().abs().amax())
+        if not m < FP16_MAX:  # also catches NaN / inf
+            return f"initial states reach {m:.4g} (fp16 operands must stay below {FP16_MAX:g})"
+    return None
+
+
+def _check_range(**kw) -> None:
+    why = fp16_range_violation(**kw)
+    if why is not None:
+        raise ValueError(f"GDN chunk prefill: {why}")
 
 
 # ----------------------------------------------------------------- g / beta --
@@ -253,6 +303,11 @@ def chunk_gated_delta_rule_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
             sstride = st.stride(0)
     if h0 is not None and hT is not None:
         assert h0.stride(0) == hT.stride(0), "initial and final state must share the slot stride"
+    if range_check_enabled():
+        read = None
+        if h0 is not None:
+            read = h0.index_select(0, ids) if ids is not None else h0
+        _check_range(rows=torch.cat([q.reshape(N, -1), k.reshape(N, -1), v.reshape(N, -1)], 1), states=read)
     if scale is None:
         scale = D ** -0.5
     o = torch.empty(N, Hv, D, dtype=v.dtype, device=v.device)
@@ -334,6 +389,11 @@ def conv_chunk_prefill_varlen(mixed: torch.Tensor, conv_state: torch.Tensor, con
     if fresh is not None:
         fr = fresh.to(device=mixed.device, dtype=torch.uint8).contiguous()
         assert fr.shape == (n,)
+    if range_check_enabled():
+        rows_read = torch.arange(n, device=mixed.device) if ids is None else ids
+        if fr is not None:
+            rows_read = rows_read[fr == 0]
+        _check_range(rows=mixed, conv_weight=w, states=state.index_select(0, rows_read))
     if scale is None:
         scale = D ** -0.5
     o = torch.empty(N, Hv, D, dtype=torch.bfloat16, device=mixed.device)

@@ -123,3 +123,40 @@ def test_fresh_flags_equal_zeroed_slots(pkg, dev, Hk, Hv, D, lens):
     assert torch.equal(o_f.view(torch.int16), o_z.view(torch.int16)), "outputs differ"
     assert torch.equal(sp_f, sp_z), "state pool differs"
     assert torch.equal(cp_f.view(torch.int16), cp_z.view(torch.int16)), "conv pool differs"
+
+
+def test_range_check_rejects_before_launch(pkg, dev, monkeypatch):
+    """NANOVLLM_GDN_CHECK_RANGE=1: inputs that could leave the fp16 operand
+    range raise before any kernel runs (pools untouched); in-range inputs
+    run as usual."""
+    Hk, Hv, D, lens = 2, 2, 64, [70, 5]
+    C, mixed, conv_w, A_log, dt_bias, a, b, conv_pool, s_pool, ids = _case(5, Hk, Hv, D, lens, 4)
+    args = [t.to(dev) for t in (mixed, conv_pool, conv_w, b, a, A_log, dt_bias)]
+    cu = _cu(lens, dev)
+    pool = s_pool.to(dev)
+    idd = ids.to(dev)
+    monkeypatch.setenv("NANOVLLM_GDN_CHECK_RANGE", "1")
+    pkg.ops.conv_chunk_prefill_varlen(*args, cu, pool, idd, Hk, Hv, D)      # in range: runs
+    torch.cuda.synchronize()
+    big = args[0].clone()
+    big[3, 7] = 3.0e4                                 # times the taps' gain: beyond fp16
+    snap = (pool.clone(), args[1].clone())
+    with pytest.raises(ValueError, match="fp16"):
+        pkg.ops.conv_chunk_prefill_varlen(big, *args[1:], cu, pool, idd, Hk, Hv, D)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, snap[0]) and torch.equal(args[1], snap[1])   # rejected before any launch
+    hot = pool.clone()
+    hot[idd[1], 0, 5, 5] = 7.0e4
+    with pytest.raises(ValueError, match="initial states"):
+        pkg.ops.conv_chunk_prefill_varlen(*args, cu, hot, idd, Hk, Hv, D)
+    fresh = torch.tensor([0, 1], dtype=torch.uint8, device=dev)   # the hot row is fresh: not read
+    pkg.ops.conv_chunk_prefill_varlen(*args, cu, hot, idd, Hk, Hv, D, fresh=fresh)
+    torch.cuda.synchronize()
+    q = torch.randn(10, Hk, D, device=dev).to(BF16)
+    k = torch.randn(10, Hk, D, device=dev).to(BF16)
+    v = torch.randn(10, Hv, D, device=dev).to(BF16)
+    v[2, 1, 3] = float("inf")
+    g = torch.zeros(10, Hv, device=dev)
+    beta = torch.full((10, Hv), 0.5, device=dev).to(BF16)
+    with pytest.raises(ValueError, match="non-finite"):
+        pkg.ops.chunk_gated_delta_rule_varlen(q, k, v, g, beta, _cu([10], dev))

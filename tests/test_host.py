@@ -210,3 +210,38 @@ def test_missing_library_fails_loudly(tmp_path):
             % (str(ROOT), str(tmp_path / "missing.so")))
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert "LOUD" in r.stdout, r.stderr
+
+
+def test_fp16_range_violation_bounds(pkg):
+    """The opt-in input check of the prefill wrappers: raw rows times the
+    conv's largest tap gain, the raw rows themselves without the conv, and
+    the initial states must stay below the fp16 maximum (65504); non-finite
+    inputs are rejected.  Pinned against hand-computed bounds."""
+    f = pkg.ops.fp16_range_violation
+    rows = torch.zeros(4, 6, dtype=torch.bfloat16)
+    rows[1, 2] = -200.0
+    w = torch.zeros(6, 4, dtype=torch.bfloat16)
+    w[3] = torch.tensor([100.0, -100.0, 50.0, 50.0])          # channel gain 300
+    assert f(rows=rows) is None
+    assert f(rows=rows, conv_weight=w) is None                # 200 * 300 = 60000 < 65504
+    w[3, 0] = 120.0                                           # gain 320 -> 64000
+    assert f(rows=rows, conv_weight=w) is None
+    w[3, 0] = 130.0                                           # gain 330 -> 66000
+    assert "after the conv" in f(rows=rows, conv_weight=w)
+    rows[0, 0] = 70000.0
+    assert "input rows reach" in f(rows=rows)
+    rows[0, 0] = float("nan")
+    assert f(rows=rows) == "non-finite input rows"
+    st = torch.zeros(2, 1, 4, 4)
+    assert f(states=st) is None
+    st[1, 0, 2, 3] = -65504.0
+    assert "initial states" in f(states=st)
+    st[1, 0, 2, 3] = float("inf")
+    assert "initial states" in f(states=st)
+
+
+def test_fp16_range_switch(pkg, monkeypatch):
+    monkeypatch.delenv("NANOVLLM_GDN_CHECK_RANGE", raising=False)
+    assert not pkg.ops.range_check_enabled()
+    monkeypatch.setenv("NANOVLLM_GDN_CHECK_RANGE", "1")
+    assert pkg.ops.range_check_enabled()
