@@ -1217,9 +1217,9 @@ __device__ __forceinline__ void o_intra_store(const APrefetch& p, const StateXch
 // v channels, and the q and k channels of its columns when h is the first
 // value head of its key head: state taps j = 0..2 <- the raw inputs at
 // positions T - 3 + j (old taps T + j where that is negative), as the
-// standalone conv kernel does.  The output waves roll after their last chunk:
-// the U waves read the v channels' old taps for their first chunk before the
-// first workgroup barrier.
+// standalone conv kernel does.  The output waves roll after the first
+// workgroup barrier: the U waves read the v channels' old taps for their first
+// chunk before it.
 // (a fresh sequence rolls from a zero state: its old taps are not read)
 
 template <int D>
@@ -1359,7 +1359,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #define GDN_LEN(j_) static_cast<int>(min<int64_t>(kC, seqlen - (j_) * kC))
   if (wave >= 2) {
     // one item per sequence (its first chunk, with outputs) rolls the conv
-    // state, in its output waves after their last chunk
+    // state, in its output waves at the start of interval 0
     const bool roll = kX && wave < 4 && c0 == 0 && mode == kSegOut;
 #define GDN_ROLL() conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], seq_bos, seq_len, h, cb, threadIdx.x - 128, 128)
     if (nch == 0) {
@@ -1411,6 +1411,11 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       a_prefetch(a1, rec1, nt, lane);
       gdn::keep_loads_here();
       gdn::lds_barrier();
+      // The conv-state roll, in interval 0: the U waves have read the old v
+      // taps before the first barrier (and the prep kernel the q and k taps
+      // before this kernel), and interval 0 has no finished chunk to store, so
+      // the roll stays off the tail of the workgroups that finish last.
+      if (roll) GDN_ROLL();
       // interval 0: S^T Q'^T of chunk 0
       o_inter<D>(q0, sm.xs, sm.sflag, 0, lane, acc);
       __builtin_amdgcn_sched_barrier(0);
@@ -1440,7 +1445,6 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
         o_intra_store(a1, sm.xv[1], acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
       else
         o_intra_store(a0, sm.xv[0], acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
-      if (roll) GDN_ROLL();
 #undef GDN_ROLL
     } else {
       // ------------------------------------------------------------ U and K --
