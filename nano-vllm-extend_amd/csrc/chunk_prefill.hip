@@ -1250,12 +1250,13 @@ __device__ __forceinline__ void conv_roll(const StateConv& cr, int64_t slot, boo
 // where R is the recurrence run from S = 0 and P the recurrence run on the
 // identity's columns with U = 0.  A long sequence is cut into segments: the
 // first runs as usual (outputs, from h0) and ends in the second's initial
-// state; each middle segment runs twice, as R and as P, in parallel with the
-// first; a scan S_{s+1} = P_s S_s + R_s gives every later segment its initial
-// state; then those segments run again with outputs, all in parallel.
-constexpr int kSegOut = 0;         // outputs; state from h0 (NULL: zero), final to hT
-constexpr int kSegState = 1;       // no outputs; state from h0 (NULL: zero), final to hT
-constexpr int kSegTransition = 2;  // no outputs, U = 0, state from the identity's columns
+// state; each middle segment runs once without outputs, in parallel with the
+// first: its chain waves run R and its output waves, idle otherwise, run P on
+// the same staged records; a scan S_{s+1} = P_s S_s + R_s gives every later
+// segment its initial state; then those segments run again with outputs, all
+// in parallel.
+constexpr int kSegOut = 0;   // outputs; state from h0 (NULL: zero), final to hT
+constexpr int kSegBoth = 1;  // no outputs; R (from zero) to hT and P to hP
 constexpr int kMaxSegItems = 64;
 constexpr int kPhasePrep = 1;   // launch the prep kernel
 constexpr int kPhaseState = 2;  // launch the state pass
@@ -1265,11 +1266,177 @@ struct SegItem {
   int pool_h0, pool_hT; // nonzero: the state at the sequence's pool row (kernel arguments h0 / hT)
   const float* h0;      // else [Hv, D, D] initial state of the item (NULL: zero)
   float* hT;            // else [Hv, D, D] final state (NULL: not stored)
+  float* hP;            // kSegBoth: [Hv, D, D] the segment's transition P
 };
 struct SegList {
   int n;  // 0: one item per sequence, states at the pool rows (the plain launch)
   SegItem it[kMaxSegItems];
 };
+
+// The recurrence of one 32-column tile of the state (ct: the tile within the
+// workgroup's 64 columns, vc0 its first column), one workgroup barrier per
+// chunk, from the identity's columns (ident), from ih0 or from zero; the final
+// state goes to ihT.  kP: the transition of a segment -- U = 0 and nothing
+// handed to the output waves (their exchange belongs to the chain waves of the
+// same workgroup, which run the segment's own recurrence beside it).
+template <int D, bool kP>
+__device__ __forceinline__ void chain_pass(StateSmem<D>& sm, int ct, int vc0, int64_t nch, bool ident,
+                                           const float* ih0, float* ihT, int h, int lane) {
+  constexpr int NR = D / 32;
+  constexpr int KS = D / 16;
+  const int li = lane & 31, g = lane >> 5;
+  f32x16_t S[NR];
+  if (ident) {
+    // the identity's columns vc0 + li (row position p holds key qswap(p))
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          S[rt][4 * i + rr] = qswap(32 * rt + 8 * i + 4 * g + rr) == vc0 + li ? 1.f : 0.f;
+  } else if (ih0) {
+    const float* hp = ih0 + static_cast<int64_t>(h) * D * D + vc0 + li;
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          S[rt][4 * i + rr] = hp[static_cast<int64_t>(qswap(32 * rt + 8 * i + 4 * g + rr)) * D];
+  } else {
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt) S[rt] = zero16();
+  }
+  if (nch > 0) gdn::lds_barrier();
+  for (int64_t jc = 0; jc < nch; ++jc) {
+    const StateStage<D>& B = sm.st[jc & 1];
+    StateXchgV& X = sm.xv[jc & 1];
+    (void)X;
+    // Re-derive lane indices from an opaque copy each chunk so the compiler
+    // does not keep every lane-dependent address live across the loop.
+    int tid_l = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tid_l));
+    const int ln = tid_l & 63;
+
+    // Operand fragments of each product are read from LDS as one batch ahead
+    // of its MFMAs, so the reads overlap each other instead of each MFMA
+    // waiting out an LDS latency: first the U tiles that the first products
+    // accumulate onto, then -W in k-step order.
+    f32x16_t U[2];
+    h16x8_t wf[2][KS];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4_t u4 = kP ? f32x4_t{0.f, 0.f, 0.f, 0.f} : B.U[ct][mt][qd][ln];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = u4[rr];
+      }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      wf[0][s] = B.W[s][ln];
+      wf[1][s] = B.W[KS + s][ln];
+    }
+    const float eg = B.vec[2 * kC];
+    __builtin_amdgcn_sched_barrier(0);
+    // S as fp16 fragments (B operand of W S here, A operand of the output
+    // wave's S^T Q'^T), packed while the reads are in flight.  Vn = U + (-W) S
+    // with both 32-token tiles interleaved; tile 1's last product is issued
+    // after the fence below, so tile 0 is packed while it runs.
+    h16x8_t Sh[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) Sh[s] = (s & 1) ? pack_h8<8>(S[s >> 1]) : pack_h8<0>(S[s >> 1]);
+#pragma unroll
+    for (int s = 0; s < KS - 1; ++s) {
+      U[0] = mfma32(wf[0][s], Sh[s], U[0]);
+      U[1] = mfma32(wf[1][s], Sh[s], U[1]);
+    }
+    U[0] = mfma32(wf[0][KS - 1], Sh[KS - 1], U[0]);
+    // the exchange copy of S (then the flag that says it is there), the decay
+    // of the old state and the update's operand reads, while W S runs
+    if constexpr (!kP) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) sm.xs.Sh[ct][s][ln] = Sh[s];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      if (ln == 0) __hip_atomic_store(&sm.sflag[ct], static_cast<int>(jc) + 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) S[rt][e] *= eg;
+    h16x8_t kf[NR][4];
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[rt][s] = B.Kt[rt * 4 + s][ln];
+    // cK of the tokens 32 mt + 8 i + 4 lgp + r held by this lane's Vn elements
+    f32x4_t ck[2][4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ck[mt][i] = *reinterpret_cast<const f32x4_t*>(&B.vec[kC + 32 * mt + 8 * i + 4 * (ln >> 5)]);
+    __builtin_amdgcn_sched_barrier(0);
+    U[1] = mfma32(wf[1][KS - 1], Sh[KS - 1], U[1]);
+    // S <- e^gamma S + K^T diag(cK) Vn, one token tile at a time: Vn as fp16
+    // (A operand of Vn^T A^T, to the exchange) and diag(cK) Vn as fp16 (B
+    // operand of the update); tile 1 is packed while tile 0's products run.
+    // The exchange gets Vn as its fp16 rounding Vh and the rounding's
+    // residual Vl, formed while the update's products run.
+    h16x8_t Vh[4], Vk[4];
+    f32x16_t Uk[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      Vh[2 * mt] = pack_h8<0>(U[mt]);
+      Vh[2 * mt + 1] = pack_h8<8>(U[mt]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Uk[mt][4 * i + r] = U[mt][4 * i + r] * ck[mt][i][r];
+      Vk[2 * mt] = pack_h8<0>(Uk[mt]);
+      Vk[2 * mt + 1] = pack_h8<8>(Uk[mt]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 2 * mt; s < 2 * mt + 2; ++s)
+#pragma unroll
+        for (int rt = 0; rt < NR; ++rt) S[rt] = mfma32(kf[rt][s], Vk[s], S[rt]);
+    }
+    if constexpr (!kP) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4_t hi = __builtin_bit_cast(u32x4_t, Vh[s]);
+        u32x4_t lo;
+#pragma unroll
+        for (int p2 = 0; p2 < 4; ++p2) {
+          const int e = 8 * (s & 1) + 2 * p2;
+          lo[p2] = f2h2_lo(U[s >> 1][e], U[s >> 1][e + 1], hi[p2]);
+        }
+        X.Vh[ct][s][ln] = Vh[s];
+        X.Vl[ct][s][ln] = __builtin_bit_cast(h16x8_t, lo);
+      }
+    }
+    gdn::lds_barrier();
+  }
+
+  if (ihT) {
+    // lane indices re-derived here, so none of the loop's is kept live across it
+    int tid_l = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tid_l));
+    const int le = tid_l & 31, ge = (tid_l >> 5) & 1;
+    float* hp = ihT + static_cast<int64_t>(h) * D * D + vc0 + le;
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          hp[static_cast<int64_t>(qswap(32 * rt + 8 * i + 4 * ge + rr)) * D] = S[rt][4 * i + rr];
+  }
+}
+
+
 
 // grid = 8 * ceil(n_items * Hv / 8) * NCB, NCB = D / 64; block = 64 * 8.
 // Workgroup (item: sequence r or a segment of it, value head h, column block cb) owns state columns
@@ -1366,21 +1533,11 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       if (roll) GDN_ROLL();
       return;
     }
-    // roles with nothing to do for this item keep the chain's barrier count
-    // (one before the first chunk, one per chunk)
-    if ((wave < 4 && mode != kSegOut) || (wave >= 6 && mode == kSegTransition)) {
-      if (wave >= 6) {
-        // a transition item runs with U = 0: the U waves clear their tile in
-        // both stages once, and nothing else writes it
-        const int c = wave - 6;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int qd = 0; qd < 4; ++qd) sm.st[b].U[c][mt][qd][lane] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      }
-      for (int64_t i = 0; i <= nch; ++i) gdn::lds_barrier();
+    if (wave < 4 && mode == kSegBoth) {
+      // the segment's transition P on the output waves: the chain of column
+      // tile wave - 2 from the identity's columns, with U = 0 (one barrier
+      // before the first chunk and one per chunk, like every role)
+      chain_pass<D, true>(sm, wave - 2, cb * kCB + 32 * (wave - 2), nch, true, nullptr, segs.it[item].hP, h, lane);
       return;
     }
     if (wave < 4) {
@@ -1552,149 +1709,8 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #undef GDN_LEN
 
   // -------------------------------------------------------------- chain --
-  const int vc0 = cb * kCB + 32 * wave;  // first state column of this wave
-  f32x16_t S[NR];
-  if (mode == kSegTransition) {
-    // the identity's columns vc0 + li (row position p holds key qswap(p))
-#pragma unroll
-    for (int rt = 0; rt < NR; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          S[rt][4 * i + rr] = qswap(32 * rt + 8 * i + 4 * g + rr) == vc0 + li ? 1.f : 0.f;
-  } else if (ih0) {
-    const float* hp = ih0 + static_cast<int64_t>(h) * D * D + vc0 + li;
-#pragma unroll
-    for (int rt = 0; rt < NR; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          S[rt][4 * i + rr] = hp[static_cast<int64_t>(qswap(32 * rt + 8 * i + 4 * g + rr)) * D];
-  } else {
-#pragma unroll
-    for (int rt = 0; rt < NR; ++rt) S[rt] = zero16();
-  }
-  if (nch > 0) gdn::lds_barrier();
-  for (int64_t jc = 0; jc < nch; ++jc) {
-    const StateStage<D>& B = sm.st[jc & 1];
-    StateXchgV& X = sm.xv[jc & 1];
-    // Re-derive lane indices from an opaque copy each chunk so the compiler
-    // does not keep every lane-dependent address live across the loop.
-    int tid_l = static_cast<int>(threadIdx.x);
-    asm volatile("" : "+v"(tid_l));
-    const int ln = tid_l & 63;
-
-    // Operand fragments of each product are read from LDS as one batch ahead
-    // of its MFMAs, so the reads overlap each other instead of each MFMA
-    // waiting out an LDS latency: first the U tiles that the first products
-    // accumulate onto, then -W in k-step order.
-    f32x16_t U[2];
-    h16x8_t wf[2][KS];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4_t u4 = B.U[wave][mt][qd][ln];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = u4[rr];
-      }
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      wf[0][s] = B.W[s][ln];
-      wf[1][s] = B.W[KS + s][ln];
-    }
-    const float eg = B.vec[2 * kC];
-    __builtin_amdgcn_sched_barrier(0);
-    // S as fp16 fragments (B operand of W S here, A operand of the output
-    // wave's S^T Q'^T), packed while the reads are in flight.  Vn = U + (-W) S
-    // with both 32-token tiles interleaved; tile 1's last product is issued
-    // after the fence below, so tile 0 is packed while it runs.
-    h16x8_t Sh[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) Sh[s] = (s & 1) ? pack_h8<8>(S[s >> 1]) : pack_h8<0>(S[s >> 1]);
-#pragma unroll
-    for (int s = 0; s < KS - 1; ++s) {
-      U[0] = mfma32(wf[0][s], Sh[s], U[0]);
-      U[1] = mfma32(wf[1][s], Sh[s], U[1]);
-    }
-    U[0] = mfma32(wf[0][KS - 1], Sh[KS - 1], U[0]);
-    // the exchange copy of S (then the flag that says it is there), the decay
-    // of the old state and the update's operand reads, while W S runs
-#pragma unroll
-    for (int s = 0; s < KS; ++s) sm.xs.Sh[wave][s][ln] = Sh[s];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    if (ln == 0) __hip_atomic_store(&sm.sflag[wave], static_cast<int>(jc) + 1, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_WORKGROUP);
-#pragma unroll
-    for (int rt = 0; rt < NR; ++rt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) S[rt][e] *= eg;
-    h16x8_t kf[NR][4];
-#pragma unroll
-    for (int rt = 0; rt < NR; ++rt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kf[rt][s] = B.Kt[rt * 4 + s][ln];
-    // cK of the tokens 32 mt + 8 i + 4 lgp + r held by this lane's Vn elements
-    f32x4_t ck[2][4];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ck[mt][i] = *reinterpret_cast<const f32x4_t*>(&B.vec[kC + 32 * mt + 8 * i + 4 * (ln >> 5)]);
-    __builtin_amdgcn_sched_barrier(0);
-    U[1] = mfma32(wf[1][KS - 1], Sh[KS - 1], U[1]);
-    // S <- e^gamma S + K^T diag(cK) Vn, one token tile at a time: Vn as fp16
-    // (A operand of Vn^T A^T, to the exchange) and diag(cK) Vn as fp16 (B
-    // operand of the update); tile 1 is packed while tile 0's products run.
-    // The exchange gets Vn as its fp16 rounding Vh and the rounding's
-    // residual Vl, formed while the update's products run.
-    h16x8_t Vh[4], Vk[4];
-    f32x16_t Uk[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      Vh[2 * mt] = pack_h8<0>(U[mt]);
-      Vh[2 * mt + 1] = pack_h8<8>(U[mt]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Uk[mt][4 * i + r] = U[mt][4 * i + r] * ck[mt][i][r];
-      Vk[2 * mt] = pack_h8<0>(Uk[mt]);
-      Vk[2 * mt + 1] = pack_h8<8>(Uk[mt]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s = 2 * mt; s < 2 * mt + 2; ++s)
-#pragma unroll
-        for (int rt = 0; rt < NR; ++rt) S[rt] = mfma32(kf[rt][s], Vk[s], S[rt]);
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4_t hi = __builtin_bit_cast(u32x4_t, Vh[s]);
-      u32x4_t lo;
-#pragma unroll
-      for (int p2 = 0; p2 < 4; ++p2) {
-        const int e = 8 * (s & 1) + 2 * p2;
-        lo[p2] = f2h2_lo(U[s >> 1][e], U[s >> 1][e + 1], hi[p2]);
-      }
-      X.Vh[wave][s][ln] = Vh[s];
-      X.Vl[wave][s][ln] = __builtin_bit_cast(h16x8_t, lo);
-    }
-    gdn::lds_barrier();
-  }
-
-  if (ihT) {
-    float* hp = ihT + static_cast<int64_t>(h) * D * D + vc0 + li;
-#pragma unroll
-    for (int rt = 0; rt < NR; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          hp[static_cast<int64_t>(qswap(32 * rt + 8 * i + 4 * g + rr)) * D] = S[rt][4 * i + rr];
-  }
+  chain_pass<D, false>(sm, wave, cb * kCB + 32 * wave, nch, false, ih0, ihT, h, lane);
 }
-
 // ---- segment scan ----
 // For each split sequence: S_1 = the first segment's final state, then
 // S_{s+1} = P_s S_s + R_s for its middle segments s = 1 .. m, in fp32 (the
@@ -1836,14 +1852,14 @@ inline SegPlan plan_segments(const int64_t* cu_host, const uint8_t* select_host,
       L = static_cast<int>((nch + S - 1) / S);
       S = static_cast<int>((nch + L - 1) / L);  // no empty last segment
     }
-    if (S >= 2 && (chains + (S >= 3) > kMaxChains || pass1 + 2 * S - 3 > kMaxSegItems ||
+    if (S >= 2 && (chains + (S >= 3) > kMaxChains || pass1 + S - 1 > kMaxSegItems ||
                    pass3 + S - 1 > kMaxSegItems))
       S = 1;
     if (S < 2) {
       S = 1;
       pass1 += 1;
     } else {
-      pass1 += 2 * S - 3;
+      pass1 += S - 1;
       pass3 += S - 1;
       chains += S >= 3;
       pl.any = true;
@@ -1903,7 +1919,8 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   p3.n = 0;
   ScanList sc;
   sc.n = 0;
-  auto item = [](int r, int64_t a, int64_t b, int mode, int ph0, int phT, const float* i0, float* iT) {
+  auto item = [](int r, int64_t a, int64_t b, int mode, int ph0, int phT, const float* i0, float* iT,
+                 float* iP = nullptr) {
     SegItem it;
     it.r = r;
     it.c0 = static_cast<int>(a);
@@ -1913,6 +1930,7 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
     it.pool_hT = phT;
     it.h0 = i0;
     it.hT = iT;
+    it.hP = iP;
     return it;
   };
   for (int r = 0; r < n_seqs; ++r) {
@@ -1930,10 +1948,8 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
     float* R = P + m * hs;
     scratch = R + m * hs;
     p1.it[p1.n++] = item(r, 0, L, kSegOut, 1, 0, nullptr, Sst);
-    for (int s = 1; s <= m; ++s) {
-      p1.it[p1.n++] = item(r, s * L, (s + 1) * L, kSegState, 0, 0, nullptr, R + (s - 1) * hs);
-      p1.it[p1.n++] = item(r, s * L, (s + 1) * L, kSegTransition, 0, 0, nullptr, P + (s - 1) * hs);
-    }
+    for (int s = 1; s <= m; ++s)
+      p1.it[p1.n++] = item(r, s * L, (s + 1) * L, kSegBoth, 0, 0, nullptr, R + (s - 1) * hs, P + (s - 1) * hs);
     for (int s = 1; s < S; ++s)
       p3.it[p3.n++] = item(r, s * L, std::min<int64_t>((s + 1) * L, nch), kSegOut, 0, s == S - 1, Sst + (s - 1) * hs,
                            nullptr);
