@@ -139,7 +139,9 @@ __device__ __forceinline__ f32x4_t mfma16x16x4f32(float a, float b, const f32x4_
 __device__ __forceinline__ float norm_gate(float x, float r, float w, float z) {
   const float n = bf2f(f2bf(x * r));
   const float wn = bf2f(f2bf(w * n));
-  const float d = 1.0f + exp_acc(fminf(-z, 88.0f));
+  // (0 - z rather than -z: a subtraction's result needs no canonicalising
+  // before the min; exp of +0 and -0 are the same)
+  const float d = 1.0f + exp_acc(fminf(0.0f - z, 88.0f));
   float rc = __builtin_amdgcn_rcpf(d);
   rc = fmaf(rc, fmaf(-d, rc, 1.0f), rc);
   return wn * (z * rc);

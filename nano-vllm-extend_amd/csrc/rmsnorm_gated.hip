@@ -3,7 +3,9 @@
 //   n  = bf16(x * rsqrt(mean(x^2) + eps))      (fp32 math)
 //   wn = bf16(w * n)                           (bf16 x bf16 product)
 //   y  = bf16(float(wn) * silu(float(z)))
-// HBM-bound: 3 * D * 2 bytes per row.  D/8 lanes per row, 16-byte vectors.
+// 3 * D * 2 bytes per row, but bound by the vector ALUs in practice: the
+// exact SiLU is most of the ~30 instructions per element.  D/8 lanes per
+// row, 16-byte vectors.
 #include "gdn_common.h"
 
 namespace {
@@ -15,16 +17,18 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const uint16_t* __re
                                                             int64_t sz_tok,
                                                             const uint16_t* __restrict__ w,
                                                             uint16_t* __restrict__ y,
-                                                            int64_t rows, int H, float eps,
+                                                            int64_t n_sel, int H, float eps,
                                                             const int64_t* __restrict__ ranges, int n_ranges,
                                                             int64_t n_tok) {
+  // block (x, y) = kRowsPerBlock consecutive selected tokens of head y: the
+  // row's token and head need no division
   constexpr int kLanes = D / 8;                 // lanes per row
   constexpr int kRowsPerBlock = 256 / kLanes;
   const int lane = threadIdx.x % kLanes;
-  const int64_t r_sel = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
-  bool active = r_sel < rows;
-  int64_t tok = active ? r_sel / H : 0;
-  const int h = active ? static_cast<int>(r_sel % H) : 0;
+  const int h = blockIdx.y;
+  const int64_t t_sel = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
+  bool active = t_sel < n_sel;
+  int64_t tok = active ? t_sel : 0;
   if (ranges && active) {
     // token ranges (start, count, tokens before it): the t-th selected token;
     // a token that no range holds, or that falls outside the n_tok rows, is
@@ -92,16 +96,16 @@ extern "C" int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16
       (reinterpret_cast<uintptr_t>(z) % 16) || (reinterpret_cast<uintptr_t>(w) % 16) ||
       (reinterpret_cast<uintptr_t>(y) % 16))
     return GDN_ERR_INVALID_ARG;
-  const int64_t rows = n_tok * H;
+  if (H > 65535) return GDN_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128) {
-    const int64_t nb = (rows + 15) / 16;
-    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                     nullptr, 0, n_tok);
+    const int64_t nb = (n_tok + 15) / 16;
+    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, n_tok,
+                                                                                        H, eps, nullptr, 0, n_tok);
   } else {
-    const int64_t nb = (rows + 31) / 32;
-    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                    nullptr, 0, n_tok);
+    const int64_t nb = (n_tok + 31) / 32;
+    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, n_tok,
+                                                                                       H, eps, nullptr, 0, n_tok);
   }
   return gdn_launch_status();
 }
@@ -117,16 +121,16 @@ extern "C" int gdn_rmsnorm_gated_ranges(const uint16_t* x, int64_t sx_tok, const
       (reinterpret_cast<uintptr_t>(z) % 16) || (reinterpret_cast<uintptr_t>(w) % 16) ||
       (reinterpret_cast<uintptr_t>(y) % 16))
     return GDN_ERR_INVALID_ARG;
-  const int64_t rows = n_sel_tok * H;
+  if (H > 65535) return GDN_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128) {
-    const int64_t nb = (rows + 15) / 16;
-    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                     ranges, n_ranges, n_tok);
+    const int64_t nb = (n_sel_tok + 15) / 16;
+    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(
+        x, sx_tok, z, sz_tok, w, y, n_sel_tok, H, eps, ranges, n_ranges, n_tok);
   } else {
-    const int64_t nb = (rows + 31) / 32;
-    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, rows, H, eps,
-                                                                                    ranges, n_ranges, n_tok);
+    const int64_t nb = (n_sel_tok + 31) / 32;
+    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(
+        x, sx_tok, z, sz_tok, w, y, n_sel_tok, H, eps, ranges, n_ranges, n_tok);
   }
   return gdn_launch_status();
 }
