@@ -20,13 +20,15 @@ __global__ __launch_bounds__(256) void rmsnorm_gated_kernel(const uint16_t* __re
                                                             int64_t n_sel, int H, float eps,
                                                             const int64_t* __restrict__ ranges, int n_ranges,
                                                             int64_t n_tok) {
-  // block (x, y) = kRowsPerBlock consecutive selected tokens of head y: the
-  // row's token and head need no division
+  // block b = kRowsPerBlock consecutive selected tokens (block b / H) of head
+  // b % H: the division is the block's, in scalar registers, and the H blocks
+  // of a token block run side by side over one contiguous stretch of rows
   constexpr int kLanes = D / 8;                 // lanes per row
   constexpr int kRowsPerBlock = 256 / kLanes;
   const int lane = threadIdx.x % kLanes;
-  const int h = blockIdx.y;
-  const int64_t t_sel = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanes;
+  const uint32_t b = blockIdx.x;
+  const int h = static_cast<int>(b % static_cast<uint32_t>(H));
+  const int64_t t_sel = static_cast<int64_t>(b / static_cast<uint32_t>(H)) * kRowsPerBlock + threadIdx.x / kLanes;
   bool active = t_sel < n_sel;
   int64_t tok = active ? t_sel : 0;
   if (ranges && active) {
@@ -96,15 +98,15 @@ extern "C" int gdn_rmsnorm_gated(const uint16_t* x, int64_t sx_tok, const uint16
       (reinterpret_cast<uintptr_t>(z) % 16) || (reinterpret_cast<uintptr_t>(w) % 16) ||
       (reinterpret_cast<uintptr_t>(y) % 16))
     return GDN_ERR_INVALID_ARG;
-  if (H > 65535) return GDN_ERR_UNSUPPORTED;
+  if ((n_tok + 15) / 16 * H >= (1LL << 32)) return GDN_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128) {
     const int64_t nb = (n_tok + 15) / 16;
-    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, n_tok,
+    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb * H)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, n_tok,
                                                                                         H, eps, nullptr, 0, n_tok);
   } else {
     const int64_t nb = (n_tok + 31) / 32;
-    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, n_tok,
+    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb * H)), dim3(256), 0, s>>>(x, sx_tok, z, sz_tok, w, y, n_tok,
                                                                                        H, eps, nullptr, 0, n_tok);
   }
   return gdn_launch_status();
@@ -121,15 +123,15 @@ extern "C" int gdn_rmsnorm_gated_ranges(const uint16_t* x, int64_t sx_tok, const
       (reinterpret_cast<uintptr_t>(z) % 16) || (reinterpret_cast<uintptr_t>(w) % 16) ||
       (reinterpret_cast<uintptr_t>(y) % 16))
     return GDN_ERR_INVALID_ARG;
-  if (H > 65535) return GDN_ERR_UNSUPPORTED;
+  if ((n_sel_tok + 15) / 16 * H >= (1LL << 32)) return GDN_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128) {
     const int64_t nb = (n_sel_tok + 15) / 16;
-    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(
+    rmsnorm_gated_kernel<128><<<dim3(static_cast<unsigned>(nb * H)), dim3(256), 0, s>>>(
         x, sx_tok, z, sz_tok, w, y, n_sel_tok, H, eps, ranges, n_ranges, n_tok);
   } else {
     const int64_t nb = (n_sel_tok + 31) / 32;
-    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb), H), dim3(256), 0, s>>>(
+    rmsnorm_gated_kernel<64><<<dim3(static_cast<unsigned>(nb * H)), dim3(256), 0, s>>>(
         x, sx_tok, z, sz_tok, w, y, n_sel_tok, H, eps, ranges, n_ranges, n_tok);
   }
   return gdn_launch_status();
