@@ -262,7 +262,10 @@ int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t*
  * (:546-558) ahead of recurrent_gdn_inplace (:597-613) in the T == 1 branch
  * (:1008-1030), with the same results bit for bit.
  *   q, k   the decode conv's q and k outputs (gdn_conv_decode over the first
- *          2*Hk*D channels), row strides sq_b, sk_b, head dim contiguous
+ *          2*Hk*D channels), row strides sq_b, sk_b, head dim contiguous; or
+ *          both NULL with Hk == Hv: the q and k channels' decode conv and
+ *          their conv-state roll run in the kernel too (whole heads per
+ *          workgroup), the same bits as gdn_conv_decode on them first
  *   x      [B, C] raw rows (C = 2*Hk*D + Hv*D), row stride sx_row (multiple of 4)
  *   conv_pool, cp_slot, cp_ch, conv_w: as gdn_conv_decode with K = 4, over all
  *          C channels (only the v channels are read and rolled here)
@@ -276,7 +279,8 @@ int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t*
  *          The kernel then runs whole heads per workgroup, as it does without
  *          z from B*Hv >= 2048; below that it otherwise splits a head's
  *          columns over workgroups, which sums S^T k in another order
- * One launch; each v channel belongs to one workgroup, which rolls its taps.
+ * One launch; each v channel (and with q == k == NULL each q and k channel)
+ * belongs to one workgroup, which rolls its taps.
  */
 int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const uint16_t* k, int64_t sk_b,
                                const uint16_t* x, int64_t sx_row, uint16_t* conv_pool, int64_t cp_slot,

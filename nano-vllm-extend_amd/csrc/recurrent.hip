@@ -51,6 +51,14 @@ struct DecodeIn {
   const void* A_log;       // [Hv], bf16 or fp32 (param_f32)
   const void* dt_bias;
   int param_f32;
+  // q and k from their raw channels too (NULL: from the q / k arguments):
+  // the decode conv of head kh's q and k channels and their roll, by wave 0.
+  // Only with Hk == Hv and whole heads per workgroup, so each of these
+  // channels belongs to one workgroup as well.
+  const uint16_t* xqk;     // raw rows at channel 0, row stride sx
+  uint16_t* qkpool;        // conv state pool at channel 0 (sp_slot, sp_ch)
+  const uint16_t* wqk;     // [C, 4] conv taps from channel 0
+  int key_dim;             // Hk * D: the first k channel
 };
 
 // Gated RMSNorm on the output (fused decode step, whole heads per workgroup):
@@ -111,6 +119,24 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   // byte offset of this lane's float4 in the tile, and of row pass j
   const int voff = (r0 * D + col) * 4;
   constexpr int kPass = RPP * D * 4;
+  // q/k conv in the kernel (one token): wave 0's raw inputs, taps and weights,
+  // loaded ahead of the state tile so their latency overlaps its loads
+  constexpr int QE = D / 64;  // channels per lane and part
+  uint16_t qx[2][QE], qs[2][QE][3];
+  uint2 qw[2][QE];
+  if (kFused && din.xqk && wave == 0) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int e = 0; e < QE; ++e) {
+        const int64_t c = (p ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + lane * QE + e;
+        qx[p][e] = din.xqk[static_cast<int64_t>(b) * din.sx + c];
+        const uint16_t* sp = din.qkpool + row * din.sp_slot + c * din.sp_ch;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) qs[p][e][j] = sp[j];
+        qw[p][e] = *reinterpret_cast<const uint2*>(din.wqk + c * 4);
+      }
+  }
   float4 S[NP];
   {
     const __amdgpu_buffer_rsrc_t r = tile_rsrc(sin);
@@ -127,12 +153,40 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
       const uint16_t* kp = k + static_cast<int64_t>(b) * sk_b + static_cast<int64_t>(t) * sk_t + static_cast<int64_t>(kh) * D;
       float qf[E], kf[E];
       float qq = 0.f, kk = 0.f;
+      if (kFused && din.xqk) {
+        // the decode conv of this lane's q and k channels (the conv kernel's
+        // arithmetic, its output rounded to bf16), then their roll (bit copies;
+        // this lane alone reads these taps).  One token: the inputs loaded
+        // before the state tile.
+        static_assert(E == QE, "q/k channels per lane");
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        qf[e] = gdn::bf2f(qp[lane * E + e]);
-        kf[e] = gdn::bf2f(kp[lane * E + e]);
-        qq += qf[e] * qf[e];
-        kk += kf[e] * kf[e];
+        for (int e = 0; e < E; ++e)
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const int64_t c = (p ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + lane * E + e;
+            uint16_t* sp = din.qkpool + row * din.sp_slot + c * din.sp_ch;
+            const uint16_t* wsv = reinterpret_cast<const uint16_t*>(&qw[p][e]);
+            const float wk[4] = {gdn::bf2f(wsv[0]), gdn::bf2f(wsv[1]), gdn::bf2f(wsv[2]), gdn::bf2f(wsv[3])};
+            const float y = gdn::bf2f(gdn::f2bf(gdn::conv_decode_silu(
+                gdn::bf2f(qx[p][e]), gdn::bf2f(qs[p][e][0]), gdn::bf2f(qs[p][e][1]), gdn::bf2f(qs[p][e][2]), wk)));
+            sp[0] = qs[p][e][1];
+            sp[1] = qs[p][e][2];
+            sp[2] = qx[p][e];
+            if (p) kf[e] = y; else qf[e] = y;
+          }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          qq += qf[e] * qf[e];
+          kk += kf[e] * kf[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          qf[e] = gdn::bf2f(qp[lane * E + e]);
+          kf[e] = gdn::bf2f(kp[lane * E + e]);
+          qq += qf[e] * qf[e];
+          kk += kf[e] * kf[e];
+        }
       }
       qq = gdn::wave_sum(qq);
       kk = gdn::wave_sum(kk);
@@ -439,8 +493,11 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
   if (B < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
   if (B == 0) return GDN_OK;
-  if (!q || !k || !x || !conv_pool || !conv_w || !a || !b || !A_log || !dt_bias || !s_pool || !ids || !o)
+  if (!x || !conv_pool || !conv_w || !a || !b || !A_log || !dt_bias || !s_pool || !ids || !o)
     return GDN_ERR_INVALID_ARG;
+  // q == k == NULL: their conv in the kernel as well (one key head per value head)
+  const bool qk_fused = !q && !k;
+  if ((!q || !k) && !(qk_fused && Hk == Hv)) return GDN_ERR_INVALID_ARG;
   const int64_t vbase = 2LL * Hk * D;  // first v channel of a raw row
   // float4 state access; 8-byte raw v and 16-byte tap reads
   if (s_stride % 4 || reinterpret_cast<uintptr_t>(s_pool) % 16 || sx_row % 4 ||
@@ -452,11 +509,24 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
   if (z && (!norm_w || sz_b % 4 || sz_b < static_cast<int64_t>(Hv) * D || reinterpret_cast<uintptr_t>(z) % 8 ||
             reinterpret_cast<uintptr_t>(norm_w) % 8))
     return GDN_ERR_INVALID_ARG;
-  const DecodeIn din{x + vbase, sx_row, conv_pool + vbase * cp_ch, cp_slot, cp_ch, conv_w + vbase * 4, a, b,
-                     A_log, dt_bias, param_is_fp32 ? 1 : 0};
+  const DecodeIn din{x + vbase,
+                     sx_row,
+                     conv_pool + vbase * cp_ch,
+                     cp_slot,
+                     cp_ch,
+                     conv_w + vbase * 4,
+                     a,
+                     b,
+                     A_log,
+                     dt_bias,
+                     param_is_fp32 ? 1 : 0,
+                     qk_fused ? x : nullptr,
+                     conv_pool,
+                     conv_w,
+                     Hk * D};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // the norm needs a head's D outputs in one workgroup
-  const int nvb = z ? 1 : recurrent_nvb(B, Hv);
+  // the norm, and the q/k conv, need a head's D columns in one workgroup
+  const int nvb = z || qk_fused ? 1 : recurrent_nvb(B, Hv);
   const NormIn nin{z, sz_b, norm_w, eps};
   const SrcIn src{};
 #define GDN_REC_ARGS q, sq_b, 0, k, sk_b, 0, nullptr, 0, 0, nullptr, nullptr, s_pool, s_stride, s_pool, s_stride, \

@@ -195,6 +195,14 @@ class GatedDeltaNetCore:
         Hk, Hv, D = self.Hk, self.Hv, self.D
         kd = self.key_dim
         if self.sw.fused_decode and self.sw.gbeta and self.sw.conv_kernel and self.sw.inplace and self.K == 4:
+            if Hk == Hv and B * Hv >= ops.WHOLE_HEAD_TILES:
+                # the whole step in one kernel: q/k/v conv, gates, recurrent
+                # update and gated norm (the same results as the calls below)
+                with self._timed("recurrent_decode"):
+                    out = ops.recurrent_decode_fused(None, mixed, conv_cache, self.conv_w, b, a, self.A_log,
+                                                     self.dt_bias, s_cache, ids, Hk, Hv, D, z=z,
+                                                     norm_weight=self.norm_w, eps=self.eps)
+                return out.view(B, Hv, D)
             # q/k conv, then gates + v conv + recurrent update + gated norm in
             # one kernel (the same results as the calls below)
             with self._timed("conv_decode"):

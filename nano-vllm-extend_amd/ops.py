@@ -597,14 +597,25 @@ def recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bi
     output: in the same kernel when B * Hv >= WHOLE_HEAD_TILES (the kernel
     runs whole heads then anyway), else as a second launch (fuse_norm=True
     forces the one-kernel form, whose core output is then the whole-head
-    kernel's)."""
+    kernel's).
+
+    qk=None (Hk == Hv only): the q and k channels' decode conv runs in the
+    kernel as well, their conv states rolled there (the whole step in one
+    launch, whole heads per workgroup); the same bits as conv_decode_step on
+    those channels followed by the call above with its output."""
     dev = _check_cuda(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bias, s_pool, ids, z, norm_weight)
     for t, nm in ((qk, "qk"), (mixed, "mixed"), (conv_pool, "conv_pool"), (b, "b"), (a, "a")):
-        _bf16(t, nm)
+        if t is not None:
+            _bf16(t, nm)
     B, C = mixed.shape
     kd = Hk * D
-    assert C == 2 * kd + Hv * D and qk.shape == (B, 2 * kd)
-    assert qk.stride(1) == 1 and mixed.stride(1) == 1 and conv_pool.stride(2) == 1
+    assert C == 2 * kd + Hv * D
+    if qk is None:
+        assert Hk == Hv, "the q/k conv runs in the decode kernel only with one key head per value head"
+        fuse_norm = True   # whole heads per workgroup in any case
+    else:
+        assert qk.shape == (B, 2 * kd) and qk.stride(1) == 1
+    assert mixed.stride(1) == 1 and conv_pool.stride(2) == 1
     w = conv_weight.reshape(C, -1)
     assert w.shape[1] == 4
     w = w.contiguous()
@@ -631,7 +642,8 @@ def recurrent_decode_fused(qk, mixed, conv_pool, conv_weight, b, a, a_log, dt_bi
     out = torch.empty(B, 1, Hv, D, dtype=mixed.dtype, device=mixed.device)
     if scale is None:
         scale = D ** -0.5
-    _lib.call("gdn_recurrent_decode_fused", _lib.ptr(qk), qk.stride(0), _lib.ptr(qk[:, kd:]), qk.stride(0),
+    q_ptr, k_ptr, sqk = (None, None, 0) if qk is None else (_lib.ptr(qk), _lib.ptr(qk[:, kd:]), qk.stride(0))
+    _lib.call("gdn_recurrent_decode_fused", q_ptr, sqk, k_ptr, sqk,
               _lib.ptr(mixed), mixed.stride(0), _lib.ptr(conv_pool), conv_pool.stride(0), conv_pool.stride(1),
               _lib.ptr(w), _lib.ptr(a), _lib.ptr(b), _lib.ptr(a_log), _lib.ptr(dt_bias),
               int(a_log.dtype == torch.float32), _lib.ptr(s_pool), s_pool.stride(0), _lib.ptr(ids64),

@@ -138,3 +138,47 @@ def test_fused_decode_norm_epilogue_small_batch_vs_oracle(pkg, dev):
     assert_out(y.cpu().view(B, Hv, D), ref, "in-kernel norm output", ulps=4)
     assert_state(sp.cpu()[ids], rs, "fused decode state")
     assert torch.equal(cp.cpu().view(torch.int16), rpool.view(torch.int16)), "conv pool"
+
+
+# (B * Hv below the whole-head threshold only with the norm: the reference
+# call then runs whole heads too, as the qk=None kernel always does)
+@pytest.mark.parametrize("Hk,Hv,D,B,slots,with_norm",
+                         [(16, 16, 128, 130, 140, False), (16, 16, 128, 130, 140, True),
+                          (8, 8, 64, 260, 270, False), (8, 8, 64, 260, 270, True), (4, 4, 128, 3, 6, True)],
+                         ids=lambda c: str(c))
+def test_fused_decode_with_qk_conv(pkg, dev, Hk, Hv, D, B, slots, with_norm):
+    """qk=None: the q/k channels' decode conv and roll run in the decode kernel
+    too (one launch for the whole step).  Bit-equal to conv_decode_step on the
+    q/k channels followed by the fused call with its output, in the whole-head
+    form the kernel then runs; conv pools equal over all channels, other
+    slots untouched."""
+    ops = pkg.ops
+    mixed, conv_w, A_log, dt_bias, a, b, conv_pool, s_pool, ids = (
+        t.to(dev) for t in _case(63, Hk, Hv, D, B, slots, False))
+    kd = Hk * D
+    gen = torch.Generator().manual_seed(64)
+    z = torch.randn(B, Hv * D, generator=gen).to(BF16).to(dev) if with_norm else None
+    nw = (1.0 + 0.1 * torch.randn(D, generator=gen)).to(BF16).to(dev) if with_norm else None
+    cp1, sp1 = conv_pool.clone(), s_pool.clone()
+    qk = ops.conv_decode_step(mixed[:, :2 * kd], cp1[:, :2 * kd], ids, conv_w[:2 * kd])
+    o1 = ops.recurrent_decode_fused(qk, mixed, cp1, conv_w, b, a, A_log, dt_bias, sp1, ids, Hk, Hv, D, z=z,
+                                    norm_weight=nw, fuse_norm=True)
+    cp2, sp2 = conv_pool.clone(), s_pool.clone()
+    o2 = ops.recurrent_decode_fused(None, mixed, cp2, conv_w, b, a, A_log, dt_bias, sp2, ids, Hk, Hv, D, z=z,
+                                    norm_weight=nw)
+    torch.cuda.synchronize()
+    assert torch.equal(o2.view(torch.int16), o1.view(torch.int16)), "outputs differ"
+    assert torch.equal(sp2, sp1), "state pool differs"
+    assert torch.equal(cp2.view(torch.int16), cp1.view(torch.int16)), "conv pool differs"
+    untouched = [i for i in range(slots) if i not in ids.tolist()]
+    assert torch.equal(cp2[untouched].view(torch.int16), conv_pool[untouched].view(torch.int16))
+    assert torch.equal(sp2[untouched], s_pool[untouched])
+
+
+def test_fused_decode_qk_conv_needs_one_key_head_per_value_head(pkg, dev):
+    """qk=None with GVA (Hk < Hv) is refused before any launch."""
+    Hk, Hv, D, B, slots = 2, 4, 64, 3, 5
+    mixed, conv_w, A_log, dt_bias, a, b, conv_pool, s_pool, ids = (
+        t.to(dev) for t in _case(65, Hk, Hv, D, B, slots, False))
+    with pytest.raises(AssertionError):
+        pkg.ops.recurrent_decode_fused(None, mixed, conv_pool, conv_w, b, a, A_log, dt_bias, s_pool, ids, Hk, Hv, D)
