@@ -93,7 +93,11 @@ def _fused_decode_method(orig):
         proj = self.in_proj_qkv(x).reshape(-1, self.conv_dim)
         w = self.conv1d.weight.view(self.conv_dim, 4)
         kd = self.key_dim
-        qk = ops.conv_decode_step(proj[:, :2 * kd], self.conv_cache[:, :2 * kd], ids, w[:2 * kd])
+        # one key head per value head and whole heads per workgroup: the q/k
+        # conv runs in the decode kernel too; else as its own launch first
+        qk = None
+        if not (self.num_k_heads == Hv and n * Hv >= ops.WHOLE_HEAD_TILES):
+            qk = ops.conv_decode_step(proj[:, :2 * kd], self.conv_cache[:, :2 * kd], ids, w[:2 * kd])
         # gates + v conv + in-place update + the gated norm (self.norm's
         # weight and eps) in one kernel
         core = ops.recurrent_decode_fused(qk, proj, self.conv_cache, w, b, a, A_log, dt_bias, self.s_cache, ids,
