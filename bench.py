@@ -388,8 +388,12 @@ def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, 
     other = [i for i in range(s_pool.shape[0]) if i not in used][:B]
     sets = [ids, torch.tensor(other, device=ids.device)] if len(other) == B else [ids]
     if core.sw.fused_decode:
-        # the kernel the decode step runs: gates + v conv + state update
-        qk = pkg.ops.conv_decode_step(x[:, :2 * kd], conv_pool[:, :2 * kd], ids, core.conv_w[:2 * kd])
+        # the kernel the decode step runs: the whole step (q/k/v conv, gates,
+        # state update, norm) with one key head per value head and whole heads
+        # per workgroup, else gates + v conv + state update after the q/k conv
+        whole = Hk == Hv and B * Hv >= pkg.ops.WHOLE_HEAD_TILES
+        qk = None if whole else pkg.ops.conv_decode_step(x[:, :2 * kd], conv_pool[:, :2 * kd], ids,
+                                                           core.conv_w[:2 * kd])
 
         zz = z_rows
 

@@ -119,23 +119,20 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   // byte offset of this lane's float4 in the tile, and of row pass j
   const int voff = (r0 * D + col) * 4;
   constexpr int kPass = RPP * D * 4;
-  // q/k conv in the kernel (one token): wave 0's raw inputs, taps and weights,
-  // loaded ahead of the state tile so their latency overlaps its loads
-  constexpr int QE = D / 64;  // channels per lane and part
-  uint16_t qx[2][QE], qs[2][QE][3];
-  uint2 qw[2][QE];
-  if (kFused && din.xqk && wave == 0) {
+  // q/k conv in the kernel (one token): thread t convolves channel t % 128 of
+  // q (t < 128) or k; its raw input, taps and weights are loaded ahead of the
+  // state tile so their latency overlaps the tile's loads
+  const int qpart = tid >> 7, qci = tid & 127;
+  const bool qact = kFused && din.xqk && qci < D;
+  const int64_t qch = (qpart ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + qci;
+  uint16_t qx = 0, qs[3] = {0, 0, 0};
+  uint2 qw = make_uint2(0u, 0u);
+  if (qact) {
+    qx = din.xqk[static_cast<int64_t>(b) * din.sx + qch];
+    const uint16_t* sp = din.qkpool + row * din.sp_slot + qch * din.sp_ch;
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int e = 0; e < QE; ++e) {
-        const int64_t c = (p ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + lane * QE + e;
-        qx[p][e] = din.xqk[static_cast<int64_t>(b) * din.sx + c];
-        const uint16_t* sp = din.qkpool + row * din.sp_slot + c * din.sp_ch;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) qs[p][e][j] = sp[j];
-        qw[p][e] = *reinterpret_cast<const uint2*>(din.wqk + c * 4);
-      }
+    for (int j = 0; j < 3; ++j) qs[j] = sp[j];
+    qw = *reinterpret_cast<const uint2*>(din.wqk + qch * 4);
   }
   float4 S[NP];
   {
@@ -146,6 +143,23 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
 
   for (int t = 0; t < T; ++t) {
     const int buf = t & 1;
+    if (kFused && din.xqk) {
+      // the decode conv of this thread's q or k channel (the conv kernel's
+      // arithmetic, its output rounded to bf16) into sq / sk, then its roll
+      // (bit copies; this thread alone reads these taps).  One token.
+      if (qact) {
+        const uint16_t* wsv = reinterpret_cast<const uint16_t*>(&qw);
+        const float wk[4] = {gdn::bf2f(wsv[0]), gdn::bf2f(wsv[1]), gdn::bf2f(wsv[2]), gdn::bf2f(wsv[3])};
+        const float y = gdn::bf2f(gdn::f2bf(
+            gdn::conv_decode_silu(gdn::bf2f(qx), gdn::bf2f(qs[0]), gdn::bf2f(qs[1]), gdn::bf2f(qs[2]), wk)));
+        (qpart ? sk : sq)[buf][qci] = y;
+        uint16_t* sp = din.qkpool + row * din.sp_slot + qch * din.sp_ch;
+        sp[0] = qs[1];
+        sp[1] = qs[2];
+        sp[2] = qx;
+      }
+      __syncthreads();
+    }
     // --- q, k of this token: wave 0 normalises and publishes them ---
     if (wave == 0) {
       constexpr int E = D / 64;
@@ -154,28 +168,12 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
       float qf[E], kf[E];
       float qq = 0.f, kk = 0.f;
       if (kFused && din.xqk) {
-        // the decode conv of this lane's q and k channels (the conv kernel's
-        // arithmetic, its output rounded to bf16), then their roll (bit copies;
-        // this lane alone reads these taps).  One token: the inputs loaded
-        // before the state tile.
-        static_assert(E == QE, "q/k channels per lane");
-#pragma unroll
-        for (int e = 0; e < E; ++e)
-#pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            const int64_t c = (p ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + lane * E + e;
-            uint16_t* sp = din.qkpool + row * din.sp_slot + c * din.sp_ch;
-            const uint16_t* wsv = reinterpret_cast<const uint16_t*>(&qw[p][e]);
-            const float wk[4] = {gdn::bf2f(wsv[0]), gdn::bf2f(wsv[1]), gdn::bf2f(wsv[2]), gdn::bf2f(wsv[3])};
-            const float y = gdn::bf2f(gdn::f2bf(gdn::conv_decode_silu(
-                gdn::bf2f(qx[p][e]), gdn::bf2f(qs[p][e][0]), gdn::bf2f(qs[p][e][1]), gdn::bf2f(qs[p][e][2]), wk)));
-            sp[0] = qs[p][e][1];
-            sp[1] = qs[p][e][2];
-            sp[2] = qx[p][e];
-            if (p) kf[e] = y; else qf[e] = y;
-          }
+        // the conv outputs from sq / sk (this lane's elements, overwritten
+        // below with the normalised values)
 #pragma unroll
         for (int e = 0; e < E; ++e) {
+          qf[e] = sq[buf][lane * E + e];
+          kf[e] = sk[buf][lane * E + e];
           qq += qf[e] * qf[e];
           kk += kf[e] * kf[e];
         }
