@@ -710,8 +710,9 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4),
                          "traffic": _profiled_traffic("recurrent_decode_config2"),
-                         "kernel": "recurrent_kernel<128,1,true> (the decode step's fused kernel: gates, v "
-                                   "conv with its state roll, state update)", "kernel_us": round(rec_us, 2),
+                         "kernel": "recurrent_kernel<128,1,4,true> (the decode step's one kernel: gates, q/k/v "
+                                   "conv with its state roll, state update, gated norm)",
+                         "kernel_us": round(rec_us, 2),
                          "timing": "20 back-to-back launches between one event pair, alternating two disjoint "
                                    "slot sets of the pool",
                          "algorithmic_bytes_per_launch": state_bytes,
