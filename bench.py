@@ -172,6 +172,26 @@ class EventTimer:
         return {k: 1e3 * statistics.fmean(s.elapsed_time(e) for s, e in v) for k, v in self.pairs.items()}
 
 
+# Untimed load before every timed leg, whatever --warmup says: the GPU's
+# clock settles only after some tenths of a second of sustained work (config
+# 1 measured 0.297 ms per step after 5 warm-up steps, 0.260 ms after 2000).
+SETTLE_S = 1.0
+
+
+def settle(step, W: int, seconds: float = SETTLE_S) -> int:
+    """Run `step` untimed at least W times and for at least `seconds` of wall
+    time, synchronising after each call so the wall time is device time.
+    Returns the number of calls."""
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + seconds
+    n = 0
+    while n < W or time.perf_counter() < t_end:
+        step()
+        torch.cuda.synchronize()
+        n += 1
+    return n
+
+
 def timed_steps(step, K: int) -> float:
     """Wall-clock seconds of exactly K steps, synchronised on both sides."""
     torch.cuda.synchronize()
@@ -182,8 +202,34 @@ def timed_steps(step, K: int) -> float:
     return time.perf_counter() - t0
 
 
+def burst_us(fn, R: int = 20, blocks: int = 3) -> float:
+    """Average duration of one call of `fn` (a fixed sequence of launches on
+    the current stream): the median over `blocks` of R back-to-back calls
+    between one event pair (an event pair around every call would add its own
+    few microseconds to each)."""
+    fn()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(blocks):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(R):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(1e3 * e0.elapsed_time(e1) / R)
+    return statistics.median(per)
+
+
 # -------------------------------------------------------------- workloads --
-def prefill_bench(pkg, cfg, dev, K, W):
+def prefill_bench(pkg, cfg, dev, K, W, rule_only=False):
+    """Config 1 / 3 layer-core prefill.  Returns (seconds per step, kernel us):
+    after a settling period, K timed steps of the whole core (the fused launch
+    pair, then the gated norm); then the fused launch pair and the norm each
+    timed on their own as bursts of back-to-back calls (burst_us), the pair
+    being the launches the steps run.  rule_only: also the chunk rule alone
+    (gdn_chunk_prefill on the conv outputs, q / k / v / g / beta precomputed
+    by the standalone kernels), as "chunk_prefill"."""
     core = pkg.GatedDeltaNetCore(cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
                                  cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
     x, z, a, b = (cfg[k].to(dev) for k in ("x", "z", "a", "b"))
@@ -192,31 +238,38 @@ def prefill_bench(pkg, cfg, dev, K, W):
     conv_pool = cfg["conv_state"].to(dev)
     ids = torch.arange(n, device=dev)
     lens = cfg["lens"]
+    Hk, Hv, D, N = cfg["Hk"], cfg["Hv"], cfg["D"], cfg["N"]
 
     def step():
         core.prefill_varlen(x, z, b, a, lens, ids, conv_pool, s_pool)
 
-    for _ in range(W):
-        step()
-    # timed steps: events around the dominant launch pair on every 10th step
-    # (an event pair delays the stream by a few microseconds)
-    timer = EventTimer(only={"conv_chunk_prefill", "chunk_prefill"})
+    settle(step, W)
+    t = timed_steps(step, K)
+    _, _, cu64_cpu, cu64_gpu = pkg.state_pool.varlen_meta(lens, dev)
+    assert core.sw.fused_prefill and core.sw.gbeta and core.sw.conv_kernel, "the bench times the fused prefill"
 
-    def sampled_step(i=[0]):
-        core.timer = timer if i[0] % 10 == 0 else None
-        i[0] += 1
-        step()
+    def pair():
+        return pkg.ops.conv_chunk_prefill_varlen(x, conv_pool, core.conv_w, b, a, core.A_log, core.dt_bias, cu64_gpu,
+                                                 s_pool, ids, Hk, Hv, D, cu_seqlens_cpu=cu64_cpu)
 
-    t = timed_steps(sampled_step, K)
-    # per-kernel breakdown of the other kernels: a few more steps with events on every kernel
-    rest = EventTimer()
-    core.timer = rest
-    for _ in range(min(K, 20)):
-        step()
-    torch.cuda.synchronize()
-    core.timer = None
-    us = rest.avg_us()
-    us.update(timer.avg_us())
+    o = pair()
+    zz = z.view(N, Hv, D)
+    us = {"conv_chunk_prefill": burst_us(pair),
+          "rmsnorm_gated": burst_us(lambda: pkg.ops.rms_norm_gated(o, zz, core.norm_w, core.eps))}
+    if rule_only:
+        lens32 = torch.tensor(lens, dtype=torch.int32, device=dev)
+        starts = torch.tensor([0] + torch.tensor(lens).cumsum(0)[:-1].tolist(), dtype=torch.int32, device=dev)
+        cstate = conv_pool.clone()
+        q, k, v = pkg.ops.causal_conv_silu_varlen_parts(x, cstate, core.conv_w, lens32, starts, Hk * D,
+                                                        state_ids=ids)
+        g, beta = pkg.ops.fused_g_beta(b, a, core.A_log, core.dt_bias, None)
+        qv, kv, vv = q.view(N, Hk, D), k.view(N, Hk, D), v.view(N, Hv, D)
+
+        def rule():
+            pkg.ops.chunk_gated_delta_rule_varlen(qv, kv, vv, g, beta, cu64_gpu, s_pool, state_ids=ids,
+                                                  final_state=s_pool, cu_seqlens_cpu=cu64_cpu)
+        settle(rule, 1, 0.3)
+        us["chunk_prefill"] = burst_us(rule)
     return t / K, us
 
 
@@ -246,8 +299,7 @@ def layer_bench(pkg, cfg, dev, K, W, hidden=2048):
     def step():
         layer.forward(x, cu, max(lens), ids, conv_pool, s_pool, lens_q=lens)
 
-    for _ in range(W):
-        step()
+    settle(step, W)
     t = timed_steps(step, K)
     timer = EventTimer()
     layer.timer = timer
@@ -262,9 +314,8 @@ def layer_bench(pkg, cfg, dev, K, W, hidden=2048):
     core_out = torch.randn(N, Hv * D, generator=gen).to(BF16).to(dev)
     y_out = torch.empty(N, hidden, dtype=BF16, device=dev)
     ref = EventTimer()
-    for _ in range(3):
-        torch.matmul(x, layer.w_in.t(), out=y_in)
-        torch.matmul(core_out, layer.w_out.t(), out=y_out)
+    settle(lambda: (torch.matmul(x, layer.w_in.t(), out=y_in), torch.matmul(core_out, layer.w_out.t(), out=y_out)),
+           3, 0.3)
     for _ in range(10):
         ref.start("in_proj_hipblaslt")
         torch.matmul(x, layer.w_in.t(), out=y_in)
@@ -299,8 +350,7 @@ def layer_decode_bench(pkg, cfg, dev, K, W, hidden=2048):
     def step():
         layer.forward(x, cu, 1, ids, conv_pool, s_pool, lens_q=lens)
 
-    for _ in range(W):
-        step()
+    settle(step, W)
     t = timed_steps(step, K)
     # the same step replayed from a captured HIP graph (how the engine runs decode)
     g = torch.cuda.CUDAGraph()
@@ -312,7 +362,7 @@ def layer_decode_bench(pkg, cfg, dev, K, W, hidden=2048):
         with torch.cuda.graph(g, stream=gs):
             step()
     torch.cuda.current_stream().wait_stream(gs)
-    g.replay()
+    settle(g.replay, W)
     t_graph = timed_steps(g.replay, K)
     timer = EventTimer()
     layer.timer = timer
@@ -326,9 +376,8 @@ def layer_decode_bench(pkg, cfg, dev, K, W, hidden=2048):
     core_out = torch.randn(B, Hv * D, generator=gen).to(BF16).to(dev)
     y_out = torch.empty(B, hidden, dtype=BF16, device=dev)
     ref = EventTimer()
-    for _ in range(3):
-        torch.matmul(x, layer.w_in.t(), out=y_in)
-        torch.matmul(core_out, layer.w_out.t(), out=y_out)
+    settle(lambda: (torch.matmul(x, layer.w_in.t(), out=y_in), torch.matmul(core_out, layer.w_out.t(), out=y_out)),
+           3, 0.3)
     for _ in range(10):
         ref.start("in_proj_hipblaslt")
         torch.matmul(x, layer.w_in.t(), out=y_in)
@@ -351,8 +400,7 @@ def decode_bench(pkg, cfg, dev, K, W):
     def step():
         core.decode(x, z, b, a, ids, conv_pool, s_pool)
 
-    for _ in range(W):
-        step()
+    settle(step, W)
     timer = EventTimer()
     core.timer = timer
     t = timed_steps(step, K)
@@ -367,10 +415,10 @@ def decode_bench(pkg, cfg, dev, K, W):
         with torch.cuda.graph(g, stream=s):
             step()
     torch.cuda.current_stream().wait_stream(s)
-    g.replay()
+    settle(g.replay, W)
     t_graph = timed_steps(g.replay, K)
-    rec_us, pass_us = recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z)
-    return t / K, t_graph / K, timer.avg_us(), rec_us, pass_us
+    rec_us, pass_us, copy_us = recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z)
+    return t / K, t_graph / K, timer.avg_us(), rec_us, pass_us, copy_us
 
 
 def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, R=20):
@@ -381,7 +429,8 @@ def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, 
     from the one before (the pool is larger than the last-level cache).
     Also times, the same way, the state tile pass: the same state tiles read
     and written back in place with no arithmetic (the ceiling of this access
-    pattern).  Returns (kernel us, tile pass us)."""
+    pattern), and its out-of-place form (the tiles written to a second pool at
+    the same offsets).  Returns (kernel us, tile pass us, tile copy us)."""
     B, Hk, Hv, D = x.shape[0], cfg["Hk"], cfg["Hv"], cfg["D"]
     kd = Hk * D
     used = set(ids.tolist())
@@ -408,29 +457,37 @@ def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, 
 
         def launch(sl):
             pkg.ops.recurrent_gdn_inplace(q, k, v, g1, b1, s_pool, sl)
-    return _burst_us(launch, sets, R), _burst_us(lambda sl: pkg.ops.state_tile_pass(s_pool, sl), sets, R)
+    rec = _burst_us(launch, sets, R)
+    tile = _burst_us(lambda sl: pkg.ops.state_tile_pass(s_pool, sl), sets, R)
+    dst = torch.empty_like(s_pool)
+    copy = _burst_us(lambda sl: pkg.ops.state_tile_copy(s_pool, dst, sl), sets, R)
+    del dst
+    return rec, tile, copy
 
 
 def _burst_us(launch, sets, R):
-    """Average duration of R back-to-back launches over the slot sets in turn,
-    between one event pair (after an untimed launch)."""
-    launch(sets[-1])
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(R):
-        launch(sets[i % len(sets)])
-    e1.record()
-    torch.cuda.synchronize()
-    return 1e3 * e0.elapsed_time(e1) / R
+    """Average duration of one launch: the median over three blocks of R
+    back-to-back launches over the slot sets in turn, each block between one
+    event pair (after an untimed launch)."""
+    i = [0]
+
+    def one():
+        launch(sets[i[0] % len(sets)])
+        i[0] += 1
+    return burst_us(lambda: [one() for _ in range(len(sets))], max(1, R // len(sets))) / len(sets)
 
 
 def spec_bench(pkg, cfg, dev, K, W):
     """Config 4 in steady state: each step verifies T draft tokens per row
     starting from the previous step's accepted states (ops.SpecVerify: the
     rollback folded into the next step, no commit copy), then records the
-    accepted lengths.  The commit-copy kernel is timed once on its own for
-    comparison."""
+    accepted lengths.  Kernel times are bursts of back-to-back steps:
+    "recurrent_multitoken" as the steps run (each verify reads the states the
+    previous one wrote, partly still in the last-level cache), and
+    "recurrent_multitoken_cold" alternating two verifiers on the pool's two
+    disjoint halves of rows, so that a verify's start states were written two
+    steps (1.2 GB of traffic) earlier.  The commit-copy kernel is timed on its
+    own for comparison."""
     B, T, Hv, D = cfg["B"], cfg["T"], cfg["Hv"], cfg["D"]
     q, k, v, a, b = (cfg[n].to(dev) for n in ("q", "k", "v", "a", "b"))
     g, beta = pkg.ops.fused_g_beta(b, a, cfg["A_log"].to(dev), cfg["dt_bias"].to(dev), None)
@@ -438,29 +495,25 @@ def spec_bench(pkg, cfg, dev, K, W):
     ids = cfg["ids"].to(dev)
     acc = cfg["accepted"].to(device=dev, dtype=torch.int64)
     spec = pkg.ops.SpecVerify(s_pool)
-    timer = EventTimer()
 
-    def step():
-        timer.start("recurrent_multitoken")
-        spec.verify(q, k, v, g, beta, ids)
-        timer.stop("recurrent_multitoken")
-        spec.accept(acc)          # no device work: the next verify reads the accepted states
+    def step(sp=spec, rows=ids):
+        sp.verify(q, k, v, g, beta, rows)
+        sp.accept(acc)          # no device work: the next verify reads the accepted states
 
-    for _ in range(W):
-        step()
-    timer.reset()
+    settle(step, W)
     t = timed_steps(step, K)
-    us = timer.avg_us()
-    # the commit copy the deferred scheme avoids (for comparison only; one
-    # untimed launch first, as for every timed kernel)
-    pkg.ops.commit_states(s_pool, ids, spec.inter, acc)
-    ct = EventTimer()
-    for _ in range(5):
-        ct.start("state_commit_copy")
-        pkg.ops.commit_states(s_pool, ids, spec.inter, acc)
-        ct.stop("state_commit_copy")
-    torch.cuda.synchronize()
-    us.update(ct.avg_us())
+    us = {"recurrent_multitoken": burst_us(step)}
+    spec.commit()
+    # the other half of the pool's rows, with a verifier of its own
+    used = set(ids.tolist())
+    other = torch.tensor([i for i in range(s_pool.shape[0]) if i not in used][:B], device=dev)
+    if other.numel() == B:
+        spec2 = pkg.ops.SpecVerify(s_pool)
+        us["recurrent_multitoken_cold"] = burst_us(lambda: (step(), step(spec2, other)), max(1, 10)) / 2
+        spec2.commit()
+        spec.commit()
+    # the commit copy the deferred scheme avoids (for comparison only)
+    us["state_commit_copy"] = burst_us(lambda: pkg.ops.commit_states(s_pool, ids, spec.inter, acc), 5)
     return t / K, us
 
 
@@ -565,6 +618,16 @@ def standalone_kernels(pkg, cfg, dev, K, W):
     return out
 
 
+CPU_SHARE = 16
+
+
+def _usable_cpus() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def cpu_baseline(cfg, n_seq: int, threads: int):
     """CPU oracle (fp32 torch restatement of the reference path) on the first
     n_seq sequences of config 1 (the bench passes all of them: the whole
@@ -597,7 +660,8 @@ def cpu_baseline(cfg, n_seq: int, threads: int):
             "sample": f"config 1 GDN core (g/beta+conv+chunk rule+gated norm) on {n_seq} of its "
                       f"{len(cfg['lens'])} sequences "
                       f"({N} tokens, lens {lens}), fp32 torch oracle, median of 3 reps ({t:.2f} s each), "
-                      f"os.cpu_count()={os.cpu_count()}, cpu='{cpu_name}'"}
+                      f"{threads} threads (os.cpu_count()={os.cpu_count()}, usable CPUs {_usable_cpus()}, at most "
+                      f"{CPU_SHARE}: one GPU's CPU share on the box), cpu='{cpu_name}'"}
 
 
 def main():
@@ -654,9 +718,9 @@ def main():
 
     cfg1 = make_prefill(1, None)
     N1 = cfg1["N"]
-    t1, k1 = prefill_bench(pkg, cfg1, dev, K, W)
-    fused = "conv_chunk_prefill" in k1
-    chunk_us = k1["conv_chunk_prefill" if fused else "chunk_prefill"]
+    t1, k1 = prefill_bench(pkg, cfg1, dev, K, W, rule_only=True)
+    fused = True
+    chunk_us = k1["conv_chunk_prefill"]
     flops = chunk_flops(N1, cfg1["Hv"], cfg1["D"])
     achieved = flops / (chunk_us * 1e-6) / 1e12
     floor1 = prefill_compulsory_bytes(cfg1)
@@ -670,7 +734,18 @@ def main():
                            "gates, the flop count is the chunk rule's matrix products)" if fused else
                            "chunk prefill = chunk_prep_kernel<128, false> + chunk_state_kernel<128, false> "
                            "(one launch pair per call)"),
-                "kernel_us": round(chunk_us, 2), "algorithmic_flop_per_launch": flops}
+                "kernel_us": round(chunk_us, 2), "algorithmic_flop_per_launch": flops,
+                "timing": "median of 3 blocks of 20 back-to-back calls, each block between one event pair, after "
+                          f"{SETTLE_S:.1f} s of untimed steps"}
+    rule_us = k1["chunk_prefill"]
+    a_rule = flops / (rule_us * 1e-6) / 1e12
+    roofline_rule = {"bound": "mfma", "achieved": round(a_rule, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(a_rule / BF16_PEAK_TFLOPS, 4),
+                     "traffic": _profiled_traffic("chunk_prefill_config1"),
+                     "kernel": "chunk rule alone = chunk_prep_kernel<128, false> + chunk_state_kernel<128, false> on "
+                               "the conv outputs (q, k, v, g, beta precomputed; the varlen fla call's boundary)",
+                     "kernel_us": round(rule_us, 2), "algorithmic_flop_per_launch": flops,
+                     "timing": "as roofline"}
     kernels1 = {k: round(v, 2) for k, v in k1.items()}
 
     if 5 in configs:
@@ -701,7 +776,7 @@ def main():
                     "[256, 2048] x [2048, 2048]^T; random-init weights"}
     if 2 in configs:
         c2 = make_decode()
-        t2, t2g, k2, rec_us, pass_us = decode_bench(pkg, c2, dev, K, W)
+        t2, t2g, k2, rec_us, pass_us, copy_us = decode_bench(pkg, c2, dev, K, W)
         state_bytes = 2 * c2["B"] * c2["Hv"] * c2["D"] * c2["D"] * 4
         gbps = state_bytes / (rec_us * 1e-6) / 1e9
         extra["decode_config2"] = {
@@ -722,14 +797,20 @@ def main():
                              "kernel_frac_of_ceiling": round(pass_us / rec_us, 4),
                              "what": "gdn_state_tile_pass: the same state tiles read and written back in place "
                                      "with the decode kernel's layout, launch shape and cache policy, no "
-                                     "arithmetic, timed the same way"}}}
+                                     "arithmetic, timed the same way"},
+                         "out_of_place_tile_copy": {
+                             "kernel_us": round(copy_us, 2),
+                             "GBps": round(state_bytes / (copy_us * 1e-6) / 1e9, 1),
+                             "inplace_over_copy": round(pass_us / copy_us, 4),
+                             "what": "gdn_state_tile_copy: the same pass with each tile written to a second pool "
+                                     "at the same offsets (out of place), timed the same way"}}}
         del c2
     if 3 in configs:
         c3 = make_prefill(4, [65536], h0_std=0.1, conv_std=1.0)
         K3 = max(2, K // 4)
         t3, k3 = prefill_bench(pkg, c3, dev, K3, 1)
         f3 = chunk_flops(c3["N"], c3["Hv"], c3["D"])
-        us3 = k3["conv_chunk_prefill" if "conv_chunk_prefill" in k3 else "chunk_prefill"]
+        us3 = k3["conv_chunk_prefill"]
         a3 = f3 / (us3 * 1e-6) / 1e12
         floor3 = prefill_compulsory_bytes(c3)
         extra["long_prefill_config3"] = {
@@ -755,12 +836,24 @@ def main():
                          "kernel": "recurrent_kernel multi-token form (reads the accepted state, writes T "
                                    "intermediate states per row)",
                          "kernel_us": round(k4["recurrent_multitoken"], 2),
-                         "algorithmic_bytes_per_launch": rb}}
+                         "algorithmic_bytes_per_launch": rb,
+                         "timing": "median of 3 blocks of 20 back-to-back steps after a settling period; each "
+                                   "verify reads the start states the previous step wrote"}}
+        if "recurrent_multitoken_cold" in k4:
+            gc = rb / (k4["recurrent_multitoken_cold"] * 1e-6) / 1e9
+            extra["spec_verify_config4"]["roofline_cold"] = {
+                "bound": "hbm", "achieved": round(gc, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(gc / HBM_PEAK_GBPS, 4), "kernel_us": round(k4["recurrent_multitoken_cold"], 2),
+                "algorithmic_bytes_per_launch": rb,
+                "timing": "two verifiers on disjoint halves of the pool's rows, alternating: a verify's start "
+                          "states were written two steps (1.2 GB of traffic) before it"}
         del c4
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(cfg1, len(cfg1["lens"]), threads=min(16, os.cpu_count() or 1))
+        # the host cores this process may use, at most 16: the CPU share of one
+        # GPU on the box, whatever os.cpu_count() reports for the whole host
+        cpu = cpu_baseline(cfg1, len(cfg1["lens"]), threads=min(CPU_SHARE, _usable_cpus()))
 
     out = {
         "metric": METRIC, "value": round(N1 / t1, 1), "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -775,6 +868,7 @@ def main():
                    "parallelism": "single GPU"},
         "kernels_us": kernels1,
         "roofline": roofline,
+        "roofline_chunk_rule": roofline_rule,
         "cpu_baseline": cpu,
     }
     out.update(extra)

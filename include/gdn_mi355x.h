@@ -312,6 +312,16 @@ int gdn_state_tile_pass(float* pool, int64_t slot_stride, const int64_t* ids, in
                         void* stream);
 
 /*
+ * Measurement pass, no counterpart in the reference: gdn_state_tile_pass with
+ * the tiles written to a second pool at the same offsets (dst[ids[b], h] =
+ * src[ids[b], h]), the same launch shape and cache policy -- the out-of-place
+ * form of the same traffic.  src and dst must not overlap; slot_stride >=
+ * Hv*D*D for both.
+ */
+int gdn_state_tile_copy(const float* src, float* dst, int64_t slot_stride, const int64_t* ids, int B, int Hv,
+                        int D, void* stream);
+
+/*
  * The layer's projections: C = A B^T, bf16 operands, fp32 accumulation, bf16
  * result.  Replaces F.linear in ColumnParallelLinear / RowParallelLinear
  * (nanovllm/layers/linear.py:56-75, :133-158) at the GDN layer's in_proj_qkv,

@@ -73,7 +73,7 @@ struct NormIn {
 
 // Initial states of a speculative-verify step taken from the previous step's
 // per-token states (deferred commit): row b starts from src[b, acc[b] - 1]
-// (src [B, T_src, Hv, D, D]) when acc[b] >= 1, else from its pool row.
+// (src [B, T_src, Hv, D, D]) when 1 <= acc[b] <= T_src, else from its pool row.
 struct SrcIn {
   const float* src;
   const int64_t* acc;  // NULL: every row from the pool
@@ -93,6 +93,9 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   constexpr int RPP = 64 * NW / CPR;  // rows per pass of the workgroup
   constexpr int NP = D / RPP;     // passes (float4 registers per thread)
   static_assert(CPR <= 64 && 64 % CPR == 0 && NP >= 1, "tile shape");
+  // the in-kernel q/k conv gives thread t channel t % 128 of q (t < 128) or
+  // of k (t >= 128): it needs exactly 256 threads and D <= 128
+  static_assert(!kFused || (NW == 4 && D <= 128), "fused q/k conv needs four waves");
 
   __shared__ float sq[2][D];
   __shared__ float sk[2][D];
@@ -113,8 +116,11 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   const int col = vb * VB + c4 * 4;
 
   const int64_t row = ids ? ids[b] : b;
+  // an accepted count outside [1, T_src] keeps the pool row, as the commit
+  // kernel leaves such a row untouched
   const int64_t acc = src.acc ? src.acc[b] : 0;
-  const float* sin = acc >= 1 ? src.src + ((static_cast<int64_t>(b) * src.T_src + acc - 1) * Hv + h) * D * D
+  const bool from_src = acc >= 1 && acc <= src.T_src;
+  const float* sin = from_src ? src.src + ((static_cast<int64_t>(b) * src.T_src + acc - 1) * Hv + h) * D * D
                               : s_in + row * s_in_stride + static_cast<int64_t>(h) * D * D;
   // byte offset of this lane's float4 in the tile, and of row pass j
   const int voff = (r0 * D + col) * 4;
@@ -373,9 +379,10 @@ __global__ __launch_bounds__(256) void state_commit_kernel(float* __restrict__ p
 // Measurement pass: each selected state tile read into registers and written
 // back unchanged, with the decode kernel's layout (NVB = 1, 4 waves), cache
 // policy and barrier between the loads and the stores: one decode step's
-// state traffic without its arithmetic.
+// state traffic without its arithmetic.  With dst != src the tiles land at
+// the same offsets of a second pool (the out-of-place form of the same pass).
 template <int D>
-__global__ __launch_bounds__(256) void state_tile_pass_kernel(float* pool, int64_t slot_stride,
+__global__ __launch_bounds__(256) void state_tile_pass_kernel(const float* src, float* dst, int64_t slot_stride,
                                                               const int64_t* __restrict__ ids, int B, int Hv) {
   constexpr int CPR = D / 4;
   constexpr int RPP = 256 / CPR;
@@ -385,14 +392,16 @@ __global__ __launch_bounds__(256) void state_tile_pass_kernel(float* pool, int64
   if (wi < 0) return;
   const int h = static_cast<int>(wi % Hv);
   const int b = static_cast<int>(wi / Hv);
-  const __amdgpu_buffer_rsrc_t r = tile_rsrc(pool + ids[b] * slot_stride + static_cast<int64_t>(h) * D * D);
+  const int64_t off = ids[b] * slot_stride + static_cast<int64_t>(h) * D * D;
+  const __amdgpu_buffer_rsrc_t r = tile_rsrc(src + off);
+  const __amdgpu_buffer_rsrc_t w = tile_rsrc(dst + off);
   const int voff = ((threadIdx.x / CPR) * D + (threadIdx.x % CPR) * 4) * 4;
   float4 S[NP];
 #pragma unroll
   for (int j = 0; j < NP; ++j) S[j] = tile_ld(r, voff, j * kPass);
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < NP; ++j) tile_st_nt(r, voff, j * kPass, S[j]);
+  for (int j = 0; j < NP; ++j) tile_st_nt(w, voff, j * kPass, S[j]);
 }
 
 template <int D, int NVB, int NW = 4>
@@ -540,18 +549,31 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
 #undef GDN_REC_ARGS
 }
 
-extern "C" int gdn_state_tile_pass(float* pool, int64_t slot_stride, const int64_t* ids, int B, int Hv, int D,
-                                   void* stream) {
+static int state_tile_pass(const float* src, float* dst, int64_t slot_stride, const int64_t* ids, int B, int Hv,
+                           int D, void* stream) {
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
   if (B < 0 || Hv <= 0 || slot_stride % 4 || slot_stride < static_cast<int64_t>(Hv) * D * D) return GDN_ERR_INVALID_ARG;
   if (B == 0) return GDN_OK;
-  if (!pool || !ids || reinterpret_cast<uintptr_t>(pool) % 16) return GDN_ERR_INVALID_ARG;
+  if (!src || !dst || !ids || reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
+    return GDN_ERR_INVALID_ARG;
   const int64_t work = static_cast<int64_t>(B) * Hv;
   const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (D == 128)
-    state_tile_pass_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(pool, slot_stride, ids, B, Hv);
+    state_tile_pass_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(src, dst, slot_stride, ids,
+                                                                                         B, Hv);
   else
-    state_tile_pass_kernel<64><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(pool, slot_stride, ids, B, Hv);
+    state_tile_pass_kernel<64><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(src, dst, slot_stride, ids, B,
+                                                                                       Hv);
   return gdn_launch_status();
+}
+
+extern "C" int gdn_state_tile_pass(float* pool, int64_t slot_stride, const int64_t* ids, int B, int Hv, int D,
+                                   void* stream) {
+  return state_tile_pass(pool, pool, slot_stride, ids, B, Hv, D, stream);
+}
+
+extern "C" int gdn_state_tile_copy(const float* src, float* dst, int64_t slot_stride, const int64_t* ids, int B,
+                                   int Hv, int D, void* stream) {
+  return state_tile_pass(src, dst, slot_stride, ids, B, Hv, D, stream);
 }

@@ -25,19 +25,24 @@ the module's own pure-torch ports, exactly as in the reference.  _HAS_FLA is
 set only when one of the two switches is on (this package then provides the
 fla entry points); with both off it keeps the module's value.
 
-With NANOVLLM_GDN_FUSED_PREFILL=1 (the default; it also needs the gate and
-conv kernels on and a conv width of 4) it further replaces the method
-Qwen3_5GatedDeltaNet._gdn_prefill_varlen (qwen3_5.py:922-965) with one whose
-gates, conv and chunk rule are the single fused call
+With NANOVLLM_GDN_FUSED_PREFILL=1 (the default) it further replaces the
+method Qwen3_5GatedDeltaNet._gdn_prefill_varlen (qwen3_5.py:922-965) with
+one whose gates, conv and chunk rule are the single fused call
 ops.conv_chunk_prefill_varlen (the same results as the three calls the
 method makes, bit for bit), on the layer's own pools and slot ids.
 
-With NANOVLLM_GDN_FUSED_DECODE=1 (the default; it also needs the gate, conv
-and in-place kernels on) it replaces Qwen3_5GatedDeltaNet._gdn_padded
-(qwen3_5.py:967-1085) with one whose T == 1 branch runs the q/k decode conv
-and then ops.recurrent_decode_fused (gates, the v channels' conv, the
-in-place recurrent update and the gated norm self.norm in one kernel; the
-same results bit for bit); other T keep the original method.
+With NANOVLLM_GDN_FUSED_DECODE=1 (the default) it replaces
+Qwen3_5GatedDeltaNet._gdn_padded (qwen3_5.py:967-1085) with one whose
+T == 1 branch runs ops.recurrent_decode_fused (gates, the conv with its
+roll, the in-place recurrent update and the gated norm self.norm in one
+kernel, after the q/k decode conv's own launch when the heads are grouped;
+the same results bit for bit); other T keep the original method.
+
+Both methods read the module's _USE_GDN_GBETA and _USE_CONV_TRITON (and the
+decode method _USE_GDN_INPLACE) on every call, as the reference's layer
+does, and run the original method when one of them is off, so the
+reference's A/B switches keep their meaning when flipped at run time; conv
+widths other than 4 also keep the original method.
 """
 from __future__ import annotations
 
@@ -52,12 +57,20 @@ PATCHED_NAMES = (
 FLAG_NAMES = ("_HAS_FLA", "_USE_FLA_CHUNK", "_USE_FLA_RECURRENT", "_USE_GDN_VARLEN")
 
 
+def _on(mod, name: str) -> bool:
+    """A module-level switch of the reference module, read at call time (the
+    layer reads _USE_GDN_GBETA, _USE_CONV_TRITON and _USE_GDN_INPLACE on every
+    call, qwen3_5.py:933, :978, :1011, :1024); absent means on."""
+    return bool(getattr(mod, name, True))
+
+
 def _fused_prefill_method(mod, orig):
     def _gdn_prefill_varlen(self, hidden, lens_q, ids):
         """Fused form of Qwen3_5GatedDeltaNet._gdn_prefill_varlen
-        (nanovllm/models/qwen3_5.py:922-965); other conv widths keep the
-        original method."""
-        if self.conv_kernel != 4:
+        (nanovllm/models/qwen3_5.py:922-965).  Other conv widths, and the
+        module's _USE_GDN_GBETA or _USE_CONV_TRITON switched off at the time of
+        the call, run the original method."""
+        if self.conv_kernel != 4 or not (_on(mod, "_USE_GDN_GBETA") and _on(mod, "_USE_CONV_TRITON")):
             return orig(self, hidden, lens_q, ids)
         b = self.in_proj_b(hidden)
         a = self.in_proj_a(hidden)
@@ -76,12 +89,15 @@ def _fused_prefill_method(mod, orig):
     return _gdn_prefill_varlen
 
 
-def _fused_decode_method(orig):
+def _fused_decode_method(mod, orig):
     def _gdn_padded(self, x, lens, ids, T):
         """Fused T == 1 branch of Qwen3_5GatedDeltaNet._gdn_padded
-        (nanovllm/models/qwen3_5.py:967-1030, :1079-1085); other T and conv
-        widths keep the original method."""
-        if T != 1 or self.conv_kernel != 4:
+        (nanovllm/models/qwen3_5.py:967-1030, :1079-1085).  Other T and conv
+        widths, and any of the module's _USE_GDN_GBETA, _USE_CONV_TRITON,
+        _USE_GDN_INPLACE switched off at the time of the call, run the
+        original method."""
+        if T != 1 or self.conv_kernel != 4 or not (
+                _on(mod, "_USE_GDN_GBETA") and _on(mod, "_USE_CONV_TRITON") and _on(mod, "_USE_GDN_INPLACE")):
             return orig(self, x, lens, ids, T)
         n = x.size(0)
         Hv, Dv = self.num_v_heads, self.head_v_dim
@@ -108,16 +124,14 @@ def _fused_decode_method(orig):
     return _gdn_padded
 
 
+# The fused methods are installed under this package's own switches; the
+# reference's kernel switches are checked by the methods on every call.
 def _fused_decode_enabled() -> bool:
-    e = os.environ.get
-    return (e("NANOVLLM_GDN_FUSED_DECODE", "1") == "1" and e("NANOVLLM_GDN_GBETA", "1") == "1"
-            and e("NANOVLLM_CONV_TRITON", "1") == "1" and e("NANOVLLM_GDN_INPLACE", "1") == "1")
+    return os.environ.get("NANOVLLM_GDN_FUSED_DECODE", "1") == "1"
 
 
 def _fused_prefill_enabled() -> bool:
-    e = os.environ.get
-    return (e("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1" and e("NANOVLLM_GDN_GBETA", "1") == "1"
-            and e("NANOVLLM_CONV_TRITON", "1") == "1")
+    return os.environ.get("NANOVLLM_GDN_FUSED_PREFILL", "1") == "1"
 
 
 def install(mod) -> dict:
@@ -145,7 +159,7 @@ def install(mod) -> dict:
         cls._gdn_prefill_varlen = _fused_prefill_method(mod, cls._gdn_prefill_varlen)
     if cls is not None and _fused_decode_enabled() and hasattr(cls, "_gdn_padded"):
         prev["Qwen3_5GatedDeltaNet._gdn_padded"] = cls.__dict__.get("_gdn_padded")
-        cls._gdn_padded = _fused_decode_method(cls._gdn_padded)
+        cls._gdn_padded = _fused_decode_method(mod, cls._gdn_padded)
     return prev
 
 

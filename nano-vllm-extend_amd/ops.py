@@ -728,7 +728,9 @@ class SpecVerify:
         return out
 
     def accept(self, accepted: torch.Tensor) -> None:
-        """accepted [B] int64 (device): tokens kept per row, 1..T."""
+        """accepted [B] int64 (device): tokens kept per row, 1..T.  A row
+        whose count lies outside 1..T starts the next verify from its pool
+        row (the last committed state), as commit() leaves it untouched."""
         assert self.inter is not None and self.accepted is None, "accept() follows one verify()"
         assert accepted.dtype == torch.int64 and accepted.shape == (self.inter.shape[0],)
         assert accepted.device == self.inter.device and accepted.is_contiguous()
@@ -766,6 +768,20 @@ def state_tile_pass(s_pool: torch.Tensor, ids: torch.Tensor) -> None:
     ids64 = ids.to(torch.int64).contiguous()
     _lib.call("gdn_state_tile_pass", _lib.ptr(s_pool), s_pool.stride(0), _lib.ptr(ids64), ids64.numel(),
               s_pool.shape[1], s_pool.shape[-1], _stream(dev))
+
+
+def state_tile_copy(src_pool: torch.Tensor, dst_pool: torch.Tensor, ids: torch.Tensor) -> None:
+    """Measurement pass (no reference counterpart): state_tile_pass with each
+    tile written to dst_pool[ids[b], h] instead of back in place (the same
+    launch shape, layout and cache policy).  Both pools [slots, Hv, D, D]
+    fp32 with the same slot stride, not overlapping."""
+    dev = _check_cuda(src_pool, dst_pool, ids)
+    assert src_pool.shape == dst_pool.shape and src_pool.stride(0) == dst_pool.stride(0)
+    assert _state_view_ok(src_pool, src_pool.shape[1], src_pool.shape[-1])
+    assert _state_view_ok(dst_pool, dst_pool.shape[1], dst_pool.shape[-1])
+    ids64 = ids.to(torch.int64).contiguous()
+    _lib.call("gdn_state_tile_copy", _lib.ptr(src_pool), _lib.ptr(dst_pool), src_pool.stride(0), _lib.ptr(ids64),
+              ids64.numel(), src_pool.shape[1], src_pool.shape[-1], _stream(dev))
 
 
 # ------------------------------------------------------------- projections --

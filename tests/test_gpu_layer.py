@@ -123,6 +123,62 @@ def test_decode_graph_replay_equals_eager(pkg, dev):
         assert torch.equal(cg[real], ce[real]), f"replay {rep}: conv pool differs"
 
 
+def test_decode_graph_one_launch_with_pad_rows_equals_eager(pkg, dev):
+    """The decode step config 2 runs (Hk == Hv = 16, whole heads per
+    workgroup: q/k/v conv and roll, gates, update and gated norm in one
+    kernel), captured in a HIP graph the way the runner captures it
+    (nanovllm/engine/model_runner.py:1584-1611): static input buffers of the
+    graph's batch size, the real rows copied in before each replay and the
+    pad rows pointed at the dummy slot (:289-299, :824-826), several of
+    whose workgroups then write that slot's states and conv taps in one
+    launch.  Three replays with new inputs and eager work in between: the
+    real rows' outputs, states and conv taps equal the eager step on the
+    unpadded batch bit for bit, and every slot but the dummy one is equal."""
+    gen = torch.Generator().manual_seed(37)
+    Hk = Hv = 16
+    D, B, pad, slots = 128, 256, 16, 512
+    Bg, dummy = B + pad, slots
+    assert Bg * Hv >= pkg.ops.WHOLE_HEAD_TILES
+    C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
+    conv0 = torch.randn(slots + 1, C, 3, generator=gen).to(BF16).to(dev)
+    s0 = (torch.randn(slots + 1, Hv, D, D, generator=gen) * 0.1).to(dev)
+    real = torch.randperm(slots, generator=gen)[:B].to(dev)
+    core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w)
+    cg, sg = conv0.clone(), s0.clone()
+    ce, se = conv0.clone(), s0.clone()
+    # the graph's static inputs; pad rows hold stale data and the dummy slot
+    st_mixed, st_z, st_b, st_a = (t.to(dev) for t in _rows(gen, Bg, C, Hv, D))
+    st_ids = torch.full((Bg,), dummy, dtype=torch.int64, device=dev)
+    st_ids[:B] = real
+    warm_c, warm_s = conv0.clone(), s0.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        core.decode(st_mixed, st_z, st_b, st_a, st_ids, warm_c, warm_s)   # warm-up on a throwaway copy
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    del warm_c, warm_s
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out_g = core.decode(st_mixed, st_z, st_b, st_a, st_ids, cg, sg)
+    for rep in range(3):
+        mixed, z, b, a = (t.to(dev) for t in _rows(gen, B, C, Hv, D))
+        st_mixed[:B].copy_(mixed)
+        st_z[:B].copy_(z)
+        st_b[:B].copy_(b)
+        st_a[:B].copy_(a)
+        graph.replay()
+        torch.cuda.synchronize()
+        out_e = core.decode(mixed, z, b, a, real, ce, se)
+        _ = (mixed.float() * 2).sum()                            # unrelated eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out_g[:B].view(torch.int16), out_e.view(torch.int16)), f"replay {rep}: outputs differ"
+        assert torch.equal(sg[:slots], se[:slots]), f"replay {rep}: state pool differs"
+        assert torch.equal(cg[:slots].view(torch.int16), ce[:slots].view(torch.int16)), \
+            f"replay {rep}: conv pool differs"
+    assert not torch.equal(sg[real], s0[real]), "the replays updated the real rows' states"
+
+
 def test_chunked_prefill_equals_one_shot_and_batched_equals_solo(pkg, dev):
     gen = torch.Generator().manual_seed(33)
     Hk = Hv = 4
@@ -365,22 +421,26 @@ def test_installed_prefill_method_equals_layer_core(pkg, dev):
     assert torch.equal(layer.conv_cache.view(torch.int16), cp1.view(torch.int16))
 
 
-def test_installed_decode_method_equals_layer_core(pkg, dev):
+@pytest.mark.parametrize("Hk,Hv,B,slots", [(2, 4, 5, 8), (16, 16, 136, 160)],
+                         ids=["gva-two-launch", "one-launch"])
+def test_installed_decode_method_equals_layer_core(pkg, dev, Hk, Hv, B, slots):
     """integration.install's fused _gdn_padded (T == 1) on a stand-in layer
     with the reference's attribute names gives the layer core's decode (with
     the fused decode switched off: fused_g_beta -> conv_decode_step ->
-    recurrent_gdn_inplace) bit for bit, and updates the same pools."""
+    recurrent_gdn_inplace) bit for bit, and updates the same pools.  Both of
+    the installed method's branches: GVA (the q/k conv as its own launch) and
+    one key head per value head with B * Hv >= WHOLE_HEAD_TILES (the whole
+    step, gated norm included, in one kernel)."""
     import types
 
     gen = torch.Generator().manual_seed(36)
-    Hk, Hv, D = 2, 4, 128
+    D = 128
     C, conv_w, A_log, dt_bias, norm_w = _layer(gen, Hk, Hv, D)
-    B = 5
+    assert (Hk == Hv and B * Hv >= pkg.ops.WHOLE_HEAD_TILES) == (Hk == 16)
     mixed, z, b, a = (t.to(dev) for t in _rows(gen, B, C, Hv, D))
-    slots = 8
     conv0 = torch.randn(slots, C, 3, generator=gen).to(BF16).to(dev)
     s0 = (torch.randn(slots, Hv, D, D, generator=gen) * 0.1).to(dev)
-    ids = torch.tensor([6, 1, 3, 0, 5], device=dev)
+    ids = torch.randperm(slots, generator=gen)[:B].to(dev)
 
     core = _core(pkg, dev, Hk, Hv, D, conv_w, A_log, dt_bias, norm_w, fused_decode=False)
     cp1, sp1 = conv0.clone(), s0.clone()

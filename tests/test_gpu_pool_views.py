@@ -53,11 +53,13 @@ def _decode_inputs(gen, B, C, Hv):
             torch.randn(B, Hv, generator=gen).to(BF16))
 
 
-@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("fused", ["separate", "two_launch", "one_launch", "one_launch_norm"])
 def test_decode_on_layer_views_config2(pkg, dev, fused):
     """Config 2 geometry (B = 256 of 512 slots, 16 heads, D = 128): the
-    in-place decode (conv kernel + recurrent kernel), or the fused decode
-    (q/k conv + fused gates / v conv / update), on s_pool[:, l] /
+    in-place decode (conv kernel + recurrent kernel), the fused decode after
+    the q/k conv (fused gates / v conv / update), or the one-launch step the
+    layer runs at this batch (q = k = NULL: the q/k conv and its roll in the
+    same kernel, with or without the fused gated norm), on s_pool[:, l] /
     conv_pool[:, l] equals the same calls on dense copies of that layer."""
     c = bench.make_decode()
     Hk, Hv, D = c["Hk"], c["Hv"], c["D"]
@@ -74,10 +76,19 @@ def test_decode_on_layer_views_config2(pkg, dev, fused):
     w, A_log, dt_bias = c["conv_w"].to(dev), c["A_log"].to(dev), c["dt_bias"].to(dev)
     kd = Hk * D
 
+    z = torch.randn(x.shape[0], Hv * D, generator=gen).to(BF16).to(dev)
+    nw = (1 + 0.02 * torch.randn(D, generator=gen)).to(BF16).to(dev)
+    assert x.shape[0] * Hv >= pkg.ops.WHOLE_HEAD_TILES and Hk == Hv   # the one-launch form applies
+
     def step(sp, cp):
-        if fused:
+        if fused == "two_launch":
             qk = pkg.ops.conv_decode_step(x[:, :2 * kd], cp[:, :2 * kd], ids, w[:2 * kd])
             return pkg.ops.recurrent_decode_fused(qk, x, cp, w, b, a, A_log, dt_bias, sp, ids, Hk, Hv, D)
+        if fused == "one_launch":
+            return pkg.ops.recurrent_decode_fused(None, x, cp, w, b, a, A_log, dt_bias, sp, ids, Hk, Hv, D)
+        if fused == "one_launch_norm":
+            return pkg.ops.recurrent_decode_fused(None, x, cp, w, b, a, A_log, dt_bias, sp, ids, Hk, Hv, D, z=z,
+                                                  norm_weight=nw, eps=1e-6)
         g, beta = pkg.ops.fused_g_beta(b, a, A_log, dt_bias, None)
         y = pkg.ops.conv_decode_step(x, cp, ids, w)
         q = y[:, :kd].view(-1, 1, Hk, D)

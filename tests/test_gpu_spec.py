@@ -66,3 +66,36 @@ def test_spec_verify_steps_without_commit(pkg, dev, B, T, Hk, Hv, D, slots):
     assert_state(pool.cpu()[ids], ref_state, "committed states vs oracle")
     untouched = [i for i in range(slots) if i not in ids.tolist()]
     assert torch.equal(pool.cpu()[untouched], pool0[untouched])
+
+
+def test_spec_verify_accepted_out_of_range_reads_pool_row(pkg, dev):
+    """An accepted count outside 1..T (0, or T + 1 from a caller that counts the
+    bonus token) makes the next verify start that row from its pool row, as the
+    commit copy leaves such a row untouched: both paths agree bit for bit, and
+    no state past the [B, T] buffer is read."""
+    gen = torch.Generator().manual_seed(72)
+    B, T, Hk, Hv, D, slots = 6, 3, 2, 4, 128, 9
+    A_log = (torch.rand(Hv, generator=gen) * 2.7).to(BF16)
+    dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(BF16)
+    pool0 = torch.randn(slots, Hv, D, D, generator=gen) * 0.1
+    ids = torch.randperm(slots, generator=gen)[:B].to(dev)
+    pool = pool0.to(dev)
+    pool_commit = pool0.clone().to(dev)
+    spec = pkg.ops.SpecVerify(pool)
+    inter_c = torch.empty(B, T, Hv, D, D, device=dev)
+    acc = torch.tensor([0, T + 1, 1, T, 0, T + 1], dtype=torch.int64, device=dev)
+    for step in range(2):
+        q, k, v, a, b = _step_inputs(gen, B, T, Hk, Hv, D)
+        g, beta = gdn_ref.g_beta(b, a, A_log, dt_bias)
+        args = (q.to(dev), k.to(dev), v.to(dev), g.view(B, T, Hv).to(dev), beta.view(B, T, Hv).to(dev))
+        out = spec.verify(*args, ids)
+        spec.accept(acc)
+        out_c = pkg.ops.recurrent_gdn_multitoken(*args, pool_commit, ids, inter_c)
+        pkg.ops.commit_states(pool_commit, ids, inter_c, acc)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), out_c.view(torch.int16)), f"step {step}: outputs vs commit path"
+    spec.commit()
+    torch.cuda.synchronize()
+    assert torch.equal(pool, pool_commit), "committed pool vs commit-copy path"
+    rows = [0, 1, 4, 5]
+    assert torch.equal(pool.cpu()[ids.cpu()[rows]], pool0[ids.cpu()[rows]]), "out-of-range rows keep their pool rows"

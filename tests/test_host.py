@@ -187,6 +187,76 @@ def test_install_replaces_padded_method(pkg, monkeypatch):
     pkg.integration.uninstall(mod, prev)
 
 
+@pytest.mark.parametrize("flag", ["_USE_GDN_GBETA", "_USE_CONV_TRITON", "_USE_GDN_INPLACE"])
+def test_installed_methods_read_switches_at_call_time(pkg, monkeypatch, flag):
+    """The reference's layer reads _USE_GDN_GBETA, _USE_CONV_TRITON and
+    _USE_GDN_INPLACE on every call (qwen3_5.py:933, :978, :1011, :1024).
+    Flipped on the module after install, the installed fused methods run the
+    original methods (which read the flags themselves); flipped back, the
+    fused path runs again.  The prefill method follows the gate and conv
+    switches (its reference form reads no in-place switch)."""
+    import types as _types
+
+    mod = _types.ModuleType("qwen3_5_stub")
+    mod._USE_GDN_GBETA = mod._USE_CONV_TRITON = mod._USE_GDN_INPLACE = True
+    calls = []
+
+    class Qwen3_5GatedDeltaNet:
+        def _gdn_prefill_varlen(self, hidden, lens_q, ids):
+            return "original prefill"
+
+        def _gdn_padded(self, x, lens, ids, T):
+            return "original padded"
+
+    mod.Qwen3_5GatedDeltaNet = Qwen3_5GatedDeltaNet
+    mod._varlen_meta = lambda lens_q: (None, None, None, None)
+
+    class _Stop(Exception):
+        pass
+
+    def fused(*a, **k):
+        calls.append("fused")
+        raise _Stop
+
+    monkeypatch.setattr(pkg.ops, "conv_chunk_prefill_varlen", fused)
+    monkeypatch.setattr(pkg.ops, "recurrent_decode_fused", fused)
+    monkeypatch.setattr(pkg.ops, "conv_decode_step", lambda *a, **k: None)
+    prev = pkg.integration.install(mod)
+    try:
+        layer = Qwen3_5GatedDeltaNet()
+        layer.conv_kernel, layer.num_k_heads, layer.num_v_heads = 4, 2, 4
+        layer.head_k_dim = layer.head_v_dim = 8
+        layer.key_dim, layer.value_dim, layer.conv_dim = 16, 32, 64
+        layer.A_log = layer.dt_bias = torch.zeros(4)
+        layer._v_head_slice = slice(0, 4)
+        layer.in_proj_b = layer.in_proj_a = lambda h: torch.zeros(*h.shape[:-1], 4)
+        layer.in_proj_z = lambda h: torch.zeros(*h.shape[:-1], 32)
+        layer.in_proj_qkv = lambda h: h
+        layer.conv1d = _types.SimpleNamespace(weight=torch.zeros(64, 1, 4))
+        layer.conv_cache, layer.s_cache = torch.zeros(3, 64, 3), None
+        layer.norm = _types.SimpleNamespace(weight=torch.ones(8), eps=1e-6)
+        x = torch.zeros(2, 64)
+
+        def run():
+            out = []
+            for fn, args in ((layer._gdn_prefill_varlen, (x, [1, 1], None)),
+                             (layer._gdn_padded, (x.view(2, 1, 64), None, None, 1))):
+                try:
+                    out.append(fn(*args))
+                except _Stop:
+                    out.append("fused")
+            return out
+
+        assert run() == ["fused", "fused"]
+        setattr(mod, flag, False)
+        expect_prefill = "fused" if flag == "_USE_GDN_INPLACE" else "original prefill"
+        assert run() == [expect_prefill, "original padded"]
+        setattr(mod, flag, True)
+        assert run() == ["fused", "fused"]
+    finally:
+        pkg.integration.uninstall(mod, prev)
+
+
 def test_ops_have_no_cpu_path(pkg):
     a = torch.zeros(4, 2, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU only"):

@@ -63,7 +63,9 @@ def test_noalloc_rejects_calls_beyond_the_array(pkg, dev):
     lib = pkg._lib.load()
     need = lib.gdn_conv_chunk_prefill_workspace_size(40000, 8, Hv, D)
     assert need > pkg._lib.NOALLOC_SCRATCH_BYTES
-    st = lib.gdn_conv_chunk_prefill_noalloc(1 << 20, 6144, 1 << 20, 18432, 3, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
-                                            1 << 20, 0, 1 << 20, 1 << 20, None, None, Hv * D * D, 1 << 20, None, 0,
-                                            8, 40000, Hk, Hv, D, 1.0, 1, 1 << 20, None)
+    # every pointer NULL: the size check comes first; were it moved behind the
+    # launch path, the NULL operands would be rejected there instead
+    st = lib.gdn_conv_chunk_prefill_noalloc(None, 6144, None, 18432, 3, None, None, None, None,
+                                            None, 0, None, None, None, None, Hv * D * D, None, None, 0,
+                                            8, 40000, Hk, Hv, D, 1.0, 1, None, None)
     assert st == pkg._lib.GDN_ERR_SCRATCH
