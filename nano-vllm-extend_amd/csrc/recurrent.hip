@@ -9,13 +9,19 @@
 //
 // HBM-bound: the D x D fp32 state tile of each (sequence, head) is read once
 // into registers and written once (plus optional per-token states).  The
-// state stores are non-temporal: a layer's states come back only after every
-// other layer's have streamed through, so allocating them in the caches only
-// evicts other data (measured: 6 % faster with the pool out of cache, the
-// same with it cached).  One
-// workgroup of 256 threads owns a (sequence, head, v-block) tile of D x VB
-// columns, VB = D / NVB; each thread holds float4 column groups of NP rows so
-// every wave access is a contiguous run of VB*4 bytes per row.
+// state stores are non-temporal, and so are the state loads of one-token
+// decode: a layer's states come back only after every other layer's have
+// streamed through, so allocating them in the caches only evicts other data
+// (an in-place pass over config 2's tiles: 108 us with cached loads, 96 us
+// with non-temporal ones).  The multi-token form keeps cached loads (its
+// start states were often written by the previous step: 104 us cached, 130 us
+// non-temporal at config 4).  One workgroup of 64 * NW threads owns a
+// (sequence, head, v-block) tile of D x VB columns, VB = D / NVB; each thread
+// holds float4 column groups of NP rows so every wave access is a contiguous
+// run of VB*4 bytes per row.  One-token decode of whole-head tiles (NVB = 1,
+// D = 128) runs 8 waves (config 2: 103.4 us at 4 waves, 101.4 us at 8; 16
+// waves need more registers than two workgroups per CU leave and measured
+// 118.7 us).
 #include "gdn_common.h"
 
 namespace {
@@ -28,9 +34,12 @@ namespace {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const float* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0), 0x7fffffff, 0x00020000);
 }
+template <int kPolicy>
 __device__ __forceinline__ float4 tile_ld(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kPolicy));
 }
+constexpr int kLoadCached = 0;
+constexpr int kLoadNT = 2;  // non-temporal (cache policy bit nt)
 __device__ __forceinline__ void tile_st_nt(__amdgpu_buffer_rsrc_t r, int voff, int soff, const float4& v) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, soff, 2);
@@ -93,14 +102,16 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   constexpr int RPP = 64 * NW / CPR;  // rows per pass of the workgroup
   constexpr int NP = D / RPP;     // passes (float4 registers per thread)
   static_assert(CPR <= 64 && 64 % CPR == 0 && NP >= 1, "tile shape");
-  // the in-kernel q/k conv gives thread t channel t % 128 of q (t < 128) or
-  // of k (t >= 128): it needs exactly 256 threads and D <= 128
-  static_assert(!kFused || (NW == 4 && D <= 128), "fused q/k conv needs four waves");
+  // the in-kernel q/k conv gives thread t < 256 channel t % 128 of q (t < 128)
+  // or of k: it needs at least 256 threads and D <= 128
+  static_assert(!kFused || (NW >= 4 && D <= 128), "fused q/k conv needs at least four waves");
 
   __shared__ float sq[2][D];
   __shared__ float sk[2][D];
   __shared__ float skq[2];
   __shared__ float red[2][NW][2][VB];
+  __shared__ float tot[NW > 4 ? 2 : 1][2][VB];  // NW > 4: column totals of S^T k and S^T q
+  __shared__ float svv[2][VB];                  // fused: the v channels' conv outputs
 
   const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(B) * Hv * NVB);
   if (wi < 0) return;
@@ -129,7 +140,7 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   // q (t < 128) or k; its raw input, taps and weights are loaded ahead of the
   // state tile so their latency overlaps the tile's loads
   const int qpart = tid >> 7, qci = tid & 127;
-  const bool qact = kFused && din.xqk && qci < D;
+  const bool qact = kFused && din.xqk && tid < 256 && qci < D;
   const int64_t qch = (qpart ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + qci;
   uint16_t qx = 0, qs[3] = {0, 0, 0};
   uint2 qw = make_uint2(0u, 0u);
@@ -143,8 +154,13 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   float4 S[NP];
   {
     const __amdgpu_buffer_rsrc_t r = tile_rsrc(sin);
+    if (T == 1) {
 #pragma unroll
-    for (int j = 0; j < NP; ++j) S[j] = tile_ld(r, voff, j * kPass);
+      for (int j = 0; j < NP; ++j) S[j] = tile_ld<kLoadNT>(r, voff, j * kPass);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NP; ++j) S[j] = tile_ld<kLoadCached>(r, voff, j * kPass);
+    }
   }
 
   for (int t = 0; t < T; ++t) {
@@ -214,11 +230,14 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
     uint16_t vx[4], vs[4][3];  // fused: the raw v inputs and the old state taps, for the roll
     if constexpr (kFused) {
       // the gate kernel's arithmetic (g in fp32, beta rounded to bf16), and the
-      // decode conv of this thread's 4 v channels (rounded to bf16 as the conv
-      // kernel's output is)
+      // decode conv of the 4 v channels of this thread's columns (rounded to
+      // bf16 as the conv kernel's output is), by the threads of row group 0,
+      // which share the results through svv
       eg = expf(gdn::gate_g(gdn::bf2f(din.a[gi]), gdn::load_param(din.A_log, h, din.param_f32),
                             gdn::load_param(din.dt_bias, h, din.param_f32)));
       bt = gdn::bf2f(gdn::gate_beta(gdn::bf2f(din.b[gi])));
+    }
+    if (kFused && r0 == 0) {
       const int64_t ch = static_cast<int64_t>(h) * D + col;
       const uint2 xu = *reinterpret_cast<const uint2*>(din.xv + static_cast<int64_t>(b) * din.sx + ch);
       const uint4 w01 = reinterpret_cast<const uint4*>(din.wv + ch * 4)[0];
@@ -238,8 +257,9 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
         vx[i] = xs[i];
         vv[i] = gdn::bf2f(gdn::f2bf(gdn::conv_decode_silu(gdn::bf2f(xs[i]), gdn::bf2f(vs[i][0]), gdn::bf2f(vs[i][1]),
                                                           gdn::bf2f(vs[i][2]), wk)));
+        svv[buf][c4 * 4 + i] = vv[i];
       }
-    } else {
+    } else if constexpr (!kFused) {
       eg = expf(g[gi]);
       bt = gdn::bf2f(beta[gi]);
       const uint16_t* vp = v + static_cast<int64_t>(b) * sv_b + static_cast<int64_t>(t) * sv_t + static_cast<int64_t>(h) * D + col;
@@ -250,7 +270,11 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
     }
     __syncthreads();
     if constexpr (kFused) {
-      // every thread of these columns has read the old taps: roll (bit copies)
+      if (r0 != 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vv[i] = svv[buf][c4 * 4 + i];
+      }
+      // the old taps have been read (by these same threads): roll (bit copies)
       if (r0 == 0) {
         uint16_t* sp = din.vpool + row * din.sp_slot + (static_cast<int64_t>(h) * D + col) * din.sp_ch;
 #pragma unroll
@@ -292,16 +316,35 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
     // --- delta, state update, output ---
     const float kq = skq[buf];
     float delta[4], out[4];
+    if constexpr (NW > 4) {
+      // the wave partials summed once per column (waves in order), then read
+      // back by every thread
+      if (tid < 2 * VB) {
+        const int sel = tid / VB, c = tid % VB;
+        float acc = red[buf][0][sel][c];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float kvt = red[buf][0][0][c4 * 4 + i], qvt = red[buf][0][1][c4 * 4 + i];
-#pragma unroll
-      for (int w = 1; w < NW; ++w) {
-        kvt += red[buf][w][0][c4 * 4 + i];
-        qvt += red[buf][w][1][c4 * 4 + i];
+        for (int w = 1; w < NW; ++w) acc += red[buf][w][sel][c];
+        tot[0][sel][c] = acc;
       }
-      delta[i] = (vv[i] - kvt) * bt;
-      out[i] = qvt + delta[i] * kq;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        delta[i] = (vv[i] - tot[0][0][c4 * 4 + i]) * bt;
+        out[i] = tot[0][1][c4 * 4 + i] + delta[i] * kq;
+      }
+      // (tot is rewritten only after the next token's first barrier)
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float kvt = red[buf][0][0][c4 * 4 + i], qvt = red[buf][0][1][c4 * 4 + i];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+          kvt += red[buf][w][0][c4 * 4 + i];
+          qvt += red[buf][w][1][c4 * 4 + i];
+        }
+        delta[i] = (vv[i] - kvt) * bt;
+        out[i] = qvt + delta[i] * kq;
+      }
     }
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
@@ -377,15 +420,15 @@ __global__ __launch_bounds__(256) void state_commit_kernel(float* __restrict__ p
 }
 
 // Measurement pass: each selected state tile read into registers and written
-// back unchanged, with the decode kernel's layout (NVB = 1, 4 waves), cache
-// policy and barrier between the loads and the stores: one decode step's
-// state traffic without its arithmetic.  With dst != src the tiles land at
+// back unchanged, with the one-token decode kernel's layout (NVB = 1; 8 waves
+// at D = 128), cache policy and barrier between the loads and the stores: one
+// decode step's state traffic without its arithmetic.  With dst != src the tiles land at
 // the same offsets of a second pool (the out-of-place form of the same pass).
-template <int D>
-__global__ __launch_bounds__(256) void state_tile_pass_kernel(const float* src, float* dst, int64_t slot_stride,
-                                                              const int64_t* __restrict__ ids, int B, int Hv) {
+template <int D, int NT>
+__global__ __launch_bounds__(NT) void state_tile_pass_kernel(const float* src, float* dst, int64_t slot_stride,
+                                                             const int64_t* __restrict__ ids, int B, int Hv) {
   constexpr int CPR = D / 4;
-  constexpr int RPP = 256 / CPR;
+  constexpr int RPP = NT / CPR;
   constexpr int NP = D / RPP;
   constexpr int kPass = RPP * D * 4;
   const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(B) * Hv);
@@ -398,7 +441,7 @@ __global__ __launch_bounds__(256) void state_tile_pass_kernel(const float* src, 
   const int voff = ((threadIdx.x / CPR) * D + (threadIdx.x % CPR) * 4) * 4;
   float4 S[NP];
 #pragma unroll
-  for (int j = 0; j < NP; ++j) S[j] = tile_ld(r, voff, j * kPass);
+  for (int j = 0; j < NP; ++j) S[j] = tile_ld<kLoadNT>(r, voff, j * kPass);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < NP; ++j) tile_st_nt(w, voff, j * kPass, S[j]);
@@ -466,7 +509,7 @@ extern "C" int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, cons
 #define GDN_REC_ARGS q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, \
                      s_out_stride, ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src, s
   if (D == 128) {
-    if (nvb == 1) return launch_recurrent<128, 1>(GDN_REC_ARGS);
+    if (nvb == 1) return T == 1 ? launch_recurrent<128, 1, 8>(GDN_REC_ARGS) : launch_recurrent<128, 1>(GDN_REC_ARGS);
     if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);
     return launch_recurrent<128, 4>(GDN_REC_ARGS);
   }
@@ -539,7 +582,7 @@ extern "C" int gdn_recurrent_decode_fused(const uint16_t* q, int64_t sq_b, const
 #define GDN_REC_ARGS q, sq_b, 0, k, sk_b, 0, nullptr, 0, 0, nullptr, nullptr, s_pool, s_stride, s_pool, s_stride, \
                      ids, nullptr, o, B, 1, Hk, Hv, scale, l2norm, din, nin, src, s
   if (D == 128) {
-    if (nvb == 1) return launch_recurrent<128, 1>(GDN_REC_ARGS);
+    if (nvb == 1) return launch_recurrent<128, 1, 8>(GDN_REC_ARGS);
     if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);
     return launch_recurrent<128, 4>(GDN_REC_ARGS);
   }
@@ -559,12 +602,13 @@ static int state_tile_pass(const float* src, float* dst, int64_t slot_stride, co
   const int64_t work = static_cast<int64_t>(B) * Hv;
   const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (D == 128)
-    state_tile_pass_kernel<128><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(src, dst, slot_stride, ids,
-                                                                                         B, Hv);
-  else
-    state_tile_pass_kernel<64><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(src, dst, slot_stride, ids, B,
-                                                                                       Hv);
+  if (D == 128) {
+    state_tile_pass_kernel<128, 512><<<dim3(static_cast<unsigned>(grid)), dim3(512), 0, s>>>(src, dst, slot_stride,
+                                                                                            ids, B, Hv);
+  } else {
+    state_tile_pass_kernel<64, 256><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(src, dst, slot_stride,
+                                                                                           ids, B, Hv);
+  }
   return gdn_launch_status();
 }
 
