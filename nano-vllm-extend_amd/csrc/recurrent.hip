@@ -89,7 +89,7 @@ struct SrcIn {
   int T_src;
 };
 
-template <int D, int NVB, int NW, bool kFused>
+template <int D, int NVB, int NW, bool kFused, int kPolicy>
 __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
     const uint16_t* __restrict__ q, int64_t sq_b, int64_t sq_t, const uint16_t* __restrict__ k,
     int64_t sk_b, int64_t sk_t, const uint16_t* __restrict__ v, int64_t sv_b, int64_t sv_t,
@@ -102,9 +102,8 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   constexpr int RPP = 64 * NW / CPR;  // rows per pass of the workgroup
   constexpr int NP = D / RPP;     // passes (float4 registers per thread)
   static_assert(CPR <= 64 && 64 % CPR == 0 && NP >= 1, "tile shape");
-  // the in-kernel q/k conv gives thread t < 256 channel t % 128 of q (t < 128)
-  // or of k: it needs at least 256 threads and D <= 128
-  static_assert(!kFused || (NW >= 4 && D <= 128), "fused q/k conv needs at least four waves");
+  // the fused v conv gives each of the tile's VB columns a thread
+  static_assert(!kFused || 64 * NW >= VB, "fused v conv: a thread per column");
 
   __shared__ float sq[2][D];
   __shared__ float sk[2][D];
@@ -136,51 +135,77 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
   // byte offset of this lane's float4 in the tile, and of row pass j
   const int voff = (r0 * D + col) * 4;
   constexpr int kPass = RPP * D * 4;
-  // q/k conv in the kernel (one token): thread t convolves channel t % 128 of
-  // q (t < 128) or k; its raw input, taps and weights are loaded ahead of the
-  // state tile so their latency overlaps the tile's loads
-  const int qpart = tid >> 7, qci = tid & 127;
-  const bool qact = kFused && din.xqk && tid < 256 && qci < D;
-  const int64_t qch = (qpart ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + qci;
-  uint16_t qx = 0, qs[3] = {0, 0, 0};
-  uint2 qw = make_uint2(0u, 0u);
-  if (qact) {
-    qx = din.xqk[static_cast<int64_t>(b) * din.sx + qch];
-    const uint16_t* sp = din.qkpool + row * din.sp_slot + qch * din.sp_ch;
-#pragma unroll
-    for (int j = 0; j < 3; ++j) qs[j] = sp[j];
-    qw = *reinterpret_cast<const uint2*>(din.wqk + qch * 4);
+  // Fused: the decode conv (one token) of the head's channels, one channel
+  // per thread: with din.xqk thread t < 3 D takes channel t % D of part
+  // t / D (q, k, v), else thread t < VB the v channel of column t.  Its raw
+  // input, taps and weights are loaded ahead of the state tile so their
+  // latency overlaps the tile's loads.
+  int cpart = -1, cci = 0;
+  if (kFused) {
+    if (din.xqk) {
+      if (tid < 3 * D) { cpart = tid / D; cci = tid % D; }
+    } else if (tid < VB) {
+      cpart = 2;
+      cci = tid;
+    }
   }
+  const bool cv_v = cpart == 2;
+  const int64_t cch = cv_v ? static_cast<int64_t>(h) * D + vb * VB + cci
+                           : (cpart == 1 ? din.key_dim : 0) + static_cast<int64_t>(kh) * D + cci;
+  uint16_t* ctap = nullptr;
+  uint16_t cx = 0, cs[3] = {0, 0, 0};
+  uint2 cw = make_uint2(0u, 0u);
+  if (cpart >= 0) {
+    cx = (cv_v ? din.xv : din.xqk)[static_cast<int64_t>(b) * din.sx + cch];
+    ctap = (cv_v ? din.vpool : din.qkpool) + row * din.sp_slot + cch * din.sp_ch;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) cs[j] = ctap[j];
+    cw = *reinterpret_cast<const uint2*>((cv_v ? din.wv : din.wqk) + cch * 4);
+  }
+  // Fused (one token): the gate inputs, and the gate row and weight of the
+  // norm epilogue, also go out ahead of the tile.
+  uint16_t g_a = 0, g_b = 0;
+  float g_alog = 0.f, g_dtb = 0.f;
+  uint2 n_z = make_uint2(0u, 0u), n_w = make_uint2(0u, 0u);
+  if constexpr (kFused) {
+    const int64_t gi0 = static_cast<int64_t>(b) * Hv + h;
+    g_a = din.a[gi0];
+    g_b = din.b[gi0];
+    g_alog = gdn::load_param(din.A_log, h, din.param_f32);
+    g_dtb = gdn::load_param(din.dt_bias, h, din.param_f32);
+    if (NVB == 1 && nin.z && r0 == 0) {
+      n_z = *reinterpret_cast<const uint2*>(nin.z + static_cast<int64_t>(b) * nin.sz + static_cast<int64_t>(h) * D +
+                                             col);
+      n_w = *reinterpret_cast<const uint2*>(nin.w + col);
+    }
+  }
+  // one load sequence (a branch between two would make the compiler wait for
+  // the whole tile before the conv above can use its inputs)
   float4 S[NP];
   {
     const __amdgpu_buffer_rsrc_t r = tile_rsrc(sin);
-    if (T == 1) {
 #pragma unroll
-      for (int j = 0; j < NP; ++j) S[j] = tile_ld<kLoadNT>(r, voff, j * kPass);
-    } else {
-#pragma unroll
-      for (int j = 0; j < NP; ++j) S[j] = tile_ld<kLoadCached>(r, voff, j * kPass);
-    }
+    for (int j = 0; j < NP; ++j) S[j] = tile_ld<kPolicy>(r, voff, j * kPass);
   }
 
   for (int t = 0; t < T; ++t) {
     const int buf = t & 1;
-    if (kFused && din.xqk) {
-      // the decode conv of this thread's q or k channel (the conv kernel's
-      // arithmetic, its output rounded to bf16) into sq / sk, then its roll
-      // (bit copies; this thread alone reads these taps).  One token.
-      if (qact) {
-        const uint16_t* wsv = reinterpret_cast<const uint16_t*>(&qw);
+    if (kFused) {
+      // the conv of this thread's channel (the conv kernel's arithmetic, its
+      // output rounded to bf16) into sq / sk / svv, then its roll (bit
+      // copies; this thread alone reads and writes these taps).  One token.
+      if (cpart >= 0) {
+        const uint16_t* wsv = reinterpret_cast<const uint16_t*>(&cw);
         const float wk[4] = {gdn::bf2f(wsv[0]), gdn::bf2f(wsv[1]), gdn::bf2f(wsv[2]), gdn::bf2f(wsv[3])};
         const float y = gdn::bf2f(gdn::f2bf(
-            gdn::conv_decode_silu(gdn::bf2f(qx), gdn::bf2f(qs[0]), gdn::bf2f(qs[1]), gdn::bf2f(qs[2]), wk)));
-        (qpart ? sk : sq)[buf][qci] = y;
-        uint16_t* sp = din.qkpool + row * din.sp_slot + qch * din.sp_ch;
-        sp[0] = qs[1];
-        sp[1] = qs[2];
-        sp[2] = qx;
+            gdn::conv_decode_silu(gdn::bf2f(cx), gdn::bf2f(cs[0]), gdn::bf2f(cs[1]), gdn::bf2f(cs[2]), wk)));
+        float* dst = cpart == 0 ? &sq[buf][0] : cpart == 1 ? &sk[buf][0] : &svv[buf][0];
+        dst[cci] = y;
+        ctap[0] = cs[1];
+        ctap[1] = cs[2];
+        ctap[2] = cx;
       }
-      __syncthreads();
+      if (din.xqk) __syncthreads();
     }
     // --- q, k of this token: wave 0 normalises and publishes them ---
     if (wave == 0) {
@@ -227,39 +252,11 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
     const int64_t gi = (static_cast<int64_t>(b) * T + t) * Hv + h;
     float eg, bt;
     float vv[4];
-    uint16_t vx[4], vs[4][3];  // fused: the raw v inputs and the old state taps, for the roll
     if constexpr (kFused) {
-      // the gate kernel's arithmetic (g in fp32, beta rounded to bf16), and the
-      // decode conv of the 4 v channels of this thread's columns (rounded to
-      // bf16 as the conv kernel's output is), by the threads of row group 0,
-      // which share the results through svv
-      eg = expf(gdn::gate_g(gdn::bf2f(din.a[gi]), gdn::load_param(din.A_log, h, din.param_f32),
-                            gdn::load_param(din.dt_bias, h, din.param_f32)));
-      bt = gdn::bf2f(gdn::gate_beta(gdn::bf2f(din.b[gi])));
-    }
-    if (kFused && r0 == 0) {
-      const int64_t ch = static_cast<int64_t>(h) * D + col;
-      const uint2 xu = *reinterpret_cast<const uint2*>(din.xv + static_cast<int64_t>(b) * din.sx + ch);
-      const uint4 w01 = reinterpret_cast<const uint4*>(din.wv + ch * 4)[0];
-      const uint4 w23 = reinterpret_cast<const uint4*>(din.wv + ch * 4)[1];
-      const uint16_t* sp = din.vpool + row * din.sp_slot + ch * din.sp_ch;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) vs[i][j] = sp[static_cast<int64_t>(i) * din.sp_ch + j];
-      const uint16_t* xs = reinterpret_cast<const uint16_t*>(&xu);
-      const uint16_t* ws = reinterpret_cast<const uint16_t*>(&w01);
-      const uint16_t* ws2 = reinterpret_cast<const uint16_t*>(&w23);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint16_t* wi = i < 2 ? ws + 4 * i : ws2 + 4 * (i - 2);
-        const float wk[4] = {gdn::bf2f(wi[0]), gdn::bf2f(wi[1]), gdn::bf2f(wi[2]), gdn::bf2f(wi[3])};
-        vx[i] = xs[i];
-        vv[i] = gdn::bf2f(gdn::f2bf(gdn::conv_decode_silu(gdn::bf2f(xs[i]), gdn::bf2f(vs[i][0]), gdn::bf2f(vs[i][1]),
-                                                          gdn::bf2f(vs[i][2]), wk)));
-        svv[buf][c4 * 4 + i] = vv[i];
-      }
-    } else if constexpr (!kFused) {
+      // the gate kernel's arithmetic (g in fp32, beta rounded to bf16); one token
+      eg = expf(gdn::gate_g(gdn::bf2f(g_a), g_alog, g_dtb));
+      bt = gdn::bf2f(gdn::gate_beta(gdn::bf2f(g_b)));
+    } else {
       eg = expf(g[gi]);
       bt = gdn::bf2f(beta[gi]);
       const uint16_t* vp = v + static_cast<int64_t>(b) * sv_b + static_cast<int64_t>(t) * sv_t + static_cast<int64_t>(h) * D + col;
@@ -270,20 +267,8 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
     }
     __syncthreads();
     if constexpr (kFused) {
-      if (r0 != 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[i] = svv[buf][c4 * 4 + i];
-      }
-      // the old taps have been read (by these same threads): roll (bit copies)
-      if (r0 == 0) {
-        uint16_t* sp = din.vpool + row * din.sp_slot + (static_cast<int64_t>(h) * D + col) * din.sp_ch;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sp[static_cast<int64_t>(i) * din.sp_ch] = vs[i][1];
-          sp[static_cast<int64_t>(i) * din.sp_ch + 1] = vs[i][2];
-          sp[static_cast<int64_t>(i) * din.sp_ch + 2] = vx[i];
-        }
-      }
+      for (int i = 0; i < 4; ++i) vv[i] = svv[buf][c4 * 4 + i];
     }
 
     // --- decay, then partial S^T k and S^T q over this thread's rows ---
@@ -357,6 +342,12 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
 #pragma unroll
       for (int j = 0; j < NP; ++j) tile_st_nt(r, voff, j * kPass, S[j]);
     }
+    if (s_out && t == T - 1) {
+      // the final state goes out before the output epilogue
+      const __amdgpu_buffer_rsrc_t r = tile_rsrc(s_out + row * s_out_stride + static_cast<int64_t>(h) * D * D);
+#pragma unroll
+      for (int j = 0; j < NP; ++j) tile_st_nt(r, voff, j * kPass, S[j]);
+    }
     if (r0 == 0) {
       uint2 u;
       uint16_t* us = reinterpret_cast<uint16_t*>(&u);
@@ -381,11 +372,8 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
 #pragma unroll
         for (int m = D / 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, 2 * m, 64);
         const float r = rsqrtf(ss / static_cast<float>(D) + nin.eps);
-        const uint2 zu = *reinterpret_cast<const uint2*>(nin.z + static_cast<int64_t>(b) * nin.sz +
-                                                         static_cast<int64_t>(h) * D + col);
-        const uint2 wu = *reinterpret_cast<const uint2*>(nin.w + col);
-        const uint16_t* zs = reinterpret_cast<const uint16_t*>(&zu);
-        const uint16_t* ws = reinterpret_cast<const uint16_t*>(&wu);
+        const uint16_t* zs = reinterpret_cast<const uint16_t*>(&n_z);
+        const uint16_t* ws = reinterpret_cast<const uint16_t*>(&n_w);
         u.x = gdn::f2bf2(gdn::norm_gate(x[0], r, gdn::bf2f(ws[0]), gdn::bf2f(zs[0])),
                          gdn::norm_gate(x[1], r, gdn::bf2f(ws[1]), gdn::bf2f(zs[1])));
         u.y = gdn::f2bf2(gdn::norm_gate(x[2], r, gdn::bf2f(ws[2]), gdn::bf2f(zs[2])),
@@ -393,12 +381,6 @@ __global__ __launch_bounds__(64 * NW) void recurrent_kernel(
       }
       *reinterpret_cast<uint2*>(o + gi * D + col) = u;
     }
-  }
-
-  if (s_out) {
-    const __amdgpu_buffer_rsrc_t r = tile_rsrc(s_out + row * s_out_stride + static_cast<int64_t>(h) * D * D);
-#pragma unroll
-    for (int j = 0; j < NP; ++j) tile_st_nt(r, voff, j * kPass, S[j]);
   }
 }
 
@@ -447,24 +429,45 @@ __global__ __launch_bounds__(NT) void state_tile_pass_kernel(const float* src, f
   for (int j = 0; j < NP; ++j) tile_st_nt(w, voff, j * kPass, S[j]);
 }
 
-template <int D, int NVB, int NW = 4>
+template <int D, int NVB, int NW, int kPolicy>
+int launch_recurrent_t(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k, int64_t sk_b,
+                     int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t, const float* g,
+                     const uint16_t* beta, const float* s_in, int64_t s_in_stride, float* s_out,
+                     int64_t s_out_stride, const int64_t* ids, float* inter, uint16_t* o, int B,
+                     int T, int Hk, int Hv, float scale, int l2norm, const DecodeIn& din, const NormIn& nin,
+                     const SrcIn& src, hipStream_t stream) {
+  // the fused conv gives each of a head's channels a thread
+  if (din.xqk && (NVB != 1 || 64 * NW < 3 * D)) return GDN_ERR_INVALID_ARG;
+  const int64_t work = static_cast<int64_t>(B) * Hv * NVB;
+  const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
+  if (din.xv)
+    recurrent_kernel<D, NVB, NW, true, kPolicy><<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, stream>>>(
+        q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
+        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
+  else
+    recurrent_kernel<D, NVB, NW, false, kPolicy><<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, stream>>>(
+        q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
+        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
+  return gdn_launch_status();
+}
+
+
+// One token: non-temporal state loads on NW1 waves; more tokens: cached
+// loads on 4 waves.
+template <int D, int NVB, int NW1 = 4>
 int launch_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, const uint16_t* k, int64_t sk_b,
                      int64_t sk_t, const uint16_t* v, int64_t sv_b, int64_t sv_t, const float* g,
                      const uint16_t* beta, const float* s_in, int64_t s_in_stride, float* s_out,
                      int64_t s_out_stride, const int64_t* ids, float* inter, uint16_t* o, int B,
                      int T, int Hk, int Hv, float scale, int l2norm, const DecodeIn& din, const NormIn& nin,
                      const SrcIn& src, hipStream_t stream) {
-  const int64_t work = static_cast<int64_t>(B) * Hv * NVB;
-  const int64_t grid = gdn::kNumXcd * ((work + gdn::kNumXcd - 1) / gdn::kNumXcd);
-  if (din.xv)
-    recurrent_kernel<D, NVB, NW, true><<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, stream>>>(
-        q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
-        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
-  else
-    recurrent_kernel<D, NVB, NW, false><<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), 0, stream>>>(
-        q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, s_out_stride,
-        ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src);
-  return gdn_launch_status();
+  if (T == 1)
+    return launch_recurrent_t<D, NVB, NW1, kLoadNT>(q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in,
+                                                    s_in_stride, s_out, s_out_stride, ids, inter, o, B, T, Hk, Hv,
+                                                    scale, l2norm, din, nin, src, stream);
+  return launch_recurrent_t<D, NVB, 4, kLoadCached>(q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in,
+                                                    s_in_stride, s_out, s_out_stride, ids, inter, o, B, T, Hk, Hv,
+                                                    scale, l2norm, din, nin, src, stream);
 }
 
 // v-split: more workgroups when there are few (b, h) tiles, so the launch
@@ -509,7 +512,7 @@ extern "C" int gdn_recurrent(const uint16_t* q, int64_t sq_b, int64_t sq_t, cons
 #define GDN_REC_ARGS q, sq_b, sq_t, k, sk_b, sk_t, v, sv_b, sv_t, g, beta, s_in, s_in_stride, s_out, \
                      s_out_stride, ids, inter, o, B, T, Hk, Hv, scale, l2norm, din, nin, src, s
   if (D == 128) {
-    if (nvb == 1) return T == 1 ? launch_recurrent<128, 1, 8>(GDN_REC_ARGS) : launch_recurrent<128, 1>(GDN_REC_ARGS);
+    if (nvb == 1) return launch_recurrent<128, 1, 8>(GDN_REC_ARGS);
     if (nvb == 2) return launch_recurrent<128, 2>(GDN_REC_ARGS);
     return launch_recurrent<128, 4>(GDN_REC_ARGS);
   }
