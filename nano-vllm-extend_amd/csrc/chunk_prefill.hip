@@ -860,7 +860,7 @@ struct __align__(16) StateSmem {
   uint16_t ot[2][32 * kCB];  // each output wave's bf16 tile on its way out, swz<64>
   uint16_t vtile[2][67 * 16];  // fused: each U wave's conv window rows (one k-step's 16 channels)
   float vw[2][32 * 4];         // fused: each U wave's 32 channels' conv taps (fp32)
-  int sflag[4];                // chain wave w: chunks whose S it has put in xs (sflag[w] = j + 1)
+  int sflag[2][64];            // chain wave w: chunks whose S it has put in xs (sflag[w][*] = j + 1)
 };
 
 constexpr int kStateWaves = 8;
@@ -1121,7 +1121,7 @@ __device__ __forceinline__ void o_inter(const QPrefetch<D>& p, const StateXchgS<
   constexpr int KS = D / 16;
   const int want = static_cast<int>(j) + 1;
   while (min(__hip_atomic_load(&sflag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
-             __hip_atomic_load(&sflag[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < want)
+             __hip_atomic_load(&sflag[64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < want)
     __builtin_amdgcn_s_sleep(1);
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
   h16x8_t sh[2][KS];
@@ -1347,25 +1347,30 @@ __device__ __forceinline__ void chain_pass(StateSmem<D>& sm, int ct, int vc0, in
     h16x8_t Sh[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) Sh[s] = (s & 1) ? pack_h8<8>(S[s >> 1]) : pack_h8<0>(S[s >> 1]);
+    // the exchange copy of S goes out at once (its flag follows the products,
+    // by when the writes have landed), and the decay of the old state sits
+    // between the products: nothing in this region waits on them
+    if constexpr (!kP) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) sm.xs.Sh[ct][s][ln] = Sh[s];
+    }
+#pragma unroll
+    for (int rt = 0; rt < NR; ++rt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) S[rt][e] *= eg;
 #pragma unroll
     for (int s = 0; s < KS - 1; ++s) {
       U[0] = mfma32(wf[0][s], Sh[s], U[0]);
       U[1] = mfma32(wf[1][s], Sh[s], U[1]);
     }
     U[0] = mfma32(wf[0][KS - 1], Sh[KS - 1], U[0]);
-    // the exchange copy of S (then the flag that says it is there), the decay
-    // of the old state and the update's operand reads, while W S runs
+    // the flag that says S is in the exchange: every lane stores the count to
+    // its own word (no branch, so the region above stays one schedule); the
+    // output waves read word 0
     if constexpr (!kP) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) sm.xs.Sh[ct][s][ln] = Sh[s];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-      if (ln == 0) __hip_atomic_store(&sm.sflag[ct], static_cast<int>(jc) + 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store(&sm.sflag[ct][ln], static_cast<int>(jc) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-#pragma unroll
-    for (int rt = 0; rt < NR; ++rt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) S[rt][e] *= eg;
     h16x8_t kf[NR][4];
 #pragma unroll
     for (int rt = 0; rt < NR; ++rt)
@@ -1513,7 +1518,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
     if (threadIdx.x == 0) s_base = part;
   }
-  if (threadIdx.x < 4) sm.sflag[threadIdx.x] = 0;
+  if (threadIdx.x < 128) sm.sflag[threadIdx.x >> 6][threadIdx.x & 63] = 0;
   __syncthreads();
   const int64_t cbase = s_base + c0;
   const int64_t rec_stride = static_cast<int64_t>(Hv) * rec_bytes(D);
@@ -1574,7 +1579,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       // the roll stays off the tail of the workgroups that finish last.
       if (roll) GDN_ROLL();
       // interval 0: S^T Q'^T of chunk 0
-      o_inter<D>(q0, sm.xs, sm.sflag, 0, lane, acc);
+      o_inter<D>(q0, sm.xs, &sm.sflag[0][0], 0, lane, acc);
       __builtin_amdgcn_sched_barrier(0);
       q_prefetch<D>(q0, rec0 + min<int64_t>(2, nch - 1) * rec_stride, nt, lane);
       gdn::keep_loads_here();
@@ -1584,7 +1589,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   __builtin_amdgcn_sched_barrier(0);                                                                        \
   a_prefetch(AP, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);                            \
   gdn::keep_loads_here();                                                                                   \
-  o_inter<D>(QC, sm.xs, sm.sflag, jj, lane, acc);                                                           \
+  o_inter<D>(QC, sm.xs, &sm.sflag[0][0], jj, lane, acc);                                                           \
   __builtin_amdgcn_sched_barrier(0);                                                                        \
   q_prefetch<D>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, nt, lane);                        \
   gdn::keep_loads_here();                                                                                   \
