@@ -1741,11 +1741,12 @@ struct ScanList {
 // P_s and R_s are loaded one step ahead and the barriers order LDS only, so
 // those loads stay in flight across them (every step issues the same loads,
 // the last one repeating itself).
+// (D = 64; D = 128 runs seg_scan_mfma_kernel below)
 template <int D>
 __global__ __launch_bounds__(256) void seg_scan_kernel(ScanList sl, int Hv) {
   constexpr int CB = 16;
   constexpr int NB = D / CB;
-  constexpr int OPT = D * CB / 256;    // outputs per thread: 8 or 4
+  constexpr int OPT = D * CB / 256;    // outputs per thread: 4 at D = 64
   constexpr int TPR = CB / OPT;        // threads per row
   constexpr int PL = D + 1;            // padded row of P in LDS
   constexpr int NV = D * D / 4 / 256;  // float4 loads of P per thread
@@ -1808,6 +1809,83 @@ __global__ __launch_bounds__(256) void seg_scan_kernel(ScanList sl, int Hv) {
     for (int o = 0; o < OPT; ++o) {
       Ss[k][col + o] = acc[o];
       c.S[(s + 1) * hs + off + o] = acc[o];
+    }
+  }
+}
+
+// The scan at D = 128 on the fp32 matrix cores: workgroup (chain, head, 16
+// state columns); wave w computes rows 32 w .. 32 w + 31 of
+// S_{s+1}[:, block] = P_s S_s[:, block] + R_s[:, block] as two 16 x 16 tiles
+// of v_mfma_f32_16x16x4_f32 over the 32 key steps (lane (c, g) holds A
+// element (row c, key 4 kk + g), B element (key 4 kk + g, column c), C rows
+// 4 g + i of column c).  P_s goes through LDS once per step (row pitch D + 4
+// floats: the 64 lanes of an A read hit distinct banks); S_s is re-staged in
+// LDS between steps; P_s and R_s are loaded one step ahead, as in the VALU
+// form above.  (Config 3's scan: 45 us in the VALU form at D = 128.)
+__global__ __launch_bounds__(256) void seg_scan_mfma_kernel(ScanList sl, int Hv) {
+  constexpr int D = 128;
+  constexpr int CB = 16;
+  constexpr int NB = D / CB;
+  constexpr int PL = D + 4;
+  constexpr int NV = D * D / 4 / 256;  // float4 loads of P per thread
+  __shared__ __align__(16) float Ps[D * PL];
+  __shared__ __align__(16) float Ss[D][CB];
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, static_cast<int64_t>(sl.n) * Hv * NB);
+  if (wi < 0) return;
+  const int blk = static_cast<int>(wi % NB);
+  const int h = static_cast<int>((wi / NB) % Hv);
+  const int ci = static_cast<int>(wi / (NB * Hv));
+  const ScanChain& c = sl.c[ci];
+  const int64_t hs = static_cast<int64_t>(Hv) * D * D;
+  const int64_t hp = static_cast<int64_t>(h) * D * D;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int lc = lane & 15, lg = lane >> 4;
+  for (int e = tid; e < D * CB; e += 256) Ss[e / CB][e % CB] = c.S[hp + static_cast<int64_t>(e / CB) * D + blk * CB + e % CB];
+  // the lane's C elements: rows r0 + 16 t + i, column lc
+  const int r0 = 32 * wave + 4 * lg;
+  const int64_t coff = hp + static_cast<int64_t>(r0) * D + blk * CB + lc;
+  // P_s as float4 per thread (row-major: float4 f = tid + 256 i is row f / 32,
+  // columns 4 (f % 32) ..) and the lane's 8 elements of R_s, one step ahead
+  const f32x4_t* pg = reinterpret_cast<const f32x4_t*>(c.P + hp) + tid;
+  const float* rg = c.R + coff;
+  f32x4_t pre[NV];
+  float rpre[8];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) pre[i] = pg[256 * i];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rpre[j] = rg[static_cast<int64_t>(16 * (j >> 2) + (j & 3)) * D];
+  gdn::keep_loads_here();
+  for (int s = 0; s < c.m; ++s) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = tid + 256 * i;
+      *reinterpret_cast<f32x4_t*>(&Ps[(f >> 5) * PL + 4 * (f & 31)]) = pre[i];
+    }
+    f32x4_t acc0 = {rpre[0], rpre[1], rpre[2], rpre[3]};
+    f32x4_t acc1 = {rpre[4], rpre[5], rpre[6], rpre[7]};
+    gdn::lds_barrier();  // P_s and S_s are in LDS
+    const int64_t nx = static_cast<int64_t>(min(s + 1, c.m - 1)) * hs;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) pre[i] = pg[nx / 4 + 256 * i];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rpre[j] = rg[nx + static_cast<int64_t>(16 * (j >> 2) + (j & 3)) * D];
+    gdn::keep_loads_here();
+    const float* pa = &Ps[(32 * wave + lc) * PL + lg];
+#pragma unroll 8
+    for (int kk = 0; kk < D / 4; ++kk) {
+      const float bv = Ss[4 * kk + lg][lc];
+      acc0 = gdn::mfma16x16x4f32(pa[4 * kk], bv, acc0);
+      acc1 = gdn::mfma16x16x4f32(pa[16 * PL + 4 * kk], bv, acc1);
+    }
+    gdn::lds_barrier();  // every row of S_s and P_s is read
+    float* so = c.S + (s + 1) * hs + coff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      Ss[r0 + i][lc] = acc0[i];
+      Ss[r0 + 16 + i][lc] = acc1[i];
+      so[static_cast<int64_t>(i) * D] = acc0[i];
+      so[static_cast<int64_t>(16 + i) * D] = acc1[i];
     }
   }
 }
@@ -1966,7 +2044,10 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   if (sc.n) {
     const int64_t swork = static_cast<int64_t>(sc.n) * Hv * (D / 16);
     const int64_t sgrid = gdn::kNumXcd * ((swork + gdn::kNumXcd - 1) / gdn::kNumXcd);
-    seg_scan_kernel<D><<<dim3(static_cast<unsigned>(sgrid)), dim3(256), 0, stream>>>(sc, Hv);
+    if constexpr (D == 128)
+      seg_scan_mfma_kernel<<<dim3(static_cast<unsigned>(sgrid)), dim3(256), 0, stream>>>(sc, Hv);
+    else
+      seg_scan_kernel<D><<<dim3(static_cast<unsigned>(sgrid)), dim3(256), 0, stream>>>(sc, Hv);
     st = gdn_launch_status();
     if (st != GDN_OK) return st;
   }
