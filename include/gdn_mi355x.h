@@ -204,12 +204,18 @@ int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Arguments
  * as gdn_conv_chunk_prefill with phase = 3 (prep and state pass together) and
  * no select_host; it calls no hipMalloc / hipFree.  A call whose workspace
- * (gdn_conv_chunk_prefill_workspace_size) exceeds the array returns
- * GDN_ERR_SCRATCH: 128 MiB holds ~2,200 chunk-heads of records at D = 128,
- * e.g. ~8,000 tokens at 16 value heads (less for calls of under 4 sequences,
- * which also reserve the segment scratch).  All calls on one GPU share the
+ * (gdn_conv_chunk_prefill_workspace_size) fits the array (128 MiB less 256
+ * bytes: ~2,200 chunk-heads of records at D = 128, e.g. ~8,000 tokens at 16
+ * value heads) runs as that entry point would, the same bits.  A larger one
+ * runs as pieces in order on the stream, without segments: groups of whole
+ * sequences whose records fit, and a sequence longer than the array holds as
+ * token ranges of whole chunks, each starting from the state and conv taps
+ * the range before it left in the pools (hT and conv_state) -- the same bits
+ * as gdn_conv_chunk_prefill with max_segments = 1.  Pieces need
+ * cu_seqlens_host, and token ranges need hT; without them a larger call
+ * returns GDN_ERR_SCRATCH before any launch.  All calls on one GPU share the
  * array: calls that overlap on one GPU race; calls in order on a stream are
- * safe.  Results are the same bits as gdn_conv_chunk_prefill's.
+ * safe.
  */
 int gdn_conv_chunk_prefill_noalloc(const uint16_t* x, int64_t sx_row, uint16_t* conv_state, int64_t ss_seq,
                                    int64_t ss_ch, const uint16_t* conv_w, const uint16_t* b, const uint16_t* a,

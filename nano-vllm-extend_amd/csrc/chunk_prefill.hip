@@ -73,7 +73,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kC = 64;   // chunk size (tokens)
 constexpr int kCB = 64;  // value columns per state workgroup
 
-__device__ __forceinline__ int64_t chunks_of(int64_t len) { return (len + kC - 1) / kC; }
+__host__ __device__ __forceinline__ int64_t chunks_of(int64_t len) { return (len + kC - 1) / kC; }
 
 // swap quads 1 and 2 of each 16-block (an involution)
 __device__ __forceinline__ int qswap(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
@@ -2105,6 +2105,50 @@ extern "C" int64_t gdn_conv_chunk_prefill_workspace_size(int64_t N, int n_seqs, 
   return gdn_chunk_prefill_workspace_size(N, n_seqs, Hv, D);
 }
 
+// Argument checks of gdn_conv_chunk_prefill that do not depend on the
+// workspace (shared with the allocation-free entry point).
+static int conv_chunk_check(const uint16_t* x, int64_t sx_row, const uint16_t* conv_state, int64_t ss_seq,
+                            int64_t ss_ch, const uint16_t* conv_w, const uint16_t* b, const uint16_t* a,
+                            const void* A_log, const void* dt_bias, const float* h0, const float* hT,
+                            int64_t state_stride, const int64_t* cu_seqlens, const int64_t* cu_seqlens_host,
+                            int max_segments, int phase, const uint8_t* select_host, int n_seqs, int Hk, int Hv,
+                            int D, const uint16_t* o) {
+  if (!x || !conv_state || !conv_w || !a || !b || !A_log || !dt_bias || !cu_seqlens || !o)
+    return GDN_ERR_INVALID_ARG;
+  if (max_segments < 0 || phase < 1 || phase > 3) return GDN_ERR_INVALID_ARG;
+  if (select_host && (!cu_seqlens_host || n_seqs > kMaxSegItems)) return GDN_ERR_INVALID_ARG;
+  const int64_t C = 2LL * Hk * D + static_cast<int64_t>(Hv) * D;
+  // 16-byte row segments of x, 8-byte output pieces
+  if (sx_row % 8 || sx_row < C || sx_row >= (1LL << 24) || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(conv_w) % 16 || reinterpret_cast<uintptr_t>(o) % 8 || ss_ch < 3 ||
+      ss_seq < C * ss_ch || ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
+    return GDN_ERR_INVALID_ARG;
+  return GDN_OK;
+}
+
+// The launches of one checked call: records at ws, segment scratch at seg_ws
+// (NULL: no segments).
+static int conv_chunk_run(const uint16_t* x, int64_t sx_row, uint16_t* conv_state, int64_t ss_seq, int64_t ss_ch,
+                          const uint16_t* conv_w, const uint16_t* b, const uint16_t* a, const void* A_log,
+                          const void* dt_bias, int param_is_fp32, const float* h0, float* hT,
+                          const int64_t* state_ids, const uint8_t* fresh, int64_t state_stride,
+                          const int64_t* cu_seqlens, const int64_t* cu_seqlens_host, int max_segments, int phase,
+                          const uint8_t* select_host, int n_seqs, int64_t N, int Hk, int Hv, int D, float scale,
+                          int l2norm, uint16_t* o, uint8_t* ws, uint8_t* seg_ws, hipStream_t s) {
+  const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
+  const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, fresh, conv_w, Hk * D, a, b, A_log, dt_bias,
+                  param_is_fp32 ? 1 : 0};
+  // the state kernel's U waves read the raw v channels and run their conv
+  const uint16_t* xv = x + 2LL * Hk * D;
+  if (D == 128)
+    return launch_chunk<128>(x, sx_row, x, sx_row, xv, sx_row, nullptr, nullptr, h0, hT, state_ids, state_stride,
+                             cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm,
+                             o, ws, seg_ws, &cv, phase, select_host, s);
+  return launch_chunk<64>(x, sx_row, x, sx_row, xv, sx_row, nullptr, nullptr, h0, hT, state_ids, state_stride,
+                          cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
+                          ws, seg_ws, &cv, phase, select_host, s);
+}
+
 extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_t* conv_state,
                                       int64_t ss_seq, int64_t ss_ch, const uint16_t* conv_w,
                                       const uint16_t* b, const uint16_t* a, const void* A_log,
@@ -2118,33 +2162,20 @@ extern "C" int gdn_conv_chunk_prefill(const uint16_t* x, int64_t sx_row, uint16_
   if (D != 64 && D != 128) return GDN_ERR_UNSUPPORTED;
   if (n_seqs < 0 || N < 0 || Hk <= 0 || Hv <= 0 || Hv % Hk) return GDN_ERR_INVALID_ARG;
   if (n_seqs == 0) return GDN_OK;
-  if (!x || !conv_state || !conv_w || !a || !b || !A_log || !dt_bias || !cu_seqlens || !o || !workspace)
-    return GDN_ERR_INVALID_ARG;
-  if (max_segments < 0 || phase < 1 || phase > 3) return GDN_ERR_INVALID_ARG;
-  if (select_host && (!cu_seqlens_host || n_seqs > kMaxSegItems)) return GDN_ERR_INVALID_ARG;
-  const int64_t C = 2LL * Hk * D + static_cast<int64_t>(Hv) * D;
-  // 16-byte row segments of x, 8-byte output pieces, 256-byte workspace records
-  if (sx_row % 8 || sx_row < C || sx_row >= (1LL << 24) || reinterpret_cast<uintptr_t>(x) % 16 ||
-      reinterpret_cast<uintptr_t>(conv_w) % 16 || reinterpret_cast<uintptr_t>(o) % 8 ||
-      reinterpret_cast<uintptr_t>(workspace) % 256 || ss_ch < 3 || ss_seq < C * ss_ch ||
-      ((h0 || hT) && state_stride < static_cast<int64_t>(Hv) * D * D))
-    return GDN_ERR_INVALID_ARG;
+  const int st = conv_chunk_check(x, sx_row, conv_state, ss_seq, ss_ch, conv_w, b, a, A_log, dt_bias, h0, hT,
+                                  state_stride, cu_seqlens, cu_seqlens_host, max_segments, phase, select_host,
+                                  n_seqs, Hk, Hv, D, o);
+  if (st != GDN_OK) return st;
+  // 256-byte workspace records
+  if (!workspace || reinterpret_cast<uintptr_t>(workspace) % 256) return GDN_ERR_INVALID_ARG;
   const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
   if (workspace_bytes < gdn_conv_chunk_prefill_workspace_size(N, n_seqs, Hv, D)) return GDN_ERR_INVALID_ARG;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  const ConvIn cv{x, sx_row, conv_state, ss_seq, ss_ch, state_ids, fresh, conv_w, Hk * D, a, b, A_log, dt_bias,
-                  param_is_fp32 ? 1 : 0};
-  // the state kernel's U waves read the raw v channels and run their conv
-  const uint16_t* xv = x + 2LL * Hk * D;
   uint8_t* seg_ws = seg_scratch_bytes(n_seqs, Hv, D) ? ws + nc_bound * Hv * rec_bytes(D) : nullptr;
-  if (D == 128)
-    return launch_chunk<128>(x, sx_row, x, sx_row, xv, sx_row, nullptr, nullptr, h0, hT, state_ids, state_stride,
-                             cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm,
-                             o, ws, seg_ws, &cv, phase, select_host, s);
-  return launch_chunk<64>(x, sx_row, x, sx_row, xv, sx_row, nullptr, nullptr, h0, hT, state_ids, state_stride,
-                          cu_seqlens, cu_seqlens_host, max_segments, n_seqs, nc_bound, Hk, Hv, scale, l2norm, o,
-                          ws, seg_ws, &cv, phase, select_host, s);
+  return conv_chunk_run(x, sx_row, conv_state, ss_seq, ss_ch, conv_w, b, a, A_log, dt_bias, param_is_fp32, h0, hT,
+                        state_ids, fresh, state_stride, cu_seqlens, cu_seqlens_host, max_segments, phase,
+                        select_host, n_seqs, N, Hk, Hv, D, scale, l2norm, o, ws, seg_ws,
+                        static_cast<hipStream_t>(stream));
 }
 
 // ---- the allocation-free variant of gdn_conv_chunk_prefill ----
@@ -2195,6 +2226,27 @@ int scratch_on(hipStream_t stream, uint8_t** out) {
 
 }  // namespace
 
+// The bytes at the array's end hold the two token offsets of a sequence
+// that runs in pieces (where the kernels read cu_seqlens).
+constexpr int64_t kNoAllocCuBytes = 256;
+
+namespace {
+__global__ void set_cu_pair_kernel(int64_t* dst, int64_t t0, int64_t t1) {
+  if (threadIdx.x == 0) {
+    dst[0] = t0;
+    dst[1] = t1;
+  }
+}
+}  // namespace
+
+// A call whose records do not fit the array runs as pieces in order on the
+// stream, without segments: groups of whole sequences whose records fit (the
+// kernels take the tokens' offsets from cu_seqlens, so a group only moves the
+// cu_seqlens, slot-id and fresh pointers), and a sequence longer than the
+// array holds as token ranges of whole chunks, each one starting from the
+// state (hT) and conv taps the range before it left in the pools -- what two
+// prefill calls over those ranges would do.  Planning needs the host offsets
+// (cu_seqlens_host); a sequence in ranges needs its final state stored (hT).
 extern "C" int gdn_conv_chunk_prefill_noalloc(const uint16_t* x, int64_t sx_row, uint16_t* conv_state,
                                               int64_t ss_seq, int64_t ss_ch, const uint16_t* conv_w,
                                               const uint16_t* b, const uint16_t* a, const void* A_log,
@@ -2208,13 +2260,68 @@ extern "C" int gdn_conv_chunk_prefill_noalloc(const uint16_t* x, int64_t sx_row,
   if (n_seqs == 0) return GDN_OK;
   const int64_t need = gdn_conv_chunk_prefill_workspace_size(N, n_seqs, Hv, D);
   if (need < 0) return GDN_ERR_INVALID_ARG;
-  if (need > kNoAllocScratchBytes) return GDN_ERR_SCRATCH;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  uint8_t* ws = nullptr;
-  const int st = scratch_on(s, &ws);
+  constexpr int64_t kCap = kNoAllocScratchBytes - kNoAllocCuBytes;
+  const int64_t rec = static_cast<int64_t>(Hv) * rec_bytes(D);  // one chunk's records
+  const int64_t cap_chunks = kCap / rec;
+  if (need > kCap && (!cu_seqlens_host || cap_chunks < 2)) return GDN_ERR_SCRATCH;
+  int st = conv_chunk_check(x, sx_row, conv_state, ss_seq, ss_ch, conv_w, b, a, A_log, dt_bias, h0, hT,
+                            state_stride, cu_seqlens, cu_seqlens_host, max_segments, kPhasePrep | kPhaseState,
+                            nullptr, n_seqs, Hk, Hv, D, o);
   if (st != GDN_OK) return st;
-  return gdn_conv_chunk_prefill(x, sx_row, conv_state, ss_seq, ss_ch, conv_w, b, a, A_log, dt_bias, param_is_fp32,
-                                h0, hT, state_ids, fresh, state_stride, cu_seqlens, cu_seqlens_host, max_segments,
-                                kPhasePrep | kPhaseState, nullptr, n_seqs, N, Hk, Hv, D, scale, l2norm, o, ws,
-                                kNoAllocScratchBytes, stream);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (need <= kCap) {
+    // one call, as the workspace entry point runs it
+    uint8_t* ws = nullptr;
+    if ((st = scratch_on(s, &ws)) != GDN_OK) return st;
+    const int64_t nc_bound = (N + kC - 1) / kC + n_seqs;
+    uint8_t* seg_ws = seg_scratch_bytes(n_seqs, Hv, D) ? ws + nc_bound * rec : nullptr;
+    return conv_chunk_run(x, sx_row, conv_state, ss_seq, ss_ch, conv_w, b, a, A_log, dt_bias, param_is_fp32, h0,
+                          hT, state_ids, fresh, state_stride, cu_seqlens, cu_seqlens_host, max_segments,
+                          kPhasePrep | kPhaseState, nullptr, n_seqs, N, Hk, Hv, D, scale, l2norm, o, ws, seg_ws, s);
+  }
+  // the plan, checked before anything launches
+  for (int r = 0; r < n_seqs; ++r) {
+    const int64_t len = cu_seqlens_host[r + 1] - cu_seqlens_host[r];
+    if (len < 0) return GDN_ERR_INVALID_ARG;
+    if (chunks_of(len) + 1 > cap_chunks && !hT) return GDN_ERR_SCRATCH;
+  }
+  uint8_t* ws = nullptr;
+  if ((st = scratch_on(s, &ws)) != GDN_OK) return st;
+  int64_t* cu_pair = reinterpret_cast<int64_t*>(ws + kCap);
+  auto piece = [&](const float* p_h0, const int64_t* p_ids, const uint8_t* p_fresh, const int64_t* p_cu,
+                   const int64_t* p_cu_host, int p_n, int64_t p_N) {
+    return conv_chunk_run(x, sx_row, conv_state, ss_seq, ss_ch, conv_w, b, a, A_log, dt_bias, param_is_fp32, p_h0,
+                          hT, p_ids, p_fresh, state_stride, p_cu, p_cu_host, 1, kPhasePrep | kPhaseState, nullptr,
+                          p_n, p_N, Hk, Hv, D, scale, l2norm, o, ws, nullptr, s);
+  };
+  for (int r = 0; r < n_seqs;) {
+    const int64_t* ids_r = state_ids ? state_ids + r : nullptr;
+    const uint8_t* fresh_r = fresh ? fresh + r : nullptr;
+    const int64_t t_beg = cu_seqlens_host[r], t_end = cu_seqlens_host[r + 1];
+    if (chunks_of(t_end - t_beg) + 1 > cap_chunks) {
+      // one sequence, token ranges of cap_chunks - 1 whole chunks
+      const int64_t step = (cap_chunks - 1) * kC;
+      for (int64_t t0 = t_beg; t0 < t_end; t0 += step) {
+        const int64_t t1 = std::min(t0 + step, t_end);
+        set_cu_pair_kernel<<<dim3(1), dim3(64), 0, s>>>(cu_pair, t0, t1);
+        if ((st = gdn_launch_status()) != GDN_OK) return st;
+        const int64_t cu_h[2] = {t0, t1};
+        const bool first = t0 == t_beg;
+        if ((st = piece(first ? h0 : hT, ids_r, first ? fresh_r : nullptr, cu_pair, cu_h, 1, t1 - t0)) != GDN_OK)
+          return st;
+      }
+      ++r;
+      continue;
+    }
+    // the longest run of whole sequences from r whose records fit
+    int r1 = r + 1;
+    while (r1 < n_seqs && chunks_of(cu_seqlens_host[r1 + 1] - t_beg) + (r1 + 1 - r) <= cap_chunks &&
+           chunks_of(cu_seqlens_host[r1 + 1] - cu_seqlens_host[r1]) + 1 <= cap_chunks)
+      ++r1;
+    if ((st = piece(h0, ids_r, fresh_r, cu_seqlens + r, cu_seqlens_host + r, r1 - r,
+                    cu_seqlens_host[r1] - t_beg)) != GDN_OK)
+      return st;
+    r = r1;
+  }
+  return GDN_OK;
 }

@@ -171,7 +171,13 @@ class GatedDeltaNetCore:
             self.norm_w = self.norm_w.to(dev)
 
     # ---------------------------------------------------------------- gates --
-    def _g_beta(self, b, a, mask):
+    def _g_beta(self, b, a, mask, gb=None):
+        """g (fp32), beta (bf16) of the rows b, a; gb: the same already
+        computed (the in_proj GEMM's gate epilogue, bit-equal to the gate
+        kernel), padded rows of g zero under mask."""
+        if gb is not None:
+            g, beta = gb
+            return (g if mask is None else g.masked_fill(~mask.unsqueeze(-1), 0.0)), beta
         if self.sw.gbeta:
             with self._timed("g_beta"):
                 return ops.fused_g_beta(b, a, self.A_log, self.dt_bias, mask)
@@ -186,7 +192,7 @@ class GatedDeltaNetCore:
             return ops.rms_norm_gated(core, z, self.norm_w, self.eps)
 
     # --------------------------------------------------------------- decode --
-    def decode(self, mixed, z, b, a, ids, conv_cache, s_cache):
+    def decode(self, mixed, z, b, a, ids, conv_cache, s_cache, gb=None):
         """One token per row (the T == 1 branch of _gdn_padded, qwen3_5.py:1008-1030).
         mixed [B, C], z [B, Hv*D], b/a [B, Hv]; pools are per-layer views.
         Returns core [B, Hv, D] bf16."""
@@ -211,7 +217,7 @@ class GatedDeltaNetCore:
                 out = ops.recurrent_decode_fused(qk, mixed, conv_cache, self.conv_w, b, a, self.A_log, self.dt_bias,
                                                  s_cache, ids, Hk, Hv, D, z=z, norm_weight=self.norm_w, eps=self.eps)
             return out.view(B, Hv, D)
-        g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
+        g, beta = self._g_beta(b.contiguous(), a.contiguous(), None, gb)
         if self.sw.conv_kernel:
             with self._timed("conv_decode"):
                 y = ops.conv_decode_step(mixed, conv_cache, ids, self.conv_w)
@@ -232,7 +238,7 @@ class GatedDeltaNetCore:
         return self._norm(out.view(B, Hv, D), z.view(B, Hv, D))
 
     # ------------------------------------------------------- varlen prefill --
-    def prefill_varlen(self, mixed, z, b, a, lens_q, ids, conv_cache, s_cache, fresh=None):
+    def prefill_varlen(self, mixed, z, b, a, lens_q, ids, conv_cache, s_cache, fresh=None, gb=None):
         """Varlen prefill group (_gdn_prefill_varlen, qwen3_5.py:922-965) with the
         conv and recurrent states read / written in the pools at `ids`.
         mixed [N, C], z [N, Hv*D], b/a [N, Hv].  fresh: optional bool [n],
@@ -258,7 +264,7 @@ class GatedDeltaNetCore:
             zero = ids[fresh.to(device=ids.device, dtype=torch.bool)]
             conv_cache[zero] = 0
             s_cache[zero] = 0
-        g, beta = self._g_beta(b.contiguous(), a.contiguous(), None)
+        g, beta = self._g_beta(b.contiguous(), a.contiguous(), None, gb)
         cu_gpu, lens_gpu, cu64_cpu, cu64_gpu = varlen_meta(lens_q, mixed.device)
         if self.sw.conv_kernel:
             with self._timed("conv_varlen"):
@@ -327,7 +333,7 @@ class GatedDeltaNetCore:
         return y[:, :kd].contiguous(), y[:, kd:2 * kd].contiguous(), y[:, 2 * kd:].contiguous()
 
     # ------------------------------------------------------- padded prefill --
-    def prefill_padded(self, x, z, b, a, lens, ids, conv_cache, s_cache):
+    def prefill_padded(self, x, z, b, a, lens, ids, conv_cache, s_cache, gb=None):
         """Padded prefill over [n, T, .] rows (T > 1 branch of _gdn_padded,
         qwen3_5.py:1032-1077): T-segments thread the conv and recurrent
         states; padding rows are exact no-ops (g = 0, masked conv output).
@@ -337,7 +343,7 @@ class GatedDeltaNetCore:
         n, T, C = x.shape
         Hk, Hv, D, K = self.Hk, self.Hv, self.D, self.K
         mask = torch.arange(T, device=x.device) < lens.unsqueeze(1)
-        g, beta = self._g_beta(b.contiguous(), a.contiguous(), mask)
+        g, beta = self._g_beta(b.contiguous(), a.contiguous(), mask, gb)
         seg = max(1, self.PREFILL_SEGMENT_TOKENS // n)
         conv_states = conv_cache[ids]
         state = s_cache[ids]
@@ -375,17 +381,20 @@ class GatedDeltaNetCore:
 
     # ------------------------------------------------------------- dispatch --
     def forward(self, mixed, z, b, a, cu_seqlens_q, max_seqlen_q, ids, conv_cache, s_cache,
-                lens_q: list[int] | None = None):
+                lens_q: list[int] | None = None, gb=None):
         """Dispatch of Qwen3_5GatedDeltaNet.forward (qwen3_5.py:864-920) over a
         varlen step: all-decode -> decode; a contiguous decode prefix goes to
         the decode path and the rest to the varlen (or padded) prefill.
-        mixed [N, C], z [N, Hv*D], b/a [N, Hv].  Returns [N, Hv*D] bf16."""
+        mixed [N, C], z [N, Hv*D], b/a [N, Hv]; gb: optional (g [N, Hv] fp32,
+        beta [N, Hv] bf16) already computed from b, a (used by the paths that
+        would run the gate kernel).  Returns [N, Hv*D] bf16."""
+        rows = (lambda i, j: None) if gb is None else (lambda i, j: (gb[0][i:j], gb[1][i:j]))
         N = mixed.shape[0]
         lens = cu_seqlens_q[1:] - cu_seqlens_q[:-1]
         bs = lens.shape[0]
         T = int(max_seqlen_q)
         if T == 1:
-            return self.decode(mixed, z, b, a, ids, conv_cache, s_cache).view(N, self.value_dim)
+            return self.decode(mixed, z, b, a, ids, conv_cache, s_cache, gb=gb).view(N, self.value_dim)
         if lens_q is None:
             lens_q = lens.tolist()
         n1 = 0
@@ -397,21 +406,22 @@ class GatedDeltaNetCore:
             off = 0
             if n1:
                 parts.append(self.decode(mixed[:n1], z[:n1], b[:n1], a[:n1], ids[:n1], conv_cache,
-                                         s_cache).view(n1, self.value_dim))
+                                         s_cache, gb=rows(0, n1)).view(n1, self.value_dim))
                 off = n1
             if self.sw.varlen:
                 parts.append(self.prefill_varlen(mixed[off:], z[off:], b[off:], a[off:], lens_q[off:],
-                                                 ids[off:], conv_cache, s_cache).view(-1, self.value_dim))
+                                                 ids[off:], conv_cache, s_cache,
+                                                 gb=rows(off, N)).view(-1, self.value_dim))
                 return torch.cat(parts, dim=0)
             lens_p = lens[off:]
             Tp = T if off == 0 else max(lens_q[off:])
             parts.append(self._padded_varlen(mixed[off:], z[off:], b[off:], a[off:], lens_p, Tp, ids[off:],
-                                             conv_cache, s_cache))
+                                             conv_cache, s_cache, gb=rows(off, N)))
             return torch.cat(parts, dim=0)
         # len-1 rows that are not a contiguous prefix: one padded pass
-        return self._padded_varlen(mixed, z, b, a, lens, T, ids, conv_cache, s_cache)
+        return self._padded_varlen(mixed, z, b, a, lens, T, ids, conv_cache, s_cache, gb=gb)
 
-    def _padded_varlen(self, mixed, z, b, a, lens, T, ids, conv_cache, s_cache):
+    def _padded_varlen(self, mixed, z, b, a, lens, T, ids, conv_cache, s_cache, gb=None):
         n = lens.shape[0]
         mask = torch.arange(T, device=mixed.device) < lens.unsqueeze(1)
 
@@ -420,7 +430,13 @@ class GatedDeltaNetCore:
             p[mask] = t
             return p
 
-        core = self.prefill_padded(pad(mixed), pad(z), pad(b), pad(a), lens, ids, conv_cache, s_cache)
+        gbp = None
+        if gb is not None:
+            # the gate kernel on padded rows: g = 0 there (mask), beta = sigmoid(0) = 0.5
+            beta_p = gb[1].new_full((n, T, gb[1].shape[-1]), 0.5)
+            beta_p[mask] = gb[1]
+            gbp = (pad(gb[0]), beta_p)
+        core = self.prefill_padded(pad(mixed), pad(z), pad(b), pad(a), lens, ids, conv_cache, s_cache, gb=gbp)
         return core.reshape(n, T, self.value_dim)[mask]
 
 
@@ -435,7 +451,9 @@ class GatedDeltaNetLayer:
     (in_proj_qkv [C, hidden], in_proj_z [Hv*D, hidden], in_proj_b [Hv, hidden],
     in_proj_a [Hv, hidden], :811-822), whose output rows hold mixed, z, b and a
     side by side; the core reads them as strided views (the fused prefill and
-    decode kernels take the raw b and a and compute g / beta themselves).
+    decode kernels take the raw b and a and compute g / beta themselves; when a
+    path would run the gate kernel instead, the GEMM's epilogue computes g and
+    beta from the b and a columns and that path uses them).
     out_proj [hidden, Hv*D] (:838-839) runs on the gated norm's output.  Both
     GEMMs are ops.linear (bf16 matrix cores, fp32 accumulation)."""
 
@@ -469,21 +487,36 @@ class GatedDeltaNetLayer:
 
         return cm()
 
-    def project_in(self, hidden):
+    def gates_in_gemm(self) -> bool:
+        """Whether a path of the core would run the gate kernel on in_proj's b
+        and a columns (the fused prefill and decode compute the gates from the
+        raw columns themselves); then in_proj's epilogue yields them instead."""
+        sw, c = self.core.sw, self.core
+        fused_ok = sw.gbeta and sw.conv_kernel and c.K == 4
+        return sw.gbeta and not (fused_ok and sw.fused_prefill and sw.varlen and sw.fused_decode and sw.inplace)
+
+    def project_in(self, hidden, gates: bool = False):
         """hidden [N, hidden] -> (mixed, z, b, a) as column views of one
-        [N, C + Hv*D + 2 Hv] bf16 buffer."""
+        [N, C + Hv*D + 2 Hv] bf16 buffer; with gates, also (g, beta) of the b
+        and a columns from the GEMM's epilogue (bit-equal to the gate kernel
+        on them, qwen3_5.py:933-934), else None."""
         c = self.core
-        with self._timed("in_proj"):
-            y = ops.linear(hidden, self.w_in)
         C, V, Hv = c.conv_dim, c.value_dim, c.Hv
-        return y[:, :C], y[:, C:C + V], y[:, C + V:C + V + Hv], y[:, C + V + Hv:]
+        with self._timed("in_proj"):
+            if gates:
+                y, g, beta = ops.linear(hidden, self.w_in, gates={"gate_col": C + V, "A_log": c.A_log,
+                                                                  "dt_bias": c.dt_bias})
+                gb = (g, beta)
+            else:
+                y, gb = ops.linear(hidden, self.w_in), None
+        return y[:, :C], y[:, C:C + V], y[:, C + V:C + V + Hv], y[:, C + V + Hv:], gb
 
     def forward(self, hidden, cu_seqlens_q, max_seqlen_q, ids, conv_cache, s_cache, lens_q=None):
         """Qwen3_5GatedDeltaNet.forward for one varlen step (qwen3_5.py:864-920):
         hidden [N, hidden] bf16 -> [N, hidden] bf16."""
-        mixed, z, b, a = self.project_in(hidden)
+        mixed, z, b, a, gb = self.project_in(hidden, gates=self.gates_in_gemm())
         self.core.timer = self.timer
         core = self.core.forward(mixed, z, b.contiguous(), a.contiguous(), cu_seqlens_q, max_seqlen_q, ids,
-                                 conv_cache, s_cache, lens_q=lens_q)
+                                 conv_cache, s_cache, lens_q=lens_q, gb=gb)
         with self._timed("out_proj"):
             return ops.linear(core, self.w_out)

@@ -442,8 +442,10 @@ def conv_chunk_prefill_varlen_noalloc(mixed: torch.Tensor, conv_state: torch.Ten
     allocation), and the output goes to the caller's `out` [N, Hv, D] bf16.
     Nothing here allocates device memory or copies: the inputs must already
     have the layouts the kernels read (checked).  Calls that overlap on one
-    GPU race on the shared array.  Raises GDNKernelError when the call needs
-    more than the array holds."""
+    GPU race on the shared array.  A call whose records do not fit the array
+    runs in pieces (sequence groups, and long sequences as token ranges), the
+    same bits as max_segments=1; that needs cu_seqlens_cpu, without which such
+    a call raises GDNKernelError."""
     dev = _check_cuda(mixed, conv_state, conv_weight, b, a, a_log, dt_bias, cu_seqlens, state, state_ids, out, fresh)
     Hk, Hv, D = num_k_heads, num_v_heads, head_dim
     N, C = mixed.shape

@@ -55,7 +55,7 @@ def test_layer_with_projections(pkg, dev):
     out = layer.forward(x.to(dev), cu.to(dev), max(lens), ids.to(dev), cp, sp, lens_q=lens)
     torch.cuda.synchronize()
     # (1) in_proj against fp32 matmuls (the GEMM's own bar: one bf16 step plus summation-order slack)
-    y_in = layer.project_in(x.to(dev))
+    y_in = layer.project_in(x.to(dev))[:4]
     w_all = torch.cat([w_qkv, w_z, w_b, w_a])
     ref_in = x.float() @ w_all.float().t()
     got_in = torch.cat([t.cpu() for t in y_in], 1).float()
@@ -84,8 +84,43 @@ def test_layer_with_projections(pkg, dev):
     xd = torch.randn(n, hidden, generator=gen).to(BF16)
     cu1 = torch.arange(n + 1, dtype=torch.int32)
     out_d = layer.forward(xd.to(dev), cu1.to(dev), 1, ids.to(dev), cp, sp)
-    md, zd, bd, ad = (t.cpu() for t in layer.project_in(xd.to(dev)))
+    md, zd, bd, ad = (t.cpu() for t in layer.project_in(xd.to(dev))[:4])
     core_d, _, s_d = gdn_ref.gdn_core_decode(md, zd, bd, ad, ids.tolist(), conv_r, s_now.clone(), conv_w, A_log,
                                              dt_bias, norm_w, Hk, Hv, D)
     assert_out(out_d.cpu(), _matmul_bf16(core_d.reshape(n, Hv * D), w_out), "decode step output")
     assert_state(sp.cpu()[ids], s_d[ids], "decode step states")
+
+
+@pytest.mark.parametrize("sw", [{"fused_prefill": False, "fused_decode": False}, {"varlen": False, "fused_decode": False}],
+                         ids=["unfused", "padded"])
+def test_layer_gates_from_in_proj_epilogue(pkg, dev, sw):
+    """With the fused prefill / decode switched off, the layer's paths run on
+    g and beta from in_proj's GEMM epilogue instead of the gate kernel: the
+    same results bit for bit as the core computing them itself from the b and
+    a columns (qwen3_5.py:933-934, :978-979)."""
+    gen = torch.Generator().manual_seed(82)
+    Hk, Hv, D, hidden = 2, 4, 128, 512
+    C, w_qkv, w_z, w_b, w_a, w_out, conv_w, A_log, dt_bias, norm_w = _weights(gen, hidden, Hk, Hv, D)
+    switches = pkg.Switches(**sw)
+    layer = pkg.GatedDeltaNetLayer(*(t.to(dev) for t in (w_qkv, w_z, w_b, w_a, w_out)), Hk, Hv, D,
+                                   conv_w.to(dev), A_log.to(dev), dt_bias.to(dev), norm_w.to(dev), switches=switches)
+    assert layer.gates_in_gemm()
+    lens = [1, 1, 90, 3, 130]
+    N = sum(lens)
+    ids = torch.tensor([4, 1, 6, 0, 3], device=dev)
+    conv0 = torch.randn(8, C, 3, generator=gen).to(BF16).to(dev)
+    s0 = (torch.randn(8, Hv, D, D, generator=gen) * 0.1).to(dev)
+    x = torch.randn(N, hidden, generator=gen).to(BF16).to(dev)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    cp1, sp1 = conv0.clone(), s0.clone()
+    out1 = layer.forward(x, cu, max(lens), ids, cp1, sp1, lens_q=lens)
+    # the same step with the core's own gate kernel
+    mixed, z, b, a, gb = layer.project_in(x)
+    assert gb is None
+    cp2, sp2 = conv0.clone(), s0.clone()
+    core = layer.core.forward(mixed, z, b.contiguous(), a.contiguous(), cu, max(lens), ids, cp2, sp2, lens_q=lens)
+    out2 = pkg.ops.linear(core, layer.w_out)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), "outputs differ"
+    assert torch.equal(sp1, sp2), "state pools differ"
+    assert torch.equal(cp1.view(torch.int16), cp2.view(torch.int16)), "conv pools differ"

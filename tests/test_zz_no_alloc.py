@@ -1,7 +1,9 @@
 """The allocation-free prefill entry point (gdn_conv_chunk_prefill_noalloc)
 against the workspace entry point (gdn_conv_chunk_prefill), bit for bit, on
 two calls in a row (the second smaller, so it runs on what the first left in
-the shared scratch array), both through the C ABI; and the size limit."""
+the shared scratch array), both through the C ABI: calls that fit the array,
+calls that run as sequence groups, and a sequence that
+runs as token ranges; and a larger call without host offsets, refused."""
 import pytest
 import torch
 
@@ -56,8 +58,29 @@ def test_noalloc_segmented_and_gva(pkg, dev):
     _both(pkg, dev, [300, 77], 2, 4, 64, 10)
 
 
+def test_noalloc_pieces_config1_then_smaller(pkg, dev):
+    print("no-alloc prefill: config 1 (241 MB of records: sequence groups), then a call that fits", flush=True)
+    lens = bench.make_prefill(1, None)["lens"]
+    lib = pkg._lib.load()
+    assert lib.gdn_conv_chunk_prefill_workspace_size(sum(lens), len(lens), 16, 128) > pkg._lib.NOALLOC_SCRATCH_BYTES
+    _both(pkg, dev, lens, 16, 16, 128, 11, segments=1)
+    _both(pkg, dev, [900, 64, 1], 16, 16, 128, 12, segments=1)
+
+
+def test_noalloc_pieces_long_sequence_in_ranges(pkg, dev):
+    print("no-alloc prefill: a 12,000-token sequence beside a short one (token ranges), then GVA, then D = 64",
+          flush=True)
+    lib = pkg._lib.load()
+    for lens, Hk, Hv, D, seed in (([300, 12000], 16, 16, 128, 13), ([20000, 70], 4, 8, 128, 14),
+                                  ([7000], 16, 32, 64, 15)):
+        assert lib.gdn_conv_chunk_prefill_workspace_size(sum(lens), len(lens), Hv, D) > \
+            pkg._lib.NOALLOC_SCRATCH_BYTES
+        _both(pkg, dev, lens, Hk, Hv, D, seed, segments=1)
+
+
 def test_noalloc_rejects_calls_beyond_the_array(pkg, dev):
-    """A call whose records would exceed the array fails before any launch."""
+    """A call whose records would exceed the array, without host offsets to
+    plan pieces from, fails before any launch."""
     Hk = Hv = 16
     D = 128
     lib = pkg._lib.load()
