@@ -447,6 +447,37 @@ def decode_bench(pkg, cfg, dev, K, W):
     return t / K, t_graph / K, timer.avg_us(), rec_us, pass_us, copy_us, t_hot / K, t_graph_hot / K
 
 
+def decode_gva_bench(pkg, dev, K, W):
+    """Config 2's decode step at Qwen3.5's grouped geometry (16 key heads, 32
+    value heads; pool [512, 32, 128, 128]), B = 256.  Two heads share each key
+    head, so the step is two launches: the q/k decode conv, then the fused
+    kernel (gates, v conv with its roll, state update, gated norm).  Returns
+    (s per step cold, fused kernel us, tile pass us).  (The q/k conv is not
+    burst-timed on its own: at 16 MB a launch it is shorter than a call's
+    host overhead, so back-to-back calls would time the host.)"""
+    cfg = make_decode(Hk=16, Hv=32)
+    core = pkg.GatedDeltaNetCore(cfg["Hk"], cfg["Hv"], cfg["D"], cfg["conv_w"].to(dev), cfg["A_log"].to(dev),
+                                 cfg["dt_bias"].to(dev), cfg["norm_w"].to(dev))
+    x, z, a, b = (cfg[k].to(dev) for k in ("x", "z", "a", "b"))
+    s_pool = cfg["s_pool"].to(dev)
+    conv_pool = cfg["conv_pool"].to(dev)
+    ids = cfg["ids"].to(dev)
+    del cfg["s_pool"]
+    used = set(ids.tolist())
+    other = torch.tensor([i for i in range(s_pool.shape[0]) if i not in used][:ids.numel()], device=dev)
+    sets = [ids, other]
+    turn = [0]
+
+    def step():
+        core.decode(x, z, b, a, sets[turn[0] % 2], conv_pool, s_pool)
+        turn[0] += 1
+
+    settle(step, W)
+    t = timed_steps(step, K)
+    rec_us, pass_us, _ = recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z)
+    return t / K, rec_us, pass_us
+
+
 def recurrent_burst_us(pkg, cfg, core, x, a, b, ids, conv_pool, s_pool, z_rows, R=20):
     """Average duration of the in-place recurrent kernel over R back-to-back
     launches between one event pair (an event pair around each launch adds a
@@ -834,6 +865,20 @@ def main():
                              "what": "gdn_state_tile_copy: the same pass with each tile written to a second pool "
                                      "at the same offsets (out of place), timed the same way"}}}
         del c2
+        tg, rec_g, pass_g = decode_gva_bench(pkg, dev, K, W)
+        sb_g = 2 * 256 * 32 * 128 * 128 * 4
+        extra["decode_gva_16_32_b256"] = {
+            "ms_per_step": round(tg * 1e3, 4),
+            "what": "config 2's step at Hk = 16, Hv = 32 (Qwen3.5's grouped geometry), B = 256, pool "
+                    "[512, 32, 128, 128], slot sets alternating as in decode_config2: two launches (the q/k decode "
+                    "conv, then the fused kernel)",
+            "kernels_us": {"recurrent_decode_fused": round(rec_g, 2)},
+            "roofline": {"bound": "hbm", "achieved": round(sb_g / (rec_g * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(sb_g / (rec_g * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                         "kernel_us": round(rec_g, 2), "algorithmic_bytes_per_launch": sb_g,
+                         "step_frac": round(sb_g / tg / 1e9 / HBM_PEAK_GBPS, 4),
+                         "inplace_tile_ceiling_us": round(pass_g, 2),
+                         "timing": "as decode_config2's roofline"}}
     if 3 in configs:
         c3 = make_prefill(4, [65536], h0_std=0.1, conv_std=1.0)
         K3 = max(2, K // 4)
