@@ -16,7 +16,8 @@
 // Tiling: a workgroup of 4 waves (one per SIMD, one workgroup per CU)
 // computes a BM x 256 tile of C (BM = 256, or 192 where that fills the last
 // wave of tiles better; 64 x 128 or 64 x 64, several workgroups per CU, for
-// small M), K in steps of 64.  Wave (wm, wn) owns rows BM / 2 wm
+// small M, with three or four LDS stages when K is long: gemm_tn_deep_kernel
+// below), K in steps of 64.  Wave (wm, wn) owns rows BM / 2 wm
 // .. and columns 128 wn ..: BM / 64 x 4 accumulator tiles of 32 x 32 (256
 // registers at BM = 256, kept in AGPRs), 64 products per step.
 //
@@ -100,6 +101,87 @@ __device__ __forceinline__ f32x16_t zero16() {
 #pragma unroll
   for (int i = 0; i < 16; ++i) z[i] = 0.f;
   return z;
+}
+
+// Epilogue of a BM x BN tile, straight from the accumulators of wave
+// (wm, wn).  `scratch`: (BM / 2) x 32 bf16 per wave of LDS that nothing reads
+// any more (the gate outputs go through it).
+template <int BM, int BN>
+__device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[BM / 64][BN / 64], uint16_t* __restrict__ C,
+                                           int64_t ldc, int M, int N, int m0, int n0, int wave, int lane,
+                                           const GemmGates& gt, uint8_t* scratch) {
+  constexpr int MI = BM / 64, NJ = BN / 64;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 31, lg = lane >> 5;
+  // acc[i][j] register 4 q + r of lane (li, lg) is C[row][col + r] with row =
+  // m0 + BM / 2 wm + 32 i + li, col = n0 + BN / 2 wn + 32 j + 8 q + 4 lg.  One
+  // swap between lanes l and l + 32 (v_permlane32_swap: the upper half of the
+  // first operand with the lower half of the second) leaves lane (li, lg)
+  // columns 16 p + 8 lg .. + 7 of pair p = (q 2p, q 2p + 1) in bf16: one
+  // 16-byte store per pair, two lanes filling 32 bytes of a row.
+  const bool vec = ldc % 8 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0;
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int m = m0 + (BM / 2) * wm + 32 * i + li;
+    const bool row_ok = m < M;  // (no early exit: the gate loop below spans every lane)
+    uint16_t* crow = C + static_cast<int64_t>(row_ok ? m : 0) * ldc;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int cb = n0 + (BN / 2) * wn + 32 * j;  // wave-uniform
+      if (cb >= N) continue;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int q = 2 * p;
+        const auto lo = __builtin_amdgcn_permlane32_swap(gdn::f2bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                                         gdn::f2bf2(acc[i][j][4 * q + 4], acc[i][j][4 * q + 5]),
+                                                         false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(gdn::f2bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]),
+                                                         gdn::f2bf2(acc[i][j][4 * q + 6], acc[i][j][4 * q + 7]),
+                                                         false, false);
+        const uint32_t w[4] = {lo[0], hi[0], lo[1], hi[1]};  // columns n .. n + 7
+        const int n = cb + 16 * p + 8 * lg;
+        if (!row_ok) {
+        } else if (vec && n + 8 <= N) {
+          *reinterpret_cast<uint4*>(crow + n) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            if (n + t < N) crow[n + t] = static_cast<uint16_t>(w[t / 2] >> (16 * (t % 2)));
+        }
+      }
+      // Gate outputs from the bf16-rounded b and a columns of this 32-column
+      // block.  The block's values go through the wave's own 8 KiB of the
+      // stage the last step no longer reads (wave-local, in order), and a
+      // rolled loop computes beta and g (unrolled over the registers, the gate
+      // arithmetic would not fit beside the accumulators).
+      if (gt.g && cb + 32 > gt.gate_col && cb < gt.gate_col + 2 * gt.Hv) {
+        uint16_t* gs = reinterpret_cast<uint16_t*>(scratch) + wave * (BM / 2) * 32;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = gdn::f2bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+          const uint32_t hi = gdn::f2bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          *reinterpret_cast<uint2*>(gs + 32 * (32 * i + li) + 8 * q + 4 * lg) = make_uint2(lo, hi);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll 1
+        for (int e = lane; e < 32 * 32; e += 64) {
+          const int r = e >> 5, c = e & 31;
+          const int mm = m - li + r, n = cb + c, col = n - gt.gate_col;
+          if (mm >= M || n >= N || col < 0 || col >= 2 * gt.Hv) continue;
+          const float v = gdn::bf2f(gs[32 * (32 * i + r) + c]);
+          if (col < gt.Hv) {
+            gt.beta[static_cast<int64_t>(mm) * gt.Hv + col] = gdn::gate_beta(v);
+          } else {
+            const int h = col - gt.Hv;
+            gt.g[static_cast<int64_t>(mm) * gt.Hv + h] =
+                gdn::gate_g(v, gdn::load_param(gt.A_log, h, gt.param_f32), gdn::load_param(gt.dt_bias, h, gt.param_f32));
+          }
+        }
+      }
+    }
+  }
 }
 
 // grid = 8 * ceil(tiles / 8); block = 256 (4 waves, 2 x 2 over the tile).
@@ -253,76 +335,142 @@ __global__ __launch_bounds__(kGemmThreads, kMinWG) void gemm_tn_kernel(const uin
     step(st1, st0, s + 1);
   }
   if (s < nk) step(st0, st1, s);  // the last step when nk is odd
-  // ---- epilogue: straight from the accumulators ----
-  // acc[i][j] register 4 q + r of lane (li, lg) is C[row][col + r] with row =
-  // m0 + BM / 2 wm + 32 i + li, col = n0 + BN / 2 wn + 32 j + 8 q + 4 lg.  One
-  // swap between lanes l and l + 32 (v_permlane32_swap: the upper half of the
-  // first operand with the lower half of the second) leaves lane (li, lg)
-  // columns 16 p + 8 lg .. + 7 of pair p = (q 2p, q 2p + 1) in bf16: one
-  // 16-byte store per pair, two lanes filling 32 bytes of a row.
-  const bool vec = ldc % 8 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0;
+  gemm_store<BM, BN>(acc, C, ldc, M, N, m0, n0, wave, lane, gt, nk % 2 ? st0 : st1);
+}
+
+// ---- small M (decode batches): a deeper load pipeline ----
+// gemm_tn_kernel's two stages let a step's loads arrive during one step's
+// products, which at 64-row tiles are four to eight products: every step then
+// waits out the memory latency (its barrier drains every load).  Here the
+// tile is 64 x BN and there are NS stages (3 or 4, separate LDS objects): the
+// loads of step s + NS - 1 go out at the start of step s, and the barrier
+// before step s waits only for the wave's loads of step s (vmcnt down to the
+// NS - 2 later steps' loads) and for its own LDS reads (so every wave is done
+// with the stage the next loads go into).  Same LDS layout, fragment reads,
+// products in the same order and epilogue as gemm_tn_kernel: the results are
+// the same bits.  Steps past the last one repeat its loads into the unused
+// stages (every path issues the same loads), drained before the epilogue.
+template <int BN, int NS>
+__global__ __launch_bounds__(kGemmThreads, 2) void gemm_tn_deep_kernel(const uint16_t* __restrict__ A, int64_t lda,
+                                                                    const uint16_t* __restrict__ B, int64_t ldb,
+                                                                    uint16_t* __restrict__ C, int64_t ldc, int M,
+                                                                    int N, int K, GemmGates gt) {
+  static_assert(NS == 3 || NS == 4, "three or four stages");
+  constexpr int BM = 64, MI = 1, NJ = BN / 64;
+  constexpr int kStage = (BM + BN) * 128;
+  constexpr int kPer = (BM + BN) / 32;  // 1 KiB blocks per wave per stage
+  constexpr int kAPer = BM / 32;
+  // s_waitcnt: vmcnt = the NS - 2 later steps' loads (bits 3:0 and 15:14),
+  // expcnt 7 (no wait), lgkmcnt 0
+  constexpr int kVm = (NS - 2) * kPer;
+  static_assert(kVm < 64, "vmcnt field");
+  constexpr int kWait = (kVm & 15) | (7 << 4) | ((kVm >> 4) << 14);
+  __shared__ __align__(16) uint8_t st0[kStage];
+  __shared__ __align__(16) uint8_t st1[kStage];
+  __shared__ __align__(16) uint8_t st2[kStage];
+  __shared__ __align__(16) uint8_t st3[NS == 4 ? kStage : 16];
+
+  const int mb_n = (M + BM - 1) / BM, nb_n = (N + BN - 1) / BN;
+  const int64_t tiles = static_cast<int64_t>(mb_n) * nb_n;
+  const int64_t L = gdn::xcd_remap(blockIdx.x, tiles);
+  if (L < 0) return;
+  const int64_t per_group = static_cast<int64_t>(kGroupM) * nb_n;
+  const int64_t grp = L / per_group, in_grp = L % per_group;
+  const int gm = static_cast<int>(min<int64_t>(kGroupM, mb_n - grp * kGroupM));
+  const int mb = static_cast<int>(grp * kGroupM + in_grp % gm);
+  const int nb = static_cast<int>(in_grp / gm);
+  const int m0 = mb * BM, n0 = nb * BN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 31, lg = lane >> 5;
+
+  const __amdgpu_buffer_rsrc_t ra = rsrc_of(A), rb = rsrc_of(B);
+  int goff[kPer];
 #pragma unroll
-  for (int i = 0; i < MI; ++i) {
-    const int m = m0 + (BM / 2) * wm + 32 * i + li;
-    const bool row_ok = m < M;  // (no early exit: the gate loop below spans every lane)
-    uint16_t* crow = C + static_cast<int64_t>(row_ok ? m : 0) * ldc;
+  for (int i = 0; i < kPer; ++i) {
+    const int b = wave + 4 * i;
+    const int gcol = 8 * ((lane & 7) ^ (((b & 1) << 2) | (lane >> 4)));
+    if (i < kAPer) {
+      goff[i] = static_cast<int>((min(m0 + 8 * b + (lane >> 3), M - 1) * lda + gcol) * 2);
+    } else {
+      goff[i] = static_cast<int>((min(n0 + 8 * (b - BM / 8) + (lane >> 3), N - 1) * ldb + gcol) * 2);
+    }
+  }
+  const int nk = K / kBK;
+  auto issue = [&](uint8_t* st, int step) {
+    const int kbyte = min(step, nk - 1) * kBK * 2;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int cb = n0 + (BN / 2) * wn + 32 * j;  // wave-uniform
-      if (cb >= N) continue;
+    for (int i = 0; i < kPer; ++i) dma16(i < kAPer ? ra : rb, st + (wave + 4 * i) * 1024, goff[i], kbyte);
+  };
+
+  f32x16_t acc[MI][NJ];
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const int q = 2 * p;
-        const auto lo = __builtin_amdgcn_permlane32_swap(gdn::f2bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                                                         gdn::f2bf2(acc[i][j][4 * q + 4], acc[i][j][4 * q + 5]),
-                                                         false, false);
-        const auto hi = __builtin_amdgcn_permlane32_swap(gdn::f2bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]),
-                                                         gdn::f2bf2(acc[i][j][4 * q + 6], acc[i][j][4 * q + 7]),
-                                                         false, false);
-        const uint32_t w[4] = {lo[0], hi[0], lo[1], hi[1]};  // columns n .. n + 7
-        const int n = cb + 16 * p + 8 * lg;
-        if (!row_ok) {
-        } else if (vec && n + 8 <= N) {
-          *reinterpret_cast<uint4*>(crow + n) = make_uint4(w[0], w[1], w[2], w[3]);
-        } else {
+  for (int j = 0; j < NJ; ++j) acc[0][j] = zero16();
+
+  // one step from stage `cur`: the four sub-steps' fragments, then their products
+  auto run = [&](const uint8_t* cur) {
+    gdn::s16x8_t fa[4], fb[4][NJ];
 #pragma unroll
-          for (int t = 0; t < 8; ++t)
-            if (n + t < N) crow[n + t] = static_cast<uint16_t>(w[t / 2] >> (16 * (t % 2)));
-        }
-      }
-      // Gate outputs from the bf16-rounded b and a columns of this 32-column
-      // block.  The block's values go through the wave's own 8 KiB of the
-      // stage the last step no longer reads (wave-local, in order), and a
-      // rolled loop computes beta and g (unrolled over the registers, the gate
-      // arithmetic would not fit beside the accumulators).
-      if (gt.g && cb + 32 > gt.gate_col && cb < gt.gate_col + 2 * gt.Hv) {
-        uint16_t* gs = reinterpret_cast<uint16_t*>(nk % 2 ? st0 : st1) + wave * (BM / 2) * 32;
+    for (int ks = 0; ks < 4; ++ks) {
+      fa[ks] = *reinterpret_cast<const gdn::s16x8_t*>(cur + sw_off(32 * wm + li, 2 * ks + lg));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t lo = gdn::f2bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
-          const uint32_t hi = gdn::f2bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-          *reinterpret_cast<uint2*>(gs + 32 * (32 * i + li) + 8 * q + 4 * lg) = make_uint2(lo, hi);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-#pragma unroll 1
-        for (int e = lane; e < 32 * 32; e += 64) {
-          const int r = e >> 5, c = e & 31;
-          const int mm = m - li + r, n = cb + c, col = n - gt.gate_col;
-          if (mm >= M || n >= N || col < 0 || col >= 2 * gt.Hv) continue;
-          const float v = gdn::bf2f(gs[32 * (32 * i + r) + c]);
-          if (col < gt.Hv) {
-            gt.beta[static_cast<int64_t>(mm) * gt.Hv + col] = gdn::gate_beta(v);
-          } else {
-            const int h = col - gt.Hv;
-            gt.g[static_cast<int64_t>(mm) * gt.Hv + h] =
-                gdn::gate_g(v, gdn::load_param(gt.A_log, h, gt.param_f32), gdn::load_param(gt.dt_bias, h, gt.param_f32));
-          }
-        }
+      for (int j = 0; j < NJ; ++j)
+        fb[ks][j] = *reinterpret_cast<const gdn::s16x8_t*>(cur + BM * 128 +
+                                                           sw_off((BN / 2) * wn + 32 * j + li, 2 * ks + lg));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[0][j] = mfma_bf16(fb[ks][j], fa[ks], acc[0][j]);
+  };
+  // step s from `cur`, the loads of step s + NS - 1 into `nxt` (the stage of
+  // step s - 1, which every wave has finished reading at the barrier)
+  auto one = [&](const uint8_t* cur, uint8_t* nxt, int step) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(kWait);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(nxt, step + NS - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    run(cur);
+  };
+  issue(st0, 0);
+  issue(st1, 1);
+  if constexpr (NS == 4) issue(st2, 2);
+  // Two rounds of the stages per trip.  The compiler's load counting merges
+  // its state at the loop head and then waits there for all but the newest
+  // step's loads before the first reads (vmcnt(kPer)); within a trip the
+  // barrier's own wait covers every read.
+  for (int s = 0; s < nk; s += 2 * NS) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int s0 = s + r * NS;
+      if constexpr (NS == 4) {
+        if (s0 >= nk) break;
+        one(st0, st3, s0);
+        if (s0 + 1 >= nk) break;
+        one(st1, st0, s0 + 1);
+        if (s0 + 2 >= nk) break;
+        one(st2, st1, s0 + 2);
+        if (s0 + 3 >= nk) break;
+        one(st3, st2, s0 + 3);
+      } else {
+        if (s0 >= nk) break;
+        one(st0, st2, s0);
+        if (s0 + 1 >= nk) break;
+        one(st1, st0, s0 + 1);
+        if (s0 + 2 >= nk) break;
+        one(st2, st1, s0 + 2);
       }
     }
   }
+  // the repeated loads land before a stage is reused as the gates' scratch
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  gemm_store<BM, BN>(acc, C, ldc, M, N, m0, n0, wave, lane, gt, st0);
 }
 
 }  // namespace
@@ -358,8 +506,18 @@ extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, 
   const int64_t grid = gdn::kNumXcd * ((tiles + gdn::kNumXcd - 1) / gdn::kNumXcd);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 g3(static_cast<unsigned>(grid)), b3(kGemmThreads);
-  if (cfg == 3)
+  // The 64-row tiles take the deeper load pipeline when K has at least 16
+  // steps (graph-replayed launches, 256 x 8224 x 2048: 21.1 -> 19.0 us; 256
+  // x 2048 x 2048: 10.1 -> 9.3 us; 64 x 8224 x 2048: 17.2 -> 10.0 us); with
+  // fewer its prologue and the repeated last loads cost more than it saves
+  // (1000 x 2080 x 512: 6.5 -> 7.0 us).
+  const bool deep = K / kBK >= 16;
+  if (cfg == 3 && deep)
+    gemm_tn_deep_kernel<64, 4><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+  else if (cfg == 3)
     gemm_tn_kernel<64, 64, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+  else if (cfg == 2 && deep)
+    gemm_tn_deep_kernel<128, 3><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
   else if (cfg == 2)
     gemm_tn_kernel<64, 128, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
   else if (cfg == 1)

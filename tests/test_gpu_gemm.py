@@ -32,15 +32,18 @@ def _ref(a, w):
 
 # The tile is 256 x 256, or 192 x 256 when ceil(tiles / 256 CUs) x rows is
 # smaller with it, or 64 x 128 when fewer than 128 tiles of 256 x 256 would
-# run, or 64 x 64 when fewer than 128 of 64 x 128 would.  64 x 64: (256, 256),
-# (300, 200), (1, 8224), (17, 2048), (256, 2048) (the decode out_proj);
-# 64 x 128: (1000, 2080), (4111, 333);
+# run, or 64 x 64 when fewer than 128 of 64 x 128 would.  The 64-row tiles run
+# the deeper load pipeline (gemm_tn_deep_kernel) when K >= 1024.  64 x 64:
+# (256, 256), (300, 200); deep: (1, 8224), (17, 2048), (256, 2048) (the decode
+# out_proj), (100, 2000, 1088) (17 steps: a partial last round of stages);
+# 64 x 128: (1000, 2080), (4111, 333); deep: (256, 8224) (the decode in_proj),
+# (300, 8224, 1024) (16 steps, ragged rows);
 # 192 x 256: (17000, 2048) = 712 tiles of 192 rows (3 waves) against 536 of 256
 # (3 waves); 256 x 256: (8190, 2047) is exactly 256 tiles of 256 rows (344 of
 # 192) and (17000, 8224) ties at 9 waves.
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (300, 200, 128), (1, 8224, 2048), (17, 2048, 2048), (256, 2048, 2048),
-                                   (1000, 2080, 512), (4111, 333, 192), (17000, 2048, 256), (8190, 2047, 128),
-                                   (17000, 8224, 128)])
+                                   (100, 2000, 1088), (1000, 2080, 512), (4111, 333, 192), (256, 8224, 2048),
+                                   (300, 8224, 1024), (17000, 2048, 256), (8190, 2047, 128), (17000, 8224, 128)])
 def test_gemm_against_fp32_matmul(pkg, dev, M, N, K):
     gen = torch.Generator().manual_seed(M * 7 + N)
     a = torch.randn(M, K, generator=gen).to(BF16)
