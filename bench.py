@@ -879,6 +879,22 @@ def main():
                          "step_frac": round(sb_g / tg / 1e9 / HBM_PEAK_GBPS, 4),
                          "inplace_tile_ceiling_us": round(pass_g, 2),
                          "timing": "as decode_config2's roofline"}}
+    if 1 in configs:
+        # config 1's lengths and inputs at Qwen3.5's grouped geometry (16 key
+        # heads, 32 value heads): twice the value heads' state work
+        cg = make_prefill(1, None, Hk=16, Hv=32)
+        tgp, kgp = prefill_bench(pkg, cg, dev, max(2, K // 4), 1)
+        fg = chunk_flops(cg["N"], cg["Hv"], cg["D"])
+        ug = kgp["conv_chunk_prefill"]
+        extra["prefill_gva_16_32_config1_lengths"] = {
+            "tokens_per_s": round(cg["N"] / tgp, 1), "ms_per_step": round(tgp * 1e3, 4),
+            "kernels_us": {k: round(v, 2) for k, v in kgp.items()},
+            "roofline": {"bound": "mfma", "achieved": round(fg / (ug * 1e-6) / 1e12, 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(fg / (ug * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                         "kernel_us": round(ug, 2), "algorithmic_flop_per_launch": fg},
+            "what": "config 1's 8 sequences (17,001 tokens, seed 1) at Hk = 16, Hv = 32, D = 128: the fused launch "
+                    "pair and the gated norm, timed as config 1"}
+        del cg
     if 3 in configs:
         c3 = make_prefill(4, [65536], h0_std=0.1, conv_std=1.0)
         K3 = max(2, K // 4)
