@@ -577,44 +577,57 @@ def spec_bench(pkg, cfg, dev, K, W):
 def gemm_shapes(pkg, dev, R=10):
     """gdn_gemm_bf16 (ops.linear) against torch.matmul (hipBLASLt) on the
     mixer's projection shapes (hidden 2048, config 1's 17,001 tokens and a
-    decode batch of 256) and a square 8192^3: an event pair around R
-    back-to-back launches, three times for each side in turn after about a
-    second of untimed launches (the clock settles under load), the median
-    kept; random operands."""
+    decode batch of 256) and a square 8192^3.  Each side's R back-to-back
+    launches are captured in a HIP graph (as a graph-captured decode step runs
+    them: no host launch cost between the kernels, which at the decode shapes
+    is longer than the kernels), and a replay is timed between one event pair,
+    three times for each side in turn after about a second of untimed replays
+    (the clock settles under load), the median kept; random operands."""
     out = {}
     gen = torch.Generator().manual_seed(13)
     shapes = [(17001, 8224, 2048, "in_proj_config1"), (17001, 2048, 2048, "out_proj_config1"),
               (256, 8224, 2048, "in_proj_decode256"), (256, 2048, 2048, "out_proj_decode256"),
               (8192, 8192, 8192, "square_8192")]
-    ops_ = {}
-    for M, N, K, tag in shapes:
-        a = torch.randn(M, K, generator=gen).to(BF16).to(dev)
-        w = (torch.randn(N, K, generator=gen) / math.sqrt(K)).to(BF16).to(dev)
-        c = torch.empty(M, N, dtype=BF16, device=dev)
-        ops_[tag] = (lambda a=a, w=w, c=c: pkg.ops.linear(a, w, out=c),
-                     lambda a=a, w=w, c=c: torch.matmul(a, w.t(), out=c))
+    graphs = {}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for M, N, K, tag in shapes:
+            a = torch.randn(M, K, generator=gen).to(BF16).to(dev)
+            w = (torch.randn(N, K, generator=gen) / math.sqrt(K)).to(BF16).to(dev)
+            c = torch.empty(M, N, dtype=BF16, device=dev)
+            pair = []
+            for fn in (lambda: pkg.ops.linear(a, w, out=c), lambda: torch.matmul(a, w.t(), out=c)):
+                fn()
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=side):
+                    for _ in range(R):
+                        fn()
+                pair.append(g)
+            graphs[tag] = (pair, a, w, c)
+    torch.cuda.current_stream().wait_stream(side)
     t_end = time.time() + 1.0
     while time.time() < t_end:
-        for ours, _ in ops_.values():
-            ours()
+        for (g_ours, _), *_ in graphs.values():
+            g_ours.replay()
         torch.cuda.synchronize()
 
-    def t(fn):
-        fn()
+    def t(g):
+        g.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(R):
-            fn()
+        g.replay()
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / R * 1e3
     for M, N, K, tag in shapes:
-        ours, lib = ops_[tag]
+        (g_ours, g_lib), *_ = graphs[tag]
         ts, th = [], []
         for _ in range(3):
-            ts.append(t(ours))
-            th.append(t(lib))
+            ts.append(t(g_ours))
+            th.append(t(g_lib))
         us, us_h = statistics.median(ts), statistics.median(th)
         fl = 2.0 * M * N * K
         out[tag] = {"M": M, "N": N, "K": K, "us": round(us, 1), "TFLOPs": round(fl / us / 1e6, 1),
