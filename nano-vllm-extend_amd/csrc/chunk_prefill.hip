@@ -833,7 +833,8 @@ struct __align__(16) StateStage {
   h16x8_t Kt[D / 32 * 4][64];  // K^T fragments [key tile * 4 + token step][lane]; rows in
                                 // position order (row p holds key qswap(p))
   h16x8_t W[2 * (D / 16)][64];  // -W fragments [token tile * D/16 + key step][lane]
-  f32x4_t U[2][2][4][64];       // U = T'' V, fp32: [column tile][token tile][quad][lane]
+  s16x8_t Vc[2][2][2][64];      // V (bf16) [column tile][token tile][16-column half][lane]: A operands of V^T = V I
+  h16x8_t Tb[6][64];            // T'' fragments (A operands of U = T'' V)
   float vec[256];               // record VEC: cQ[64], cK[64], e^gamma
 };
 
@@ -878,9 +879,11 @@ constexpr int kStateWaves = 8;
 //           significant bits
 //   w 4, 5  K: the record's K^T and -W = -T' K for key tiles w - 4 (+ 2), and
 //           the record's vec block, into the stage
-//   w 6, 7  U: U = T'' V for value-column tile w - 6 (fused variant: V is the
-//           conv1d + SiLU of the raw v channels, computed here)
-// Per chunk the chain, U, output and K roles issue 32, 10, 40 and 12
+//   w 6, 7  U: V of value-column tile w - 6 and T'' into the stage (fused
+//           variant: V is the conv1d + SiLU of the raw v channels, computed
+//           here); the chain wave of those columns forms V^T and U = T'' V at
+//           the start of its interval
+// Per chunk the chain, U, output and K roles issue 42, 0, 40 and 12
 // matrix-core products of 32x32x16.
 
 // Per-lane prefetch registers of one chunk, one struct per role.
@@ -906,7 +909,7 @@ struct StateConv {
 
 struct UPrefetch {
   s16x8_t v[2][2];  // V rows (fused: raw rows): token tile tt, value k-step h
-  s16x8_t tb[6];    // T'' fragments
+  s16x8_t tb[3];    // this wave's three of the six T'' fragments (3 c .. 3 c + 2)
 };
 
 template <int D>
@@ -966,7 +969,7 @@ __device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int
 
   const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
-  for (int j = 0; j < 6; ++j) p.tb[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * j);
+  for (int j = 0; j < 3; ++j) p.tb[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * (3 * c + j));
 }
 
 template <int D>
@@ -1072,13 +1075,13 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
   }
 }
 
-// U waves: V^T of column tile c by the natural identity, then U = T'' V; U's
-// C tiles are stored lane-major for the chain wave that owns the columns.
+// U waves: V of column tile c (fused variant: the conv1d + SiLU of the raw
+// v channels) into the stage as the A operands of V^T = V I, with the wave's
+// three of T''s six fragments; the chain wave that owns the columns forms
+// V^T and U = T'' V itself.
 template <int D, bool kX>
 __device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, int c, int lane, s16x8_t (&carry)[2],
                                         uint16_t* tile, const float* wt) {
-  const int li = lane & 31, g = lane >> 5;
-  const s16x8_t in0 = ident_frag(0, li, g), in1 = ident_frag(1, li, g);
   s16x8_t vc[2][2];
   if constexpr (kX) {
     u_conv(p, carry, tile, wt, lane, vc);
@@ -1089,27 +1092,12 @@ __device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, in
       vc[tt][1] = p.v[tt][1];
     }
   }
-  f32x16_t vt[2];
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    vt[tt] = mfma32_bf16(vc[tt][0], in0, zero16());
-    vt[tt] = mfma32_bf16(vc[tt][1], in1, vt[tt]);
-  }
-  h16x8_t vb[4];
+  for (int j = 0; j < 3; ++j) S.Tb[3 * c + j][lane] = as_h8(p.tb[j]);
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) vb[ks] = (ks & 1) ? pack_h8<8>(vt[ks >> 1]) : pack_h8<0>(vt[ks >> 1]);
-  f32x16_t u0 = zero16(), u1 = zero16();
-  u0 = mfma32(as_h8(p.tb[0]), vb[0], u0);
-  u1 = mfma32(as_h8(p.tb[2]), vb[0], u1);
-  u0 = mfma32(as_h8(p.tb[1]), vb[1], u0);
-  u1 = mfma32(as_h8(p.tb[3]), vb[1], u1);
-  u1 = mfma32(as_h8(p.tb[4]), vb[2], u1);
-  u1 = mfma32(as_h8(p.tb[5]), vb[3], u1);
+  for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    S.U[c][0][qd][lane] = f32x4_t{u0[4 * qd], u0[4 * qd + 1], u0[4 * qd + 2], u0[4 * qd + 3]};
-    S.U[c][1][qd][lane] = f32x4_t{u1[4 * qd], u1[4 * qd + 1], u1[4 * qd + 2], u1[4 * qd + 3]};
-  }
+    for (int h = 0; h < 2; ++h) S.Vc[c][tt][h][lane] = vc[tt][h];
 }
 
 // Output waves, first half of a chunk: acc = S^T Q'^T for token tile nt and
@@ -1321,18 +1309,21 @@ __device__ __forceinline__ void chain_pass(StateSmem<D>& sm, int ct, int vc0, in
 
     // Operand fragments of each product are read from LDS as one batch ahead
     // of its MFMAs, so the reads overlap each other instead of each MFMA
-    // waiting out an LDS latency: first the U tiles that the first products
-    // accumulate onto, then -W in k-step order.
-    f32x16_t U[2];
+    // waiting out an LDS latency: first the V^T and T'' fragments of
+    // U = T'' V (the products -W S accumulate onto; U = 0 for a transition),
+    // then -W in k-step order.
+    f32x16_t U[2] = {zero16(), zero16()};
     h16x8_t wf[2][KS];
+    s16x8_t vcf[2][2];
+    h16x8_t tbf[6];
+    if constexpr (!kP) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4_t u4 = kP ? f32x4_t{0.f, 0.f, 0.f, 0.f} : B.U[ct][mt][qd][ln];
+        for (int h = 0; h < 2; ++h) vcf[tt][h] = B.Vc[ct][tt][h][ln];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) U[mt][4 * qd + rr] = u4[rr];
-      }
+      for (int j = 0; j < 6; ++j) tbf[j] = B.Tb[j][ln];
+    }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       wf[0][s] = B.W[s][ln];
@@ -1353,6 +1344,25 @@ __device__ __forceinline__ void chain_pass(StateSmem<D>& sm, int ct, int vc0, in
     if constexpr (!kP) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) sm.xs.Sh[ct][s][ln] = Sh[s];
+      // V^T by the natural identity (exact), then U = T'' V: these products
+      // do not wait on S, and the decay below runs while they do (the same
+      // products in the same order as a separate wave's would be)
+      const s16x8_t in0 = ident_frag(0, ln & 31, ln >> 5), in1 = ident_frag(1, ln & 31, ln >> 5);
+      f32x16_t vt[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        vt[tt] = mfma32_bf16(vcf[tt][0], in0, zero16());
+        vt[tt] = mfma32_bf16(vcf[tt][1], in1, vt[tt]);
+      }
+      h16x8_t vbf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) vbf[ks] = (ks & 1) ? pack_h8<8>(vt[ks >> 1]) : pack_h8<0>(vt[ks >> 1]);
+      U[0] = mfma32(tbf[0], vbf[0], U[0]);
+      U[1] = mfma32(tbf[2], vbf[0], U[1]);
+      U[0] = mfma32(tbf[1], vbf[1], U[0]);
+      U[1] = mfma32(tbf[3], vbf[1], U[1]);
+      U[1] = mfma32(tbf[4], vbf[2], U[1]);
+      U[1] = mfma32(tbf[5], vbf[3], U[1]);
     }
 #pragma unroll
     for (int rt = 0; rt < NR; ++rt)
