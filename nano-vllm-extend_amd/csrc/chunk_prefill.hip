@@ -877,12 +877,12 @@ constexpr int kStateWaves = 8;
 //           chain waves' flags show S), Vn^T A^T in the next one, as three
 //           fp16 products (Vh A + Vl A + Vh A_lo) that carry Vn and A to ~22
 //           significant bits
-//   w 4, 5  K: the record's K^T and -W = -T' K for key tiles w - 4 (+ 2), and
-//           the record's vec block, into the stage
-//   w 6, 7  U: V of value-column tile w - 6 and T'' into the stage (fused
-//           variant: V is the conv1d + SiLU of the raw v channels, computed
-//           here); the chain wave of those columns forms V^T and U = T'' V at
-//           the start of its interval
+//   w 4, 5  K: the record's K^T and -W = -T' K for key tiles w - 4 (+ 2), the
+//           record's vec block and T'' (three fragments each), into the stage
+//   w 6, 7  U: V of value-column tile w - 6 into the stage (fused variant: V
+//           is the conv1d + SiLU of the raw v channels, computed here); the
+//           chain wave of those columns forms V^T and U = T'' V at the start
+//           of its interval
 // Per chunk the chain, U, output and K roles issue 42, 0, 40 and 12
 // matrix-core products of 32x32x16.
 
@@ -892,6 +892,7 @@ struct KPrefetch {
   static constexpr int NKT = D / 64;  // key tiles per K wave: pk, pk + 2
   s16x8_t k[NKT][4];                  // K^T fragments: key tile pk + 2u, token step
   s16x8_t tw[6];                      // -T' fragments
+  s16x8_t tb[3];                      // this wave's three of the six T'' fragments (3 pk .. 3 pk + 2)
   s16x8_t vec;                        // the lane's 16 bytes of the record vec block
 };
 
@@ -909,7 +910,6 @@ struct StateConv {
 
 struct UPrefetch {
   s16x8_t v[2][2];  // V rows (fused: raw rows): token tile tt, value k-step h
-  s16x8_t tb[3];    // this wave's three of the six T'' fragments (3 c .. 3 c + 2)
 };
 
 template <int D>
@@ -948,16 +948,18 @@ __device__ __forceinline__ void k_prefetch_kt(KPrefetch<D>& p, const uint8_t* re
 }
 
 template <int D>
-__device__ __forceinline__ void k_prefetch_tw(KPrefetch<D>& p, const uint8_t* rec, int lane) {
+__device__ __forceinline__ void k_prefetch_tw(KPrefetch<D>& p, const uint8_t* rec, int pk, int lane) {
   const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
   for (int j = 0; j < 6; ++j) p.tw[j] = buf_ld(r, 16 * lane, Rec::TW + 1024 * j);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) p.tb[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * (3 * pk + j));
 }
 
 // V rows past the sequence end re-read its last token: those tokens carry
 // zero weights in T'', and their outputs are not stored.
-__device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int sv, const uint8_t* rec,
-                                           int64_t tok0, int len, int c, int lane) {
+__device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int sv, int64_t tok0, int len, int c,
+                                           int lane) {
   const int li = lane & 31, g = lane >> 5;
   const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vh + tok0 * sv);
 #pragma unroll
@@ -966,10 +968,6 @@ __device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int
     p.v[tt][0] = buf_ld(rv, off, 0);
     p.v[tt][1] = buf_ld(rv, off, 32);
   }
-
-  const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
-#pragma unroll
-  for (int j = 0; j < 3; ++j) p.tb[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * (3 * c + j));
 }
 
 template <int D>
@@ -1000,6 +998,8 @@ __device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int p
   constexpr int KS = D / 16;
   constexpr int NKT = KPrefetch<D>::NKT;
   *reinterpret_cast<s16x8_t*>(reinterpret_cast<uint8_t*>(S.vec) + 16 * lane) = p.vec;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) S.Tb[3 * pk + j][lane] = as_h8(p.tb[j]);
   f32x16_t cw[NKT][2];
 #pragma unroll
   for (int u = 0; u < NKT; ++u) {
@@ -1016,7 +1016,7 @@ __device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int p
   // The next chunk's loads go out as soon as these registers are read: a
   // single set of registers then carries a whole iteration's worth of loads.
   k_prefetch_kt<D>(p, next_rec, pk, lane);
-  k_prefetch_tw<D>(p, next_rec, lane);
+  k_prefetch_tw<D>(p, next_rec, pk, lane);
   gdn::keep_loads_here();
 #pragma unroll
   for (int u = 0; u < NKT; ++u) {
@@ -1092,8 +1092,6 @@ __device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, in
       vc[tt][1] = p.v[tt][1];
     }
   }
-#pragma unroll
-  for (int j = 0; j < 3; ++j) S.Tb[3 * c + j][lane] = as_h8(p.tb[j]);
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -1661,7 +1659,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
           }
           wave_sync();
         }
-#define GDN_UPF(P, jc) u_prefetch(P, vh, svi, rec0 + (jc) * rec_stride, bos + (jc) * kC, GDN_LEN(jc), c, lane)
+#define GDN_UPF(P, jc) u_prefetch(P, vh, svi, bos + (jc) * kC, GDN_LEN(jc), c, lane)
 #define GDN_UST(P, jc) u_stage<D, kX>(P, sm.st[(jc) & 1], c, lane, carry, sm.vtile[c], sm.vw[c])
         UPrefetch p0, p1, p2;
         GDN_UPF(p0, 0);
@@ -1696,10 +1694,10 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #define GDN_KSTAGE(P, jc, jn) k_stage<D>(P, sm.st[(jc) & 1], pk, lane, rec0 + (jn) * rec_stride)
         KPrefetch<D> p0, p1;
         k_prefetch_kt<D>(p0, rec0, pk, lane);
-        k_prefetch_tw<D>(p0, rec0, lane);
+        k_prefetch_tw<D>(p0, rec0, pk, lane);
         gdn::keep_loads_here();
         k_prefetch_kt<D>(p1, rec0 + min<int64_t>(1, nch - 1) * rec_stride, pk, lane);
-        k_prefetch_tw<D>(p1, rec0 + min<int64_t>(1, nch - 1) * rec_stride, lane);
+        k_prefetch_tw<D>(p1, rec0 + min<int64_t>(1, nch - 1) * rec_stride, pk, lane);
         gdn::keep_loads_here();
         GDN_KSTAGE(p0, 0, min<int64_t>(2, nch - 1));
         gdn::lds_barrier();
