@@ -1126,12 +1126,9 @@ __device__ __forceinline__ void o_inter(const QPrefetch<D>& p, const StateXchgS<
 }
 
 // Output waves, second half (the interval after): acc += Vn^T A^T as
-// Vh A + Vl A + Vh A_lo, then the bf16 tile goes out.  The C tiles give each
-// lane 4 columns of a row per store; rows go out whole instead (8 lanes per
-// 128-byte row), through the wave's own LDS tile.
-__device__ __forceinline__ void o_intra_store(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[2],
-                                              uint16_t* ot, uint16_t* ob, int len, int Hv, int D, int nt,
-                                              int lane) {
+// Vh A + Vl A + Vh A_lo (o_intra), then the bf16 tile goes out (o_store).
+__device__ __forceinline__ void o_intra(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[2], int nt,
+                                        int lane) {
   h16x8_t vh[2][4], vl[2][4];
 #pragma unroll
   for (int c = 0; c < 2; ++c)
@@ -1170,6 +1167,15 @@ __device__ __forceinline__ void o_intra_store(const APrefetch& p, const StateXch
     acc[0] = mfma32(vh[0][s], af[s], acc[0]);
     acc[1] = mfma32(vh[1][s], af[s], acc[1]);
   }
+}
+
+// The C tiles give each lane 4 columns of a row per store; rows go out whole
+// instead (8 lanes per 128-byte row), through the wave's own LDS tile.  The
+// caller issues the next chunk's A loads before this: gfx9 counts loads and
+// stores on one counter, in order, so loads issued after the stores would not
+// count as arrived before the stores had completed.
+__device__ __forceinline__ void o_store(const f32x16_t (&acc)[2], uint16_t* ot, uint16_t* ob, int len, int Hv, int D,
+                                        int nt, int lane) {
   const int tl = lane & 31, g = lane >> 5;
 #pragma unroll
   for (int c = 0; c < 2; ++c)
@@ -1593,10 +1599,11 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       gdn::keep_loads_here();
       gdn::lds_barrier();
 #define GDN_OITER(jj, QC, AP)                                                                               \
-  o_intra_store(AP, sm.xv[((jj) - 1) & 1], acc, sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, D, nt, lane); \
+  o_intra(AP, sm.xv[((jj) - 1) & 1], acc, nt, lane);                                                       \
   __builtin_amdgcn_sched_barrier(0);                                                                        \
   a_prefetch(AP, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);                            \
   gdn::keep_loads_here();                                                                                   \
+  o_store(acc, sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, D, nt, lane);                                  \
   o_inter<D>(QC, sm.xs, &sm.sflag[0][0], jj, lane, acc);                                                           \
   __builtin_amdgcn_sched_barrier(0);                                                                        \
   q_prefetch<D>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, nt, lane);                        \
@@ -1612,9 +1619,10 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       }
 #undef GDN_OITER
       if ((nch - 1) & 1)
-        o_intra_store(a1, sm.xv[1], acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
+        o_intra(a1, sm.xv[1], acc, nt, lane);
       else
-        o_intra_store(a0, sm.xv[0], acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
+        o_intra(a0, sm.xv[0], acc, nt, lane);
+      o_store(acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
 #undef GDN_ROLL
     } else {
       // ------------------------------------------------------------ U and K --
