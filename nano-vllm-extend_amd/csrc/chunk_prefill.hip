@@ -1101,9 +1101,12 @@ __device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, in
 // Output waves, first half of a chunk: acc = S^T Q'^T for token tile nt and
 // the 32 columns of each chain (two independent accumulation chains), once
 // both chain waves have put the chunk's S in the exchange (flag >= j + 1).
+// Each Q' register is reloaded from `next` (the chunk two ahead) right after
+// its last product: one load between two products, so the wave's loads do not
+// queue up in one burst at the address unit ahead of its products.
 template <int D>
-__device__ __forceinline__ void o_inter(const QPrefetch<D>& p, const StateXchgS<D>& X, const int* sflag,
-                                        int64_t j, int lane, f32x16_t (&acc)[2]) {
+__device__ __forceinline__ void o_inter(QPrefetch<D>& p, const uint8_t* next, const StateXchgS<D>& X,
+                                        const int* sflag, int64_t j, int nt, int lane, f32x16_t (&acc)[2]) {
   constexpr int KS = D / 16;
   const int want = static_cast<int>(j) + 1;
   while (min(__hip_atomic_load(&sflag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
@@ -1118,15 +1121,21 @@ __device__ __forceinline__ void o_inter(const QPrefetch<D>& p, const StateXchgS<
   __builtin_amdgcn_sched_barrier(0);
   acc[0] = zero16();
   acc[1] = zero16();
+  const __amdgpu_buffer_rsrc_t r = buf_rsrc(next);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     acc[0] = mfma32(sh[0][s], as_h8(p.q[s]), acc[0]);
     acc[1] = mfma32(sh[1][s], as_h8(p.q[s]), acc[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    p.q[s] = buf_ld(r, 16 * lane, Rec::QP + 1024 * (nt * KS + s));
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
 // Output waves, second half (the interval after): acc += Vn^T A^T as
 // Vh A + Vl A + Vh A_lo (o_intra), then the bf16 tile goes out (o_store).
+// The A registers are reloaded after all of the products (a_prefetch): the
+// masked copies of fragments 2 and 3 leave no registers for loads in between.
 __device__ __forceinline__ void o_intra(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[2], int nt,
                                         int lane) {
   h16x8_t vh[2][4], vl[2][4];
@@ -1593,9 +1602,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       // the roll stays off the tail of the workgroups that finish last.
       if (roll) GDN_ROLL();
       // interval 0: S^T Q'^T of chunk 0
-      o_inter<D>(q0, sm.xs, &sm.sflag[0][0], 0, lane, acc);
-      __builtin_amdgcn_sched_barrier(0);
-      q_prefetch<D>(q0, rec0 + min<int64_t>(2, nch - 1) * rec_stride, nt, lane);
+      o_inter<D>(q0, rec0 + min<int64_t>(2, nch - 1) * rec_stride, sm.xs, &sm.sflag[0][0], 0, nt, lane, acc);
       gdn::keep_loads_here();
       gdn::lds_barrier();
 #define GDN_OITER(jj, QC, AP)                                                                               \
@@ -1604,9 +1611,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   a_prefetch(AP, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);                            \
   gdn::keep_loads_here();                                                                                   \
   o_store(acc, sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, D, nt, lane);                                  \
-  o_inter<D>(QC, sm.xs, &sm.sflag[0][0], jj, lane, acc);                                                           \
-  __builtin_amdgcn_sched_barrier(0);                                                                        \
-  q_prefetch<D>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, nt, lane);                        \
+  o_inter<D>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, sm.xs, &sm.sflag[0][0], jj, nt, lane, acc); \
   gdn::keep_loads_here();                                                                                   \
   gdn::lds_barrier();
       int64_t j = 1;
