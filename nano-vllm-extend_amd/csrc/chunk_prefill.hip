@@ -2009,20 +2009,6 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
           v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
     return gdn_launch_status();
   };
-  const SegPlan pl = plan_segments(cu_host, select_host, n_seqs, Hv, D, max_segments, seg_ws != nullptr);
-  if (!pl.any && !select_host) {
-    SegList none;
-    none.n = 0;
-    return state_launch(none, n_seqs);
-  }
-  // segment states: per split sequence S_1 .. S_{m+1}, P_1 .. P_m, R_1 .. R_m
-  const int64_t hs = static_cast<int64_t>(Hv) * D * D;
-  float* scratch = reinterpret_cast<float*>(seg_ws);
-  SegList p1, p3;
-  p1.n = 0;
-  p3.n = 0;
-  ScanList sc;
-  sc.n = 0;
   auto item = [](int r, int64_t a, int64_t b, int mode, int ph0, int phT, const float* i0, float* iT,
                  float* iP = nullptr) {
     SegItem it;
@@ -2037,6 +2023,38 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
     it.hP = iP;
     return it;
   };
+  const SegPlan pl = plan_segments(cu_host, select_host, n_seqs, Hv, D, max_segments, seg_ws != nullptr);
+  if (!pl.any && !select_host) {
+    if (cu_host && n_seqs <= kMaxSegItems && static_cast<int64_t>(n_seqs) * Hv * (D / kCB) > gdn::kNumCu) {
+      // More workgroups than CUs (a state workgroup fills its CU): the
+      // sequences go longest first, so that no long chain starts only after a
+      // short one has finished (longest-processing-time order); the ties keep
+      // the sequence order.
+      int order[kMaxSegItems];
+      int64_t nch[kMaxSegItems];
+      for (int r = 0; r < n_seqs; ++r) {
+        nch[r] = (cu_host[r + 1] - cu_host[r] + kC - 1) / kC;
+        int i = r;
+        for (; i > 0 && nch[order[i - 1]] < nch[r]; --i) order[i] = order[i - 1];
+        order[i] = r;
+      }
+      SegList lpt;
+      lpt.n = 0;
+      for (int i = 0; i < n_seqs; ++i) lpt.it[lpt.n++] = item(order[i], 0, nch[order[i]], kSegOut, 1, 1, nullptr, nullptr);
+      return state_launch(lpt, lpt.n);
+    }
+    SegList none;
+    none.n = 0;
+    return state_launch(none, n_seqs);
+  }
+  // segment states: per split sequence S_1 .. S_{m+1}, P_1 .. P_m, R_1 .. R_m
+  const int64_t hs = static_cast<int64_t>(Hv) * D * D;
+  float* scratch = reinterpret_cast<float*>(seg_ws);
+  SegList p1, p3;
+  p1.n = 0;
+  p3.n = 0;
+  ScanList sc;
+  sc.n = 0;
   for (int r = 0; r < n_seqs; ++r) {
     if (select_host && !select_host[r]) continue;
     const int S = pl.any ? pl.nseg[r] : 1;

@@ -186,6 +186,7 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t total) {
 }
 
 constexpr int kNumXcd = 8;
+constexpr int kNumCu = 256;  // MI355X compute units: 8 XCDs x 32
 
 }  // namespace gdn
 

@@ -52,7 +52,7 @@ namespace {
 constexpr int kBK = 64;  // the tile (BM x BN) is a template argument
 constexpr int kGemmThreads = 256;
 constexpr int kGroupM = 4;  // row blocks per tile group
-constexpr int kCUs = 256;   // MI355X compute units: 8 XCDs x 32
+constexpr int kCUs = gdn::kNumCu;
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
