@@ -149,6 +149,17 @@ int gdn_chunk_prefill(const uint16_t* q, int64_t sq_tok, const uint16_t* k, int6
  * sequences (an upper bound over the sequence lengths); -1 on bad args. */
 int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D);
 
+/* Column split of the chunk prefills' state pass when no sequence is cut into
+ * segments (no counterpart in the reference: a tuning and test control).  The
+ * state's value columns are independent, so a sequence's heads can run in
+ * workgroups of 64 columns (the default) or of 32, which finish each chunk
+ * sooner but take twice the CUs; results are the same either way, bit for
+ * bit.  mode 0 = the k longest sequences (k <= 4, from a list-schedule
+ * estimate over the CUs) in 32-column workgroups, 1 = all in 64-column ones,
+ * 2 = all in 32-column ones.  Process-wide; set it between calls.  Returns
+ * GDN_ERR_INVALID_ARG for another mode. */
+int gdn_set_column_split(int mode);
+
 /*
  * Fused varlen prefill of the layer core's first three steps: gates, causal
  * conv1d + SiLU with the conv-state roll, and the chunked gated delta rule.

@@ -46,6 +46,7 @@ SIGNATURES: dict[str, list] = {
     "gdn_chunk_prefill": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _p, _p, _i32, _i32, _i64,
                           _i32, _i32, _i32, _f32, _i32, _p, _p, _i64, _p],
     "gdn_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],
+    "gdn_set_column_split": [_i32],
     "gdn_conv_chunk_prefill": [_p, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _i64, _p, _p,
                                _i32, _i32, _p, _i32, _i64, _i32, _i32, _i32, _f32, _i32, _p, _p, _i64, _p],
     "gdn_conv_chunk_prefill_workspace_size": [_i64, _i32, _i32, _i32],

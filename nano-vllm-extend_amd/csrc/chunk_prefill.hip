@@ -909,7 +909,7 @@ struct StateConv {
 };
 
 struct UPrefetch {
-  s16x8_t v[2][2];  // V rows (fused: raw rows): token tile tt, value k-step h
+  s16x8_t v[2][2];  // V rows (fused: raw rows): token tile tt, the wave's value k-step i (NH of them)
 };
 
 template <int D>
@@ -958,15 +958,18 @@ __device__ __forceinline__ void k_prefetch_tw(KPrefetch<D>& p, const uint8_t* re
 
 // V rows past the sequence end re-read its last token: those tokens carry
 // zero weights in T'', and their outputs are not stored.
+// (NH 16-column halves of tile c from half hb on: both halves in a
+// 64-column workgroup, one per U wave in a 32-column one)
+template <int NH>
 __device__ __forceinline__ void u_prefetch(UPrefetch& p, const uint16_t* vh, int sv, int64_t tok0, int len, int c,
-                                           int lane) {
+                                           int hb, int lane) {
   const int li = lane & 31, g = lane >> 5;
   const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vh + tok0 * sv);
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     const int off = 2 * (min(32 * tt + li, len - 1) * sv + 32 * c + 8 * g);
-    p.v[tt][0] = buf_ld(rv, off, 0);
-    p.v[tt][1] = buf_ld(rv, off, 32);
+#pragma unroll
+    for (int i = 0; i < NH; ++i) p.v[tt][i] = buf_ld(rv, off, 32 * (hb + i));
   }
 }
 
@@ -1037,21 +1040,23 @@ __device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int p
 // channels' taps (fp32, 4 per channel).  Every conv goes through
 // gdn::conv4_silu in the standalone kernel's operation order, so the values
 // are bit-identical.
+template <int NH>
 __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], uint16_t* tile, const float* wt,
-                                       int lane, s16x8_t (&vc)[2][2]) {
+                                       int lane, s16x8_t (&vc)[2][2], int hb) {
   const int li = lane & 31, g = lane >> 5;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    *reinterpret_cast<s16x8_t*>(&tile[(3 + li) * 16 + 8 * g]) = p.v[0][h];
-    *reinterpret_cast<s16x8_t*>(&tile[(35 + li) * 16 + 8 * g]) = p.v[1][h];
-    if (li < 3) *reinterpret_cast<s16x8_t*>(&tile[li * 16 + 8 * g]) = carry[h];
+  for (int i = 0; i < NH; ++i) {
+    const int h = hb + i;  // the half's 16 channels within the tile
+    *reinterpret_cast<s16x8_t*>(&tile[(3 + li) * 16 + 8 * g]) = p.v[0][i];
+    *reinterpret_cast<s16x8_t*>(&tile[(35 + li) * 16 + 8 * g]) = p.v[1][i];
+    if (li < 3) *reinterpret_cast<s16x8_t*>(&tile[li * 16 + 8 * g]) = carry[i];
     wave_sync();
     uint4 x[2][3];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int i = 0; i < 3; ++i) x[tt][i] = *reinterpret_cast<const uint4*>(&tile[(32 * tt + li + i) * 16 + 8 * g]);
-    carry[h] = *reinterpret_cast<const s16x8_t*>(&tile[(64 + min(li, 2)) * 16 + 8 * g]);
+    carry[i] = *reinterpret_cast<const s16x8_t*>(&tile[(64 + min(li, 2)) * 16 + 8 * g]);
     uint32_t y[2][4];
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) {
@@ -1064,13 +1069,13 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
           yy[tt][cc] = gdn::conv4_silu(bf_elem(x[tt][0], e), bf_elem(x[tt][1], e), bf_elem(x[tt][2], e),
-                                       bf_elem(__builtin_bit_cast(uint4, p.v[tt][h]), e), wk);
+                                       bf_elem(__builtin_bit_cast(uint4, p.v[tt][i]), e), wk);
       }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) y[tt][e2] = gdn::f2bf2(yy[tt][0], yy[tt][1]);
     }
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) vc[tt][h] = __builtin_bit_cast(s16x8_t, u32x4_t{y[tt][0], y[tt][1], y[tt][2], y[tt][3]});
+    for (int tt = 0; tt < 2; ++tt) vc[tt][i] = __builtin_bit_cast(s16x8_t, u32x4_t{y[tt][0], y[tt][1], y[tt][2], y[tt][3]});
     wave_sync();  // the tile is read before the next half's rows go in
   }
 }
@@ -1079,53 +1084,58 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
 // v channels) into the stage as the A operands of V^T = V I, with the wave's
 // three of T''s six fragments; the chain wave that owns the columns forms
 // V^T and U = T'' V itself.
-template <int D, bool kX>
-__device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, int c, int lane, s16x8_t (&carry)[2],
-                                        uint16_t* tile, const float* wt) {
+template <int D, bool kX, int NH>
+__device__ __forceinline__ void u_stage(const UPrefetch& p, StateStage<D>& S, int c, int hb, int lane,
+                                        s16x8_t (&carry)[2], uint16_t* tile, const float* wt) {
   s16x8_t vc[2][2];
   if constexpr (kX) {
-    u_conv(p, carry, tile, wt, lane, vc);
+    u_conv<NH>(p, carry, tile, wt, lane, vc, hb);
   } else {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      vc[tt][0] = p.v[tt][0];
-      vc[tt][1] = p.v[tt][1];
-    }
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < NH; ++i) vc[tt][i] = p.v[tt][i];
   }
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) S.Vc[c][tt][h][lane] = vc[tt][h];
+    for (int i = 0; i < NH; ++i) S.Vc[c][tt][hb + i][lane] = vc[tt][i];
 }
 
 // Output waves, first half of a chunk: acc = S^T Q'^T for token tile nt and
-// the 32 columns of each chain (two independent accumulation chains), once
-// both chain waves have put the chunk's S in the exchange (flag >= j + 1).
+// the 32 columns of each of the workgroup's NC chains (independent
+// accumulation chains), once the chain waves have put the chunk's S in the
+// exchange (flag >= j + 1).
 // Each Q' register is reloaded from `next` (the chunk two ahead) right after
 // its last product: one load between two products, so the wave's loads do not
 // queue up in one burst at the address unit ahead of its products.
-template <int D>
+template <int D, int NC>
 __device__ __forceinline__ void o_inter(QPrefetch<D>& p, const uint8_t* next, const StateXchgS<D>& X,
-                                        const int* sflag, int64_t j, int nt, int lane, f32x16_t (&acc)[2]) {
+                                        const int* sflag, int64_t j, int nt, int lane, f32x16_t (&acc)[NC]) {
   constexpr int KS = D / 16;
   const int want = static_cast<int>(j) + 1;
-  while (min(__hip_atomic_load(&sflag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
-             __hip_atomic_load(&sflag[64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < want)
-    __builtin_amdgcn_s_sleep(1);
+  if constexpr (NC == 2) {
+    while (min(__hip_atomic_load(&sflag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
+               __hip_atomic_load(&sflag[64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < want)
+      __builtin_amdgcn_s_sleep(1);
+  } else {
+    while (__hip_atomic_load(&sflag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < want)
+      __builtin_amdgcn_s_sleep(1);
+  }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-  h16x8_t sh[2][KS];
+  h16x8_t sh[NC][KS];
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int s = 0; s < KS; ++s) sh[c][s] = X.Sh[c][s][lane];
   __builtin_amdgcn_sched_barrier(0);
-  acc[0] = zero16();
-  acc[1] = zero16();
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = zero16();
   const __amdgpu_buffer_rsrc_t r = buf_rsrc(next);
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    acc[0] = mfma32(sh[0][s], as_h8(p.q[s]), acc[0]);
-    acc[1] = mfma32(sh[1][s], as_h8(p.q[s]), acc[1]);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = mfma32(sh[c][s], as_h8(p.q[s]), acc[c]);
     __builtin_amdgcn_sched_barrier(0);
     p.q[s] = buf_ld(r, 16 * lane, Rec::QP + 1024 * (nt * KS + s));
     __builtin_amdgcn_sched_barrier(0);
@@ -1136,11 +1146,12 @@ __device__ __forceinline__ void o_inter(QPrefetch<D>& p, const uint8_t* next, co
 // Vh A + Vl A + Vh A_lo (o_intra), then the bf16 tile goes out (o_store).
 // The A registers are reloaded after all of the products (a_prefetch): the
 // masked copies of fragments 2 and 3 leave no registers for loads in between.
-__device__ __forceinline__ void o_intra(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[2], int nt,
+template <int NC>
+__device__ __forceinline__ void o_intra(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[NC], int nt,
                                         int lane) {
-  h16x8_t vh[2][4], vl[2][4];
+  h16x8_t vh[NC][4], vl[NC][4];
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       vh[c][s] = X.Vh[c][s][lane];
@@ -1162,38 +1173,40 @@ __device__ __forceinline__ void o_intra(const APrefetch& p, const StateXchgV& X,
   }
   // the residual products, then the rounded one
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    acc[0] = mfma32(vl[0][s], af[s], acc[0]);
-    acc[1] = mfma32(vl[1][s], af[s], acc[1]);
-  }
+  for (int s = 0; s < 4; ++s)
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    acc[0] = mfma32(vh[0][s], alf[s], acc[0]);
-    acc[1] = mfma32(vh[1][s], alf[s], acc[1]);
-  }
+    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vl[c][s], af[s], acc[c]);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    acc[0] = mfma32(vh[0][s], af[s], acc[0]);
-    acc[1] = mfma32(vh[1][s], af[s], acc[1]);
-  }
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vh[c][s], alf[s], acc[c]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vh[c][s], af[s], acc[c]);
 }
 
 // The C tiles give each lane 4 columns of a row per store; rows go out whole
-// instead (8 lanes per 128-byte row), through the wave's own LDS tile.  The
-// caller issues the next chunk's A loads before this: gfx9 counts loads and
-// stores on one counter, in order, so loads issued after the stores would not
-// count as arrived before the stores had completed.
-__device__ __forceinline__ void o_store(const f32x16_t (&acc)[2], uint16_t* ot, uint16_t* ob, int len, int Hv, int D,
+// instead (the tile's 32 NC columns as 16-byte pieces, 4 NC lanes per row),
+// through the wave's own LDS tile.  The caller issues the next chunk's A loads
+// before this: gfx9 counts loads and stores on one counter, in order, so loads
+// issued after the stores would not count as arrived before the stores had
+// completed.
+template <int NC>
+__device__ __forceinline__ void o_store(const f32x16_t (&acc)[NC], uint16_t* ot, uint16_t* ob, int len, int Hv, int D,
                                         int nt, int lane) {
+  constexpr int W = 32 * NC;       // tile columns
+  constexpr int LPR = W / 8;       // lanes per row
+  constexpr int RPI = 64 / LPR;    // rows per store instruction
   const int tl = lane & 31, g = lane >> 5;
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       u32x2_t pk;
       pk[0] = gdn::f2bf2(acc[c][4 * i], acc[c][4 * i + 1]);
       pk[1] = gdn::f2bf2(acc[c][4 * i + 2], acc[c][4 * i + 3]);
-      *reinterpret_cast<u32x2_t*>(&ot[swz<kCB>(tl, 32 * c + 8 * i + 4 * g)]) = pk;
+      *reinterpret_cast<u32x2_t*>(&ot[swz<W>(tl, 32 * c + 8 * i + 4 * g)]) = pk;
     }
   wave_sync();
   // Raw buffer stores whose range ends at the chunk's last token: rows past
@@ -1201,11 +1214,11 @@ __device__ __forceinline__ void o_store(const f32x16_t (&acc)[2], uint16_t* ot, 
   // the same stores.
   const __amdgpu_buffer_rsrc_t r =
       __builtin_amdgcn_make_buffer_rsrc(ob, static_cast<short>(0), len * Hv * D * 2, 0x00020000);
-  const int gr = lane & 7;
+  const int gr = lane % LPR;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int row = 8 * u + (lane >> 3);
-    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(&ot[swz<kCB>(row, 8 * gr)]);
+  for (int u = 0; u < 32 / RPI; ++u) {
+    const int row = RPI * u + lane / LPR;
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(&ot[swz<W>(row, 8 * gr)]);
     __builtin_amdgcn_raw_buffer_store_b128(x, r, 2 * ((32 * nt + row) * Hv * D + 8 * gr), 0, 0);
   }
   wave_sync();  // the tile is read before the next chunk's writes
@@ -1214,9 +1227,9 @@ __device__ __forceinline__ void o_store(const f32x16_t (&acc)[2], uint16_t* ot, 
 // Conv-state roll of the fused variant, done here because the prep kernel
 // reads the old q and k taps from every chunk-0 workgroup of a sequence (the
 // value heads that share a key head included), and this kernel runs after all
-// of them.  Workgroup (sequence r, value head h, column block cb) rolls its 64
-// v channels, and the q and k channels of its columns when h is the first
-// value head of its key head: state taps j = 0..2 <- the raw inputs at
+// of them.  Workgroup (sequence r, value head h, columns col0 .. col0 +
+// width - 1) rolls those v channels, and the q and k channels of its columns
+// when h is the first value head of its key head: state taps j = 0..2 <- the raw inputs at
 // positions T - 3 + j (old taps T + j where that is negative), as the
 // standalone conv kernel does.  The output waves roll after the first
 // workgroup barrier: the U waves read the v channels' old taps for their first
@@ -1225,14 +1238,14 @@ __device__ __forceinline__ void o_store(const f32x16_t (&acc)[2], uint16_t* ot, 
 
 template <int D>
 __device__ __forceinline__ void conv_roll(const StateConv& cr, int64_t slot, bool fresh, int64_t bos, int64_t T, int h,
-                                          int cb, int i0, int nthreads) {
+                                          int col0, int width, int i0, int nthreads) {
   const bool qk = h % cr.ratio == 0;
   const int kh = h / cr.ratio;
-  const int ntask = (qk ? 3 : 1) * kCB;
+  const int ntask = (qk ? 3 : 1) * width;
   for (int task = i0; task < ntask; task += nthreads) {
-    const int part = qk ? task / kCB : 2;
-    const int ch = (part == 0 ? kh * D : part == 1 ? cr.key_dim + kh * D : 2 * cr.key_dim + h * D) + cb * kCB +
-                   task % kCB;
+    const int part = qk ? task / width : 2;
+    const int ch = (part == 0 ? kh * D : part == 1 ? cr.key_dim + kh * D : 2 * cr.key_dim + h * D) + col0 +
+                   task % width;
     uint16_t* st = cr.cstate + slot * cr.ss_seq + static_cast<int64_t>(ch) * cr.ss_ch;
     uint16_t val[3];
 #pragma unroll
@@ -1270,8 +1283,14 @@ struct SegItem {
   float* hP;            // kSegBoth: [Hv, D, D] the segment's transition P
 };
 struct SegList {
-  int n;  // 0: one item per sequence, states at the pool rows (the plain launch)
+  int n = 0;  // 0: one item per sequence, states at the pool rows (the plain launch)
+  int n_narrow = 0;  // items 0 .. n_narrow - 1 run in 32-column workgroups (the rest in 64)
   SegItem it[kMaxSegItems];
+};
+
+template <int N>
+struct NcTag {
+  static constexpr int value = N;
 };
 
 // The recurrence of one 32-column tile of the state (ct: the tile within the
@@ -1472,12 +1491,11 @@ __device__ __forceinline__ void chain_pass(StateSmem<D>& sm, int ct, int vc0, in
 // chain consumes stage j % 2 and writes exchange j % 2, the K and U waves fill
 // stage (j + 1) % 2, and the output waves read exchange (j - 1) % 2.  No wave
 // reads what another wave wrote before the barrier that separates them.
-template <int D, bool kX>
+template <int D, bool kX, bool kMix>
 __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     const uint16_t* __restrict__ v, int64_t sv, const uint8_t* __restrict__ ws, const float* h0, float* hT,
     const int64_t* __restrict__ ids, int64_t sstride, const int64_t* __restrict__ cu, int n_seqs, int Hv,
     uint16_t* __restrict__ o, StateConv cr, const uint8_t* __restrict__ fresh, SegList segs) {
-  constexpr int NCB = D / kCB;
   constexpr int NR = D / 32;  // 32-row tiles of the state
   constexpr int KS = D / 16;  // k-steps over keys
   __shared__ StateSmem<D> sm;
@@ -1489,17 +1507,33 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   // its XCD's L2 and fabric link loaded while others idle; the NCB column
   // blocks of a head are consecutive on one XCD and share its record reads
   // in that XCD's L2.  grid = 8 * ceil(n_items * Hv / 8) * NCB.
+  // Two grid regions: the first n_narrow items in 32-column workgroups (one
+  // chain, nc = 1 tile of 32 columns, D / 32 blocks per head), then the rest
+  // in 64-column ones (nc = 2).  The first region is a multiple of 8
+  // workgroups, so workgroup b runs on XCD b % 8 in both.
   const int64_t n_items = segs.n ? segs.n : n_seqs;
-  int64_t wi;
+  // (kMix: the instance that holds the 32-column paths; the 64-column-only
+  // instance leaves them out, so its code is not shaped by them)
+  const int64_t n_nar = kMix && segs.n ? segs.n_narrow : 0;
+  const int64_t grid_nar =
+      n_nar ? gdn::kNumXcd * ((n_nar * Hv + gdn::kNumXcd - 1) / gdn::kNumXcd) * (D / 32) : 0;
+  const bool narrow = kMix && blockIdx.x < grid_nar;
+  const int nc = narrow ? 1 : 2;  // 32-column state tiles of the workgroup
+  const int ncb = D / (32 * nc);  // column blocks per head
+  int64_t wi, item0;
   {
-    const int64_t xcd = blockIdx.x % gdn::kNumXcd, k = blockIdx.x / gdn::kNumXcd;
-    const int64_t pair = (k / NCB) * gdn::kNumXcd + xcd;
-    if (pair >= n_items * Hv) return;
-    wi = pair * NCB + k % NCB;
+    const int64_t b = narrow ? blockIdx.x : blockIdx.x - grid_nar;
+    item0 = narrow ? 0 : n_nar;
+    const int64_t n_reg = narrow ? n_nar : n_items - n_nar;
+    const int64_t xcd = b % gdn::kNumXcd, k = b / gdn::kNumXcd;
+    const int64_t pair = (k / ncb) * gdn::kNumXcd + xcd;
+    if (pair >= n_reg * Hv) return;
+    wi = pair * ncb + k % ncb;
   }
-  const int cb = static_cast<int>(wi % NCB);
-  const int h = static_cast<int>((wi / NCB) % Hv);
-  const int item = static_cast<int>(wi / (static_cast<int64_t>(NCB) * Hv));
+  const int cb = static_cast<int>(wi % ncb);
+  const int h = static_cast<int>((wi / ncb) % Hv);
+  const int item = static_cast<int>(item0 + wi / (static_cast<int64_t>(ncb) * Hv));
+  const int col0 = cb * 32 * nc;  // the workgroup's first state column
   int r, mode;
   int64_t c0;
   int64_t nch;  // chunks of the item
@@ -1550,13 +1584,21 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int li = lane & 31, g = lane >> 5;
+  // A narrow workgroup's second chain wave has no columns: it takes part in
+  // the nch + 1 barriers every other wave takes.
+  if (kMix && nc == 1 && wave == 1) {
+    if (nch > 0)
+      for (int64_t j = 0; j <= nch; ++j) gdn::lds_barrier();
+    return;
+  }
 
 #define GDN_LEN(j_) static_cast<int>(min<int64_t>(kC, seqlen - (j_) * kC))
   if (wave >= 2) {
     // one item per sequence (its first chunk, with outputs) rolls the conv
     // state, in its output waves at the start of interval 0
     const bool roll = kX && wave < 4 && c0 == 0 && mode == kSegOut;
-#define GDN_ROLL() conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], seq_bos, seq_len, h, cb, threadIdx.x - 128, 128)
+#define GDN_ROLL() \
+  conv_roll<D>(cr, ids ? ids[r] : r, fresh && fresh[r], seq_bos, seq_len, h, col0, 32 * nc, threadIdx.x - 128, 128)
     if (nch == 0) {
       if (roll) GDN_ROLL();
       return;
@@ -1565,11 +1607,14 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       // the segment's transition P on the output waves: the chain of column
       // tile wave - 2 from the identity's columns, with U = 0 (one barrier
       // before the first chunk and one per chunk, like every role)
-      chain_pass<D, true>(sm, wave - 2, cb * kCB + 32 * (wave - 2), nch, true, nullptr, segs.it[item].hP, h, lane);
+      chain_pass<D, true>(sm, wave - 2, col0 + 32 * (wave - 2), nch, true, nullptr, segs.it[item].hP, h, lane);
       return;
     }
-    if (wave < 4) {
-      // ------------------------------------------------------------ output --
+    // ------------------------------------------------------------ output --
+    // (NC: the workgroup's 32-column tiles, a compile-time count for the
+    // accumulators)
+    auto output_role = [&](auto nc_tag) {
+      constexpr int NC = decltype(nc_tag)::value;
       // In the interval of chunk c (between workgroup barriers c and c + 1)
       // an output wave finishes chunk c - 1 (Vn^T A^T, the store) and runs
       // S^T Q'^T of chunk c.  Chunk c's Q' fragments live in register set
@@ -1581,11 +1626,11 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       // sets go out oldest first, and the loop has a single exit (two chunks
       // per trip, the odd one after it).
       const int nt = wave - 2;
-      uint16_t* oh = o + (bos * Hv + h) * D + cb * kCB;
+      uint16_t* oh = o + (bos * Hv + h) * D + col0;
       const int64_t ostride = static_cast<int64_t>(kC) * Hv * D;
       QPrefetch<D> q0, q1;
       APrefetch a0, a1;
-      f32x16_t acc[2];
+      f32x16_t acc[NC];
       const uint8_t* rec1 = rec0 + min<int64_t>(1, nch - 1) * rec_stride;
       q_prefetch<D>(q0, rec0, nt, lane);
       gdn::keep_loads_here();  // the sets go out oldest first, as in the loop
@@ -1602,16 +1647,17 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       // the roll stays off the tail of the workgroups that finish last.
       if (roll) GDN_ROLL();
       // interval 0: S^T Q'^T of chunk 0
-      o_inter<D>(q0, rec0 + min<int64_t>(2, nch - 1) * rec_stride, sm.xs, &sm.sflag[0][0], 0, nt, lane, acc);
+      o_inter<D, NC>(q0, rec0 + min<int64_t>(2, nch - 1) * rec_stride, sm.xs, &sm.sflag[0][0], 0, nt, lane, acc);
       gdn::keep_loads_here();
       gdn::lds_barrier();
 #define GDN_OITER(jj, QC, AP)                                                                               \
-  o_intra(AP, sm.xv[((jj) - 1) & 1], acc, nt, lane);                                                       \
+  o_intra<NC>(AP, sm.xv[((jj) - 1) & 1], acc, nt, lane);                                                   \
   __builtin_amdgcn_sched_barrier(0);                                                                        \
   a_prefetch(AP, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);                            \
   gdn::keep_loads_here();                                                                                   \
-  o_store(acc, sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, D, nt, lane);                                  \
-  o_inter<D>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, sm.xs, &sm.sflag[0][0], jj, nt, lane, acc); \
+  o_store<NC>(acc, sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, D, nt, lane);                              \
+  o_inter<D, NC>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, sm.xs, &sm.sflag[0][0], jj, nt, lane, \
+                 acc);                                                                                      \
   gdn::keep_loads_here();                                                                                   \
   gdn::lds_barrier();
       int64_t j = 1;
@@ -1624,10 +1670,16 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       }
 #undef GDN_OITER
       if ((nch - 1) & 1)
-        o_intra(a1, sm.xv[1], acc, nt, lane);
+        o_intra<NC>(a1, sm.xv[1], acc, nt, lane);
       else
-        o_intra(a0, sm.xv[0], acc, nt, lane);
-      o_store(acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
+        o_intra<NC>(a0, sm.xv[0], acc, nt, lane);
+      o_store<NC>(acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
+    };
+    if (wave < 4) {
+      if (!kMix || nc == 2)
+        output_role(NcTag<2>{});
+      else
+        output_role(NcTag<1>{});
 #undef GDN_ROLL
     } else {
       // ------------------------------------------------------------ U and K --
@@ -1641,39 +1693,46 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   gdn::keep_loads_here();                                    \
   if ((jj) + 1 < nch) STAGE(ST, (jj) + 1);                   \
   gdn::lds_barrier();
-      if (wave >= 6) {
-        const int c = wave - 6;
-        const uint16_t* vh = v + static_cast<int64_t>(h) * D + cb * kCB;
+      // U waves: in a 64-column workgroup wave 6 + c takes tile c (both of
+      // its 16-column halves), in a 32-column one wave 6 + hb takes half hb of
+      // the one tile (NH: halves per wave, a compile-time count; the wave's
+      // halves sit in register slots 0 .. NH - 1, hb only moves addresses)
+      auto u_role = [&](auto nh_tag) {
+        constexpr int NH = decltype(nh_tag)::value;
+        const int u = wave - 6;
+        const int c = NH == 2 ? u : 0;
+        const int hb = NH == 2 ? 0 : u;
+        const uint16_t* vh = v + static_cast<int64_t>(h) * D + col0;
         const int svi = static_cast<int>(sv);
-        // fused: the conv taps of the wave's channels into LDS, and the carry
+        // fused: the conv taps of the tile's channels into LDS, and the carry
         // rows of the first chunk's window (the rows before the item, or
         // before a sequence its state's taps -- zero, not read, when fresh)
         s16x8_t carry[2] = {s16x8_t{0, 0, 0, 0, 0, 0, 0, 0}, s16x8_t{0, 0, 0, 0, 0, 0, 0, 0}};
         if constexpr (kX) {
           const int li = lane & 31, g = lane >> 5;
-          const int64_t ch0 = 2LL * cr.key_dim + static_cast<int64_t>(h) * D + cb * kCB + 32 * c;
+          const int64_t ch0 = 2LL * cr.key_dim + static_cast<int64_t>(h) * D + col0 + 32 * c;
           if (lane < 32) {
             // channel ch0 + lane's 4 taps, as fp32
             const uint2 wb = reinterpret_cast<const uint2*>(cr.w + ch0 * 4)[lane];
-            reinterpret_cast<float4*>(sm.vw[c])[lane] =
+            reinterpret_cast<float4*>(sm.vw[u])[lane] =
                 make_float4(lo_half(wb.x), hi_half(wb.x), lo_half(wb.y), hi_half(wb.y));
           }
           const int64_t ch = ch0 + 8 * g;
           if (c0 != 0) {
             const uint16_t* hp = vh + (bos - 3 + min(li, 2)) * sv + 32 * c + 8 * g;
-            carry[0] = *reinterpret_cast<const s16x8_t*>(hp);
-            carry[1] = *reinterpret_cast<const s16x8_t*>(hp + 16);
+#pragma unroll
+            for (int i = 0; i < NH; ++i) carry[i] = *reinterpret_cast<const s16x8_t*>(hp + 16 * (hb + i));
           } else if (!(fresh && fresh[r])) {
             const uint16_t* sp = cr.cstate + (ids ? ids[r] : r) * cr.ss_seq + ch * cr.ss_ch + min(li, 2);
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
+            for (int i = 0; i < NH; ++i)
 #pragma unroll
-              for (int e = 0; e < 8; ++e) carry[hh][e] = static_cast<short>(sp[(16 * hh + e) * cr.ss_ch]);
+              for (int e = 0; e < 8; ++e) carry[i][e] = static_cast<short>(sp[(16 * (hb + i) + e) * cr.ss_ch]);
           }
           wave_sync();
         }
-#define GDN_UPF(P, jc) u_prefetch(P, vh, svi, bos + (jc) * kC, GDN_LEN(jc), c, lane)
-#define GDN_UST(P, jc) u_stage<D, kX>(P, sm.st[(jc) & 1], c, lane, carry, sm.vtile[c], sm.vw[c])
+#define GDN_UPF(P, jc) u_prefetch<NH>(P, vh, svi, bos + (jc) * kC, GDN_LEN(jc), c, hb, lane)
+#define GDN_UST(P, jc) u_stage<D, kX, NH>(P, sm.st[(jc) & 1], c, hb, lane, carry, sm.vtile[u], sm.vw[u])
         UPrefetch p0, p1, p2;
         GDN_UPF(p0, 0);
         gdn::keep_loads_here();  // the sets go out oldest first, as in the loop
@@ -1697,6 +1756,12 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
         }
 #undef GDN_UPF
 #undef GDN_UST
+      };
+      if (wave >= 6) {
+        if (!kMix || nc == 2)
+          u_role(NcTag<2>{});
+        else
+          u_role(NcTag<1>{});
       } else {
         // Chunk c's inputs live in register set c % 2; each stage issues the
         // loads of the chunk two ahead as soon as it has read the registers
@@ -1735,7 +1800,7 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
 #undef GDN_LEN
 
   // -------------------------------------------------------------- chain --
-  chain_pass<D, false>(sm, wave, cb * kCB + 32 * wave, nch, false, ih0, ihT, h, lane);
+  chain_pass<D, false>(sm, wave, col0 + 32 * wave, nch, false, ih0, ihT, h, lane);
 }
 // ---- segment scan ----
 // For each split sequence: S_1 = the first segment's final state, then
@@ -1975,6 +2040,99 @@ inline SegPlan plan_segments(const int64_t* cu_host, const uint8_t* select_host,
   return pl;
 }
 
+// Column split of the plain state launch (gdn_set_column_split): 0 = by the
+// estimate below, 1 = every sequence in 64-column workgroups, 2 = every
+// sequence in 32-column ones.
+int g_column_split = 0;
+
+// Chunk period of a 32-column state workgroup, in 64-column periods: its output
+// waves run one accumulation chain instead of two, and its single chain and U
+// waves no longer share their SIMDs' issue with a second output tile.
+constexpr double kNarrowPeriod = 0.93;
+
+// Grid of the state launch: the narrow region (first n_narrow items, D / 32
+// workgroups per head), then the wide one (D / 64 per head), each padded to a
+// multiple of 8 workgroups as the kernel's mapping expects.
+inline int64_t state_grid(int64_t items, int64_t n_narrow, int Hv, int D) {
+  auto region = [&](int64_t n, int ncb) {
+    return n ? gdn::kNumXcd * ((n * Hv + gdn::kNumXcd - 1) / gdn::kNumXcd) * ncb : 0;
+  };
+  return region(n_narrow, D / 32) + region(items - n_narrow, D / kCB);
+}
+
+// The plain launch's item list (no segments): the sequences longest first
+// (longest-processing-time order, ties in sequence order), the k longest in
+// 32-column workgroups.  A state workgroup fills its CU, so the pass is a list
+// schedule of workgroups over the CUs in grid order, each taking nch chunk
+// periods; k is the count (up to 4) whose estimated finish is lowest, narrow
+// only where it saves at least 2 %.  n = 0: the plain order does as well (no
+// narrow item, and every workgroup starts at once).
+inline SegList plan_columns(const int64_t* cu_host, int n_seqs, int Hv, int D) {
+  SegList pl;
+  if (!cu_host || n_seqs > kMaxSegItems || D % 64) return pl;
+  int order[kMaxSegItems];
+  int64_t nch[kMaxSegItems];
+  for (int r = 0; r < n_seqs; ++r) {
+    nch[r] = (cu_host[r + 1] - cu_host[r] + kC - 1) / kC;
+    int i = r;
+    for (; i > 0 && nch[order[i - 1]] < nch[r]; --i) order[i] = order[i - 1];
+    order[i] = r;
+  }
+  const int wide_wgs = Hv * (D / kCB), nar_wgs = Hv * (D / 32);
+  double ft[gdn::kNumCu];  // min-heap of the CUs' finish times
+  auto finish = [&](int k) {
+    int used = 0;
+    double end = 0;
+    for (int i = 0; i < n_seqs; ++i) {
+      const bool nar = i < k;
+      const double dur = static_cast<double>(nch[order[i]]) * (nar ? kNarrowPeriod : 1.0);
+      const int m = nar ? nar_wgs : wide_wgs;
+      for (int w = 0; w < m; ++w) {
+        double t0 = 0;
+        if (used < gdn::kNumCu) {
+          ft[used++] = dur;
+          std::push_heap(ft, ft + used, std::greater<double>());
+        } else {
+          std::pop_heap(ft, ft + used, std::greater<double>());
+          t0 = ft[used - 1];
+          ft[used - 1] = t0 + dur;
+          std::push_heap(ft, ft + used, std::greater<double>());
+        }
+        end = std::max(end, t0 + dur);
+      }
+    }
+    return end;
+  };
+  int k = 0;
+  if (g_column_split == 2) {
+    k = n_seqs;
+  } else if (g_column_split == 0) {
+    double best = finish(0);
+    for (int kk = 1; kk <= std::min(n_seqs, 4); ++kk) {
+      const double t = finish(kk);
+      if (t < 0.98 * best) {
+        best = t;
+        k = kk;
+      }
+    }
+  }
+  if (k == 0 && static_cast<int64_t>(n_seqs) * wide_wgs <= gdn::kNumCu) return pl;
+  for (int i = 0; i < n_seqs; ++i) {
+    SegItem& it = pl.it[pl.n++];
+    it.r = order[i];
+    it.c0 = 0;
+    it.c1 = static_cast<int>(nch[order[i]]);
+    it.mode = kSegOut;
+    it.pool_h0 = 1;
+    it.pool_hT = 1;
+    it.h0 = nullptr;
+    it.hT = nullptr;
+    it.hP = nullptr;
+  }
+  pl.n_narrow = k;
+  return pl;
+}
+
 template <int D>
 int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, const uint16_t* v,
                  int64_t sv, const float* g, const uint16_t* beta, const float* h0, float* hT,
@@ -2000,13 +2158,21 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   if (!(phase & kPhaseState)) return GDN_OK;
   const uint8_t* fresh = cv ? cv->fresh : nullptr;
   auto state_launch = [&](const SegList& sl, int64_t items) {
-    const int64_t cgrid = gdn::kNumXcd * ((items * Hv + gdn::kNumXcd - 1) / gdn::kNumXcd) * (D / kCB);
-    if (cv)
-      chunk_state_kernel<D, true><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
-          v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
+    const int64_t n_nar = sl.n ? sl.n_narrow : 0;
+    const int64_t cgrid = state_grid(items, n_nar, Hv, D);
+    const dim3 gr(static_cast<unsigned>(cgrid)), bl(64 * kStateWaves);
+    if (cv && n_nar)
+      chunk_state_kernel<D, true, true><<<gr, bl, 0, stream>>>(v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr,
+                                                               fresh, sl);
+    else if (cv)
+      chunk_state_kernel<D, true, false><<<gr, bl, 0, stream>>>(v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o,
+                                                                cr, fresh, sl);
+    else if (n_nar)
+      chunk_state_kernel<D, false, true><<<gr, bl, 0, stream>>>(v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o,
+                                                                cr, fresh, sl);
     else
-      chunk_state_kernel<D, false><<<dim3(static_cast<unsigned>(cgrid)), dim3(64 * kStateWaves), 0, stream>>>(
-          v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o, cr, fresh, sl);
+      chunk_state_kernel<D, false, false><<<gr, bl, 0, stream>>>(v, sv, ws, h0, hT, ids, sstride, cu, n_seqs, Hv, o,
+                                                                 cr, fresh, sl);
     return gdn_launch_status();
   };
   auto item = [](int r, int64_t a, int64_t b, int mode, int ph0, int phT, const float* i0, float* iT,
@@ -2025,24 +2191,8 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
   };
   const SegPlan pl = plan_segments(cu_host, select_host, n_seqs, Hv, D, max_segments, seg_ws != nullptr);
   if (!pl.any && !select_host) {
-    if (cu_host && n_seqs <= kMaxSegItems && static_cast<int64_t>(n_seqs) * Hv * (D / kCB) > gdn::kNumCu) {
-      // More workgroups than CUs (a state workgroup fills its CU): the
-      // sequences go longest first, so that no long chain starts only after a
-      // short one has finished (longest-processing-time order); the ties keep
-      // the sequence order.
-      int order[kMaxSegItems];
-      int64_t nch[kMaxSegItems];
-      for (int r = 0; r < n_seqs; ++r) {
-        nch[r] = (cu_host[r + 1] - cu_host[r] + kC - 1) / kC;
-        int i = r;
-        for (; i > 0 && nch[order[i - 1]] < nch[r]; --i) order[i] = order[i - 1];
-        order[i] = r;
-      }
-      SegList lpt;
-      lpt.n = 0;
-      for (int i = 0; i < n_seqs; ++i) lpt.it[lpt.n++] = item(order[i], 0, nch[order[i]], kSegOut, 1, 1, nullptr, nullptr);
-      return state_launch(lpt, lpt.n);
-    }
+    const SegList plan = plan_columns(cu_host, n_seqs, Hv, D);
+    if (plan.n) return state_launch(plan, plan.n);
     SegList none;
     none.n = 0;
     return state_launch(none, n_seqs);
@@ -2094,6 +2244,15 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
 }
 
 }  // namespace
+
+// Column split of the plain state pass: 0 = by the list-schedule estimate
+// (the default), 1 = every sequence in 64-column workgroups, 2 = every
+// sequence in 32-column ones.  Process-wide; set it between calls.
+extern "C" int gdn_set_column_split(int mode) {
+  if (mode < 0 || mode > 2) return GDN_ERR_INVALID_ARG;
+  g_column_split = mode;
+  return GDN_OK;
+}
 
 extern "C" int64_t gdn_chunk_prefill_workspace_size(int64_t N, int n_seqs, int Hv, int D) {
   if (N < 0 || n_seqs < 0 || Hv <= 0 || (D != 64 && D != 128)) return -1;

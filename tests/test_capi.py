@@ -137,6 +137,19 @@ def test_argument_validation_before_launch(pkg):
         _lib.check("gdn_chunk_prefill", _lib.GDN_ERR_UNSUPPORTED)
 
 
+def test_column_split_control(pkg):
+    """gdn_set_column_split takes modes 0-2 only (a host setting, no device work)."""
+    lib = pkg._lib.load()
+    _lib = pkg._lib
+    try:
+        for bad in (-1, 3, 100):
+            assert lib.gdn_set_column_split(bad) == _lib.GDN_ERR_INVALID_ARG
+        for mode in (1, 2, 0):
+            assert lib.gdn_set_column_split(mode) == _lib.GDN_OK
+    finally:
+        lib.gdn_set_column_split(0)
+
+
 def test_stride_validation_before_launch(pkg):
     """Strides too short for the shapes return error codes without touching the device."""
     lib = pkg._lib.load()
