@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 3
+#define GDN_ABI_VERSION 4
 
 #define GDN_OK 0
 #define GDN_ERR_INVALID_ARG (-1) /* shape / stride / pointer rejected */

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = Path(os.environ.get("GDN_MI355X_LIB", Path(__file__).resolve().parent / "lib" / "libgdn_mi355x.so"))
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 GDN_OK = 0
 GDN_ERR_INVALID_ARG = -1
@@ -85,13 +85,16 @@ def load() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
     except OSError as e:  # pragma: no cover - environment dependent
         raise GDNLibraryError(f"cannot load {LIB_PATH}: {e}") from e
+    # the version first: a library of another version may lack entry points
+    lib.gdn_abi_version.argtypes = []
+    lib.gdn_abi_version.restype = ctypes.c_int
+    v = lib.gdn_abi_version()
+    if v != ABI_VERSION:
+        raise GDNLibraryError(f"ABI mismatch: library {v}, bindings {ABI_VERSION}")
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = RESTYPES.get(name, ctypes.c_int)
-    v = lib.gdn_abi_version()
-    if v != ABI_VERSION:
-        raise GDNLibraryError(f"ABI mismatch: library {v}, bindings {ABI_VERSION}")
     _LIB = lib
     return lib
 

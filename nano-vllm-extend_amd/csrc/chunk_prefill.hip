@@ -1045,18 +1045,18 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
                                        int lane, s16x8_t (&vc)[2][2], int hb) {
   const int li = lane & 31, g = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < NH; ++i) {
-    const int h = hb + i;  // the half's 16 channels within the tile
-    *reinterpret_cast<s16x8_t*>(&tile[(3 + li) * 16 + 8 * g]) = p.v[0][i];
-    *reinterpret_cast<s16x8_t*>(&tile[(35 + li) * 16 + 8 * g]) = p.v[1][i];
-    if (li < 3) *reinterpret_cast<s16x8_t*>(&tile[li * 16 + 8 * g]) = carry[i];
+  for (int hs = 0; hs < NH; ++hs) {
+    const int h = hb + hs;  // the half's 16 channels within the tile (register slot hs)
+    *reinterpret_cast<s16x8_t*>(&tile[(3 + li) * 16 + 8 * g]) = p.v[0][hs];
+    *reinterpret_cast<s16x8_t*>(&tile[(35 + li) * 16 + 8 * g]) = p.v[1][hs];
+    if (li < 3) *reinterpret_cast<s16x8_t*>(&tile[li * 16 + 8 * g]) = carry[hs];
     wave_sync();
     uint4 x[2][3];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int i = 0; i < 3; ++i) x[tt][i] = *reinterpret_cast<const uint4*>(&tile[(32 * tt + li + i) * 16 + 8 * g]);
-    carry[i] = *reinterpret_cast<const s16x8_t*>(&tile[(64 + min(li, 2)) * 16 + 8 * g]);
+    carry[hs] = *reinterpret_cast<const s16x8_t*>(&tile[(64 + min(li, 2)) * 16 + 8 * g]);
     uint32_t y[2][4];
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) {
@@ -1069,13 +1069,13 @@ __device__ __forceinline__ void u_conv(const UPrefetch& p, s16x8_t (&carry)[2], 
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
           yy[tt][cc] = gdn::conv4_silu(bf_elem(x[tt][0], e), bf_elem(x[tt][1], e), bf_elem(x[tt][2], e),
-                                       bf_elem(__builtin_bit_cast(uint4, p.v[tt][i]), e), wk);
+                                       bf_elem(__builtin_bit_cast(uint4, p.v[tt][hs]), e), wk);
       }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) y[tt][e2] = gdn::f2bf2(yy[tt][0], yy[tt][1]);
     }
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) vc[tt][i] = __builtin_bit_cast(s16x8_t, u32x4_t{y[tt][0], y[tt][1], y[tt][2], y[tt][3]});
+    for (int tt = 0; tt < 2; ++tt) vc[tt][hs] = __builtin_bit_cast(s16x8_t, u32x4_t{y[tt][0], y[tt][1], y[tt][2], y[tt][3]});
     wave_sync();  // the tile is read before the next half's rows go in
   }
 }
