@@ -2065,8 +2065,10 @@ inline int64_t state_grid(int64_t items, int64_t n_narrow, int Hv, int D) {
 // 32-column workgroups.  A state workgroup fills its CU, so the pass is a list
 // schedule of workgroups over the CUs in grid order, each taking nch chunk
 // periods; k is the count (up to 4) whose estimated finish is lowest, narrow
-// only where it saves at least 2 %.  n = 0: the plain order does as well (no
-// narrow item, and every workgroup starts at once).
+// only where it saves at least 2 %.  Beyond two rounds of 64-column
+// workgroups the estimate is skipped (k = 0): narrow ones only add to a full
+// GPU there.  n = 0: the plain order does as well (no narrow item, and every
+// workgroup starts at once).
 inline SegList plan_columns(const int64_t* cu_host, int n_seqs, int Hv, int D) {
   SegList pl;
   if (!cu_host || n_seqs > kMaxSegItems || D % 64) return pl;
@@ -2106,7 +2108,7 @@ inline SegList plan_columns(const int64_t* cu_host, int n_seqs, int Hv, int D) {
   int k = 0;
   if (g_column_split == 2) {
     k = n_seqs;
-  } else if (g_column_split == 0) {
+  } else if (g_column_split == 0 && static_cast<int64_t>(n_seqs) * wide_wgs <= 2 * gdn::kNumCu) {
     double best = finish(0);
     for (int kk = 1; kk <= std::min(n_seqs, 4); ++kk) {
       const double t = finish(kk);
