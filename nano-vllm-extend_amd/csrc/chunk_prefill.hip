@@ -884,7 +884,10 @@ constexpr int kStateWaves = 8;
 //           chain wave of those columns forms V^T and U = T'' V at the start
 //           of its interval
 // Per chunk the chain, U, output and K roles issue 42, 0, 40 and 12
-// matrix-core products of 32x32x16.
+// matrix-core products of 32x32x16.  A 32-column workgroup (one tile) runs
+// chain wave 0 only (wave 1 takes part in the barriers), output waves on one
+// accumulation chain each (20 products), and U waves 6 and 7 on one 16-column
+// half of the tile each.
 
 // Per-lane prefetch registers of one chunk, one struct per role.
 template <int D>
@@ -1485,9 +1488,11 @@ __device__ __forceinline__ void chain_pass(StateSmem<D>& sm, int ct, int vc0, in
 
 
 
-// grid = 8 * ceil(n_items * Hv / 8) * NCB, NCB = D / 64; block = 64 * 8.
+// grid = state_grid(...) (the 32-column region, then the 64-column one); block = 64 * 8.
 // Workgroup (item: sequence r or a segment of it, value head h, column block cb) owns state columns
-// cb*64 .. cb*64 + 63.  One workgroup barrier per chunk j: before it the
+// col0 .. col0 + 32 nc - 1 (nc = 2 tiles of 32, or 1 in the 32-column region; col0 = 32 nc cb).
+// kMix: the instance that holds the 32-column paths (launched only when the item list has
+// 32-column items).  One workgroup barrier per chunk j: before it the
 // chain consumes stage j % 2 and writes exchange j % 2, the K and U waves fill
 // stage (j + 1) % 2, and the output waves read exchange (j - 1) % 2.  No wave
 // reads what another wave wrote before the barrier that separates them.
@@ -1501,12 +1506,12 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
   __shared__ StateSmem<D> sm;
   __shared__ long long s_base;
 
-  // Work item wi = (item * Hv + h) * NCB + cb.  The (item, head) pairs go
+  // Work item wi = (item * Hv + h) * ncb + cb within a region.  The (item, head) pairs go
   // round-robin over the 8 XCDs (workgroup b runs on XCD b % 8), so every
   // sequence's heads spread over all XCDs and a long sequence does not leave
-  // its XCD's L2 and fabric link loaded while others idle; the NCB column
+  // its XCD's L2 and fabric link loaded while others idle; the ncb column
   // blocks of a head are consecutive on one XCD and share its record reads
-  // in that XCD's L2.  grid = 8 * ceil(n_items * Hv / 8) * NCB.
+  // in that XCD's L2.  A region has 8 * ceil(items * Hv / 8) * ncb workgroups.
   // Two grid regions: the first n_narrow items in 32-column workgroups (one
   // chain, nc = 1 tile of 32 columns, D / 32 blocks per head), then the rest
   // in 64-column ones (nc = 2).  The first region is a multiple of 8
@@ -1977,7 +1982,7 @@ __global__ __launch_bounds__(256) void seg_scan_mfma_kernel(ScanList sl, int Hv)
 }
 
 // Segment plan of one call: how many segments each sequence is cut into.
-// Only when few workgroups would run otherwise (n_seqs * Hv * NCB < 128) and
+// Only when few workgroups would run otherwise (n_seqs * Hv * D / 64 < 128) and
 // the host knows the lengths.  max_segments: 0 = automatic (segments of at
 // least 16 chunks, at most one workgroup per CU in the second pass), 1 =
 // never, k >= 2 = up to k segments per sequence.
