@@ -11,8 +11,8 @@
 //   S   <- e^gamma S + K^T diag(e^{gamma-G}) Vn
 //
 // Two kernels.
-//   chunk_prep_kernel: one workgroup per (chunk, value head), all chunks in
-//     parallel.  Everything that needs only the chunk's own q, k, g, beta:
+//   chunk_prep_kernel: one workgroup per (chunk, key head), all chunks in
+//     parallel, writing one record per value head.  Everything that needs only the chunk's own q, k, g, beta:
 //     the row norms, K K^T, Q K^T, the triangular inverse T (fp32), and it
 //     writes a 57 KiB record: -T' = -T diag(beta e^G / |k|), T'' = T diag(beta),
 //     A and A's fp16 rounding residual as fp16 tiles, the per-token scales,
@@ -466,11 +466,12 @@ __device__ __forceinline__ void conv_chunk_rows(const ConvIn& cv, uint16_t (*Qc)
   conv_compute<D>(R, cv, part, Qc, Kr, tok0, len, kh, h, Hv, ptid);
 }
 
-// grid = 8 * ceil(nc_bound * Hv / 8); block = 256.  One workgroup per
-// (chunk, value head); writes the chunk's record.
+// grid = 8 * ceil(nc_bound * Hv / kR / 8); block = 256.  One workgroup per
+// (chunk, kR value heads of one key head); writes the chunk's record of each.
+// kR = 1, or 2 when Hv = 2 Hk (every value head of a key head).
 // kConv: q, k are the conv1d + SiLU of cv.x and g, beta the gates of cv.a,
 // cv.b, all computed here (the q, k, g, beta arguments unused).
-template <int D, bool kConv>
+template <int D, bool kConv, int kR>
 __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     const uint16_t* __restrict__ q, int64_t sq, const uint16_t* __restrict__ k, int64_t sk,
     const float* __restrict__ g, const uint16_t* __restrict__ beta, const int64_t* __restrict__ cu,
@@ -484,16 +485,20 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
   static_assert(kC * SEG % NT == 0 && NT % SEG == 0, "segment tiling");
   __shared__ PrepSmem<D> sm;
 
-  const int64_t wi = gdn::xcd_remap(blockIdx.x, nc_bound * Hv);
+  // One workgroup per (chunk, kR value heads of one key head): the q and k
+  // rows, their conv and their sums of squares are the key head's; with kR =
+  // 2 the two value heads then run one after the other, each writing its own
+  // record, so the shared part runs once per key head.
+  const int64_t wi = gdn::xcd_remap(blockIdx.x, nc_bound * (Hv / kR));
   if (wi < 0) return;
-  const int h = static_cast<int>(wi % Hv);
-  const int64_t cidx = wi / Hv;
+  const int64_t cidx = wi / (Hv / kR);
+  int h = static_cast<int>(wi % (Hv / kR)) * kR;  // the value head in hand
+  const int kh = h / (Hv / Hk);
   int r;
   int64_t jc;
   if (!locate_chunk(cu, n_seqs, cidx, &r, &jc)) return;
   const int64_t tok0 = cu[r] + jc * kC;
   const int len = static_cast<int>(min<int64_t>(kC, cu[r + 1] - tok0));
-  const int kh = h / (Hv / Hk);
   const uint16_t* qh = q + static_cast<int64_t>(kh) * D;
   const uint16_t* kh_ = k + static_cast<int64_t>(kh) * D;
   uint8_t* rec = ws + (cidx * Hv + h) * rec_bytes(D);
@@ -526,21 +531,45 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     }
   };
   if constexpr (!kConv) q_rows();
-  // gate inputs of token tok0 + lane (used by wave 0), loaded ahead of the
-  // rows by every wave with in-range addresses, so no load waits on a branch
-  float gin, bin, al = 0.f, dtb = 0.f;
-  {
-    const int64_t gi = (tok0 + min(lane, len - 1)) * Hv + h;
+  // gate inputs of token tok0 + lane and value head hh (used by wave 0),
+  // loaded ahead of their use by every wave with in-range addresses, so no
+  // load waits on a branch
+  auto gate_in = [&](int hh, float& gi_, float& bi_, float& al_, float& dt_) {
+    const int64_t gi = (tok0 + min(lane, len - 1)) * Hv + hh;
     if constexpr (kConv) {
-      gin = gdn::bf2f(cv.a[gi]);
-      bin = gdn::bf2f(cv.b[gi]);
-      al = param_bits(cv.A_log, h, cv.param_f32);
-      dtb = param_bits(cv.dt_bias, h, cv.param_f32);
+      gi_ = gdn::bf2f(cv.a[gi]);
+      bi_ = gdn::bf2f(cv.b[gi]);
+      al_ = param_bits(cv.A_log, hh, cv.param_f32);
+      dt_ = param_bits(cv.dt_bias, hh, cv.param_f32);
     } else {
-      gin = g[gi];
-      bin = gdn::bf2f(beta[gi]);
+      gi_ = g[gi];
+      bi_ = gdn::bf2f(beta[gi]);
     }
-  }
+  };
+  // wave 0: the gates' cumulative log-decay G and beta of the chunk's tokens
+  auto gates = [&](float gi_, float bi_, float al_, float dt_) {
+    if (wave == 0) {
+      float gv = 0.f, bv = 0.f;
+      if (lane < len) {
+        if constexpr (kConv) {
+          gv = gdn::gate_g(gi_, al_, dt_);
+          bv = gdn::bf2f(gdn::gate_beta(bi_));
+        } else {
+          gv = gi_;
+          bv = bi_;
+        }
+      }
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o_ = __shfl_up(gv, d, 64);
+        if (lane >= d) gv += o_;
+      }
+      sm.G[lane] = gv;
+      sm.bt[lane] = bv;
+    }
+  };
+  float gin, bin, al = 0.f, dtb = 0.f;
+  gate_in(h, gin, bin, al, dtb);
   gdn::keep_loads_here();
   if constexpr (kConv) {
     conv_chunk_rows<D>(cv, Qc, sm.u.Kr, tok0, len, jc == 0, r, kh, h, Hv, tid);
@@ -555,25 +584,7 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
       *reinterpret_cast<s16x8_t*>(&sm.u.Kr[t][c8 * 8]) = kv8;
     }
   }
-  if (wave == 0) {
-    float gv = 0.f, bv = 0.f;
-    if (lane < len) {
-      if constexpr (kConv) {
-        gv = gdn::gate_g(gin, al, dtb);
-        bv = gdn::bf2f(gdn::gate_beta(bin));
-      } else {
-        gv = gin;
-        bv = bin;
-      }
-    }
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float o_ = __shfl_up(gv, d, 64);
-      if (lane >= d) gv += o_;
-    }
-    sm.G[lane] = gv;
-    sm.bt[lane] = bv;
-  }
+  gates(gin, bin, al, dtb);
   if constexpr (kConv) {
     __syncthreads();  // the conv's q rows are in LDS
     q_rows();
@@ -602,6 +613,34 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     }
   }
   __syncthreads();
+
+  // The K rows, kept in registers for the value heads after the first (the
+  // solve reuses their LDS bytes), and the loop over the key head's value
+  // heads; each writes its record (h, rec), the next one's gate inputs loaded
+  // one head ahead.
+  s16x8_t kkeep[NSEG1];
+  if constexpr (kR > 1) {
+#pragma unroll
+    for (int j = 0; j < NSEG1; ++j) {
+      const int e = tid + NT * j;
+      kkeep[j] = *reinterpret_cast<const s16x8_t*>(&sm.u.Kr[e / SEG][(e % SEG) * 8]);
+    }
+  }
+  float ngin = 0.f, nbin = 0.f, nal = 0.f, ndtb = 0.f;
+#pragma unroll
+  for (int rr = 0; rr < kR; ++rr) {
+  if (rr > 0) {
+    ++h;
+    rec += rec_bytes(D);
+#pragma unroll
+    for (int j = 0; j < NSEG1; ++j) {
+      const int e = tid + NT * j;
+      *reinterpret_cast<s16x8_t*>(&sm.u.Kr[e / SEG][(e % SEG) * 8]) = kkeep[j];
+    }
+    gates(ngin, nbin, nal, ndtb);
+    __syncthreads();
+  }
+  if (rr + 1 < kR) gate_in(h + 1, ngin, nbin, nal, ndtb);
 
   // ---- K^T (as soon as the K rows are in LDS, so its stores retire during
   //      the solve), key tile kt = wave, by a bf16 identity product C = K I
@@ -824,6 +863,10 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     pk.z = f2h2(b.x, b.y);
     pk.w = f2h2(b.z, b.w);
     *reinterpret_cast<uint4*>(rec + (which ? Rec::TB : Rec::TW) + tri_frag_byte(t, 8 * gp)) = pk;
+  }
+  // the T tiles and gates are read before the next value head's K rows and
+  // gates overwrite them
+  if (rr + 1 < kR) __syncthreads();
   }
 }
 
@@ -2146,19 +2189,29 @@ int launch_chunk(const uint16_t* q, int64_t sq, const uint16_t* k, int64_t sk, c
                  const int64_t* ids, int64_t sstride, const int64_t* cu, const int64_t* cu_host, int max_segments,
                  int n_seqs, int64_t nc_bound, int Hk, int Hv, float scale, int l2norm, uint16_t* o, uint8_t* ws,
                  uint8_t* seg_ws, const ConvIn* cv, int phase, const uint8_t* select_host, hipStream_t stream) {
-  const int64_t lwork = nc_bound * Hv;
+  // prep: one workgroup per (chunk, key head) when each key head has two value
+  // heads, else per (chunk, value head)
+  const int kR = Hv == 2 * Hk ? 2 : 1;
+  const int64_t lwork = nc_bound * (Hv / kR);
   const int64_t lgrid = gdn::kNumXcd * ((lwork + gdn::kNumXcd - 1) / gdn::kNumXcd);
   StateConv cr{};
   if (cv)
     cr = StateConv{cv->x, cv->sx, const_cast<uint16_t*>(cv->cstate), cv->ss_seq, cv->ss_ch, cv->w, cv->key_dim, Hv / Hk};
   int st = GDN_OK;
   if (phase & kPhasePrep) {
-    if (cv)
-      chunk_prep_kernel<D, true><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
-          q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, *cv);
+    const dim3 pg(static_cast<unsigned>(lgrid)), pb(256);
+    if (cv && kR == 2)
+      chunk_prep_kernel<D, true, 2><<<pg, pb, 0, stream>>>(q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale,
+                                                           l2norm, ws, *cv);
+    else if (cv)
+      chunk_prep_kernel<D, true, 1><<<pg, pb, 0, stream>>>(q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale,
+                                                           l2norm, ws, *cv);
+    else if (kR == 2)
+      chunk_prep_kernel<D, false, 2><<<pg, pb, 0, stream>>>(q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv,
+                                                            scale, l2norm, ws, ConvIn{});
     else
-      chunk_prep_kernel<D, false><<<dim3(static_cast<unsigned>(lgrid)), dim3(256), 0, stream>>>(
-          q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv, scale, l2norm, ws, ConvIn{});
+      chunk_prep_kernel<D, false, 1><<<pg, pb, 0, stream>>>(q, sq, k, sk, g, beta, cu, n_seqs, nc_bound, Hk, Hv,
+                                                            scale, l2norm, ws, ConvIn{});
     st = gdn_launch_status();
     if (st != GDN_OK) return st;
   }
