@@ -59,6 +59,8 @@ SIGNATURES: dict[str, list] = {
                                    _p],
     "gdn_state_commit": [_p, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _p],
     "gdn_gemm_bf16": [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _i32, _i32, _p],
+    "gdn_gemm_bf16_cols": [_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i32, _i32,
+                           _i32, _p],
     "gdn_rmsnorm_gated": [_p, _i64, _p, _i64, _p, _p, _i64, _i32, _i32, _f32, _p],
     "gdn_state_tile_pass": [_p, _i64, _p, _i32, _i32, _i32, _p],
     "gdn_state_tile_copy": [_p, _p, _i64, _p, _i32, _i32, _i32, _p],

@@ -57,6 +57,17 @@ constexpr int kCUs = gdn::kNumCu;
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// The output: C's columns in up to three parts, part s holding columns
+// [end[s - 1], end[s]) (end[-1] = 0) at c[s] with row stride ld[s]; vec[s]: its
+// rows take 16-byte stores.  Every part boundary is a multiple of 32, so each
+// 32-column block of a tile lies in one part.
+struct GemmOut {
+  uint16_t* c[3];
+  int64_t ld[3];
+  int end[3];
+  int vec[3];
+};
+
 struct GemmGates {
   float* g;               // [M, Hv] fp32 (NULL: no gate outputs)
   uint16_t* beta;         // [M, Hv] bf16
@@ -107,9 +118,9 @@ __device__ __forceinline__ f32x16_t zero16() {
 // (wm, wn).  `scratch`: (BM / 2) x 32 bf16 per wave of LDS that nothing reads
 // any more (the gate outputs go through it).
 template <int BM, int BN>
-__device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[BM / 64][BN / 64], uint16_t* __restrict__ C,
-                                           int64_t ldc, int M, int N, int m0, int n0, int wave, int lane,
-                                           const GemmGates& gt, uint8_t* scratch) {
+__device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[BM / 64][BN / 64], const GemmOut& out, int M,
+                                           int N, int m0, int n0, int wave, int lane, const GemmGates& gt,
+                                           uint8_t* scratch) {
   constexpr int MI = BM / 64, NJ = BN / 64;
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, lg = lane >> 5;
@@ -119,16 +130,19 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[BM / 64][BN / 6
   // first operand with the lower half of the second) leaves lane (li, lg)
   // columns 16 p + 8 lg .. + 7 of pair p = (q 2p, q 2p + 1) in bf16: one
   // 16-byte store per pair, two lanes filling 32 bytes of a row.
-  const bool vec = ldc % 8 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0;
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     const int m = m0 + (BM / 2) * wm + 32 * i + li;
     const bool row_ok = m < M;  // (no early exit: the gate loop below spans every lane)
-    uint16_t* crow = C + static_cast<int64_t>(row_ok ? m : 0) * ldc;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int cb = n0 + (BN / 2) * wn + 32 * j;  // wave-uniform
       if (cb >= N) continue;
+      // the output part of this 32-column block (wave-uniform)
+      const int s = cb < out.end[0] ? 0 : cb < out.end[1] ? 1 : 2;
+      const int cbeg = s == 0 ? 0 : out.end[s - 1], cend = out.end[s];
+      const bool vec = out.vec[s] != 0;
+      uint16_t* crow = out.c[s] + static_cast<int64_t>(row_ok ? m : 0) * out.ld[s] - cbeg;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const int q = 2 * p;
@@ -141,12 +155,12 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[BM / 64][BN / 6
         const uint32_t w[4] = {lo[0], hi[0], lo[1], hi[1]};  // columns n .. n + 7
         const int n = cb + 16 * p + 8 * lg;
         if (!row_ok) {
-        } else if (vec && n + 8 <= N) {
+        } else if (vec && n + 8 <= cend) {
           *reinterpret_cast<uint4*>(crow + n) = make_uint4(w[0], w[1], w[2], w[3]);
         } else {
 #pragma unroll
           for (int t = 0; t < 8; ++t)
-            if (n + t < N) crow[n + t] = static_cast<uint16_t>(w[t / 2] >> (16 * (t % 2)));
+            if (n + t < cend) crow[n + t] = static_cast<uint16_t>(w[t / 2] >> (16 * (t % 2)));
         }
       }
       // Gate outputs from the bf16-rounded b and a columns of this 32-column
@@ -191,7 +205,7 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[BM / 64][BN / 6
 template <int BM, int BN, int kMinWG>
 __global__ __launch_bounds__(kGemmThreads, kMinWG) void gemm_tn_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                    const uint16_t* __restrict__ B, int64_t ldb,
-                                                                   uint16_t* __restrict__ C, int64_t ldc, int M,
+                                                                   GemmOut out, int M,
                                                                    int N, int K, GemmGates gt) {
   constexpr int MI = BM / 64, NJ = BN / 64;
   constexpr int kStage = (BM + BN) * 128;  // bytes per stage: 64 KiB at 256 x 256
@@ -335,7 +349,7 @@ __global__ __launch_bounds__(kGemmThreads, kMinWG) void gemm_tn_kernel(const uin
     step(st1, st0, s + 1);
   }
   if (s < nk) step(st0, st1, s);  // the last step when nk is odd
-  gemm_store<BM, BN>(acc, C, ldc, M, N, m0, n0, wave, lane, gt, nk % 2 ? st0 : st1);
+  gemm_store<BM, BN>(acc, out, M, N, m0, n0, wave, lane, gt, nk % 2 ? st0 : st1);
 }
 
 // ---- small M (decode batches): a deeper load pipeline ----
@@ -353,7 +367,7 @@ __global__ __launch_bounds__(kGemmThreads, kMinWG) void gemm_tn_kernel(const uin
 template <int BN, int NS>
 __global__ __launch_bounds__(kGemmThreads, 2) void gemm_tn_deep_kernel(const uint16_t* __restrict__ A, int64_t lda,
                                                                     const uint16_t* __restrict__ B, int64_t ldb,
-                                                                    uint16_t* __restrict__ C, int64_t ldc, int M,
+                                                                    GemmOut out, int M,
                                                                     int N, int K, GemmGates gt) {
   static_assert(NS == 3 || NS == 4, "three or four stages");
   constexpr int BM = 64, MI = 1, NJ = BN / 64;
@@ -470,26 +484,17 @@ __global__ __launch_bounds__(kGemmThreads, 2) void gemm_tn_deep_kernel(const uin
   // the repeated loads land before a stage is reused as the gates' scratch
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  gemm_store<BM, BN>(acc, C, ldc, M, N, m0, n0, wave, lane, gt, st0);
+  gemm_store<BM, BN>(acc, out, M, N, m0, n0, wave, lane, gt, st0);
 }
 
 }  // namespace
 
-extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, uint16_t* C,
-                             int64_t ldc, int M, int N, int K, float* g, uint16_t* beta, const void* A_log,
-                             const void* dt_bias, int param_is_fp32, int gate_col, int Hv, void* stream) {
-  if (M < 0 || N < 0 || K < 0) return GDN_ERR_INVALID_ARG;
-  if (M == 0 || N == 0) return GDN_OK;
-  if (!A || !B || !C) return GDN_ERR_INVALID_ARG;
-  // K in steps of 64; 16-byte row pieces of A, B and C; 32-bit buffer offsets
-  // (C rows whose stride is not a multiple of 8 go out element by element)
-  if (K % kBK || K == 0 || lda % 8 || ldb % 8 || lda < K || ldb < K || ldc < N ||
-      reinterpret_cast<uintptr_t>(A) % 16 || reinterpret_cast<uintptr_t>(B) % 16 ||
-      reinterpret_cast<uintptr_t>(C) % (ldc % 8 ? 2 : 16) || static_cast<int64_t>(M) * lda * 2 >= (1LL << 31) ||
-      static_cast<int64_t>(N) * ldb * 2 >= (1LL << 31))
-    return GDN_ERR_INVALID_ARG;
-  if (g && (!beta || !A_log || !dt_bias || Hv <= 0 || gate_col < 0 || gate_col + 2 * Hv > N)) return GDN_ERR_INVALID_ARG;
-  const GemmGates gt{g, beta, A_log, dt_bias, param_is_fp32 ? 1 : 0, gate_col, Hv};
+namespace {
+
+// Tile choice and launch for C = A B^T into `out` (arguments checked by the
+// entry points).
+int gemm_launch(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, const GemmOut& out, int M, int N,
+                int K, const GemmGates& gt, void* stream) {
   // Tile: 256 x 256 with one workgroup per CU, so a launch runs in
   // ceil(tiles / CUs) waves of tiles, each taking time in proportion to the
   // tile's rows.  192 x 256 is taken when its waves x rows is smaller (a
@@ -513,16 +518,84 @@ extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, 
   // (1000 x 2080 x 512: 6.5 -> 7.0 us).
   const bool deep = K / kBK >= 16;
   if (cfg == 3 && deep)
-    gemm_tn_deep_kernel<64, 4><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+    gemm_tn_deep_kernel<64, 4><<<g3, b3, 0, st>>>(A, lda, B, ldb, out, M, N, K, gt);
   else if (cfg == 3)
-    gemm_tn_kernel<64, 64, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+    gemm_tn_kernel<64, 64, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, out, M, N, K, gt);
   else if (cfg == 2 && deep)
-    gemm_tn_deep_kernel<128, 3><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+    gemm_tn_deep_kernel<128, 3><<<g3, b3, 0, st>>>(A, lda, B, ldb, out, M, N, K, gt);
   else if (cfg == 2)
-    gemm_tn_kernel<64, 128, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+    gemm_tn_kernel<64, 128, 2><<<g3, b3, 0, st>>>(A, lda, B, ldb, out, M, N, K, gt);
   else if (cfg == 1)
-    gemm_tn_kernel<192, 256, 1><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+    gemm_tn_kernel<192, 256, 1><<<g3, b3, 0, st>>>(A, lda, B, ldb, out, M, N, K, gt);
   else
-    gemm_tn_kernel<256, 256, 1><<<g3, b3, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K, gt);
+    gemm_tn_kernel<256, 256, 1><<<g3, b3, 0, st>>>(A, lda, B, ldb, out, M, N, K, gt);
   return gdn_launch_status();
+}
+
+// The checks both entry points share: K in steps of 64; 16-byte row pieces
+// of A and B; 32-bit buffer offsets; the gate outputs' arguments.
+int gemm_check(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, int M, int N, int K, float* g,
+               uint16_t* beta, const void* A_log, const void* dt_bias, int gate_col, int Hv) {
+  if (K % kBK || K == 0 || lda % 8 || ldb % 8 || lda < K || ldb < K || reinterpret_cast<uintptr_t>(A) % 16 ||
+      reinterpret_cast<uintptr_t>(B) % 16 || static_cast<int64_t>(M) * lda * 2 >= (1LL << 31) ||
+      static_cast<int64_t>(N) * ldb * 2 >= (1LL << 31))
+    return GDN_ERR_INVALID_ARG;
+  if (g && (!beta || !A_log || !dt_bias || Hv <= 0 || gate_col < 0 || gate_col + 2 * Hv > N)) return GDN_ERR_INVALID_ARG;
+  return GDN_OK;
+}
+
+// One output part: rows of ld elements at c (16-byte stores when ld is a
+// multiple of 8 and c 16-byte aligned, else element by element: c then only
+// 2-byte aligned).
+bool part_ok(const uint16_t* c, int64_t ld, int width) {
+  return c && ld >= width && reinterpret_cast<uintptr_t>(c) % (ld % 8 ? 2 : 16) == 0;
+}
+
+}  // namespace
+
+extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, uint16_t* C,
+                             int64_t ldc, int M, int N, int K, float* g, uint16_t* beta, const void* A_log,
+                             const void* dt_bias, int param_is_fp32, int gate_col, int Hv, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return GDN_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return GDN_OK;
+  if (!A || !B || !C) return GDN_ERR_INVALID_ARG;
+  const int st = gemm_check(A, lda, B, ldb, M, N, K, g, beta, A_log, dt_bias, gate_col, Hv);
+  if (st != GDN_OK) return st;
+  if (!part_ok(C, ldc, N)) return GDN_ERR_INVALID_ARG;
+  const int v = ldc % 8 == 0;
+  const GemmOut out{{C, C, C}, {ldc, ldc, ldc}, {N, N, N}, {v, v, v}};
+  const GemmGates gt{g, beta, A_log, dt_bias, param_is_fp32 ? 1 : 0, gate_col, Hv};
+  return gemm_launch(A, lda, B, ldb, out, M, N, K, gt, stream);
+}
+
+extern "C" int gdn_gemm_bf16_cols(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, int M, int N, int K,
+                                  int n_parts, uint16_t* const* C, const int64_t* ldc, const int* col_end, float* g,
+                                  uint16_t* beta, const void* A_log, const void* dt_bias, int param_is_fp32,
+                                  int gate_col, int Hv, void* stream) {
+  if (M < 0 || N < 0 || K < 0 || n_parts < 1 || n_parts > 3 || !C || !ldc || !col_end) return GDN_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return GDN_OK;
+  if (!A || !B) return GDN_ERR_INVALID_ARG;
+  const int st = gemm_check(A, lda, B, ldb, M, N, K, g, beta, A_log, dt_bias, gate_col, Hv);
+  if (st != GDN_OK) return st;
+  GemmOut out{};
+  int beg = 0;
+  for (int s = 0; s < 3; ++s) {
+    const int e = s < n_parts ? col_end[s] : N;
+    if (s < n_parts) {
+      // increasing boundaries at multiples of 32, the last one at N
+      if (e <= beg || (s + 1 < n_parts ? e % 32 != 0 || e >= N : e != N)) return GDN_ERR_INVALID_ARG;
+      if (!part_ok(C[s], ldc[s], e - beg)) return GDN_ERR_INVALID_ARG;
+      out.c[s] = C[s];
+      out.ld[s] = ldc[s];
+      out.vec[s] = ldc[s] % 8 == 0;
+    } else {
+      out.c[s] = out.c[n_parts - 1];
+      out.ld[s] = out.ld[n_parts - 1];
+      out.vec[s] = out.vec[n_parts - 1];
+    }
+    out.end[s] = e;
+    beg = e;
+  }
+  const GemmGates gt{g, beta, A_log, dt_bias, param_is_fp32 ? 1 : 0, gate_col, Hv};
+  return gemm_launch(A, lda, B, ldb, out, M, N, K, gt, stream);
 }

@@ -9,6 +9,7 @@ CPU or eager fallback: a CPU tensor or a missing library raises.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 
 import torch
@@ -834,6 +835,57 @@ def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = Non
               int(a_log is not None and a_log.dtype == torch.float32), gate_col, Hv, _stream(dev))
     y = y.view(*x.shape[:-1], N) if out is None else y
     return y if gates is None else (y, g, beta)
+
+
+def linear_cols(x: torch.Tensor, weight: torch.Tensor, widths: list[int],
+                gates: dict | None = None):
+    """linear(x, weight) with the output's columns split into len(widths)
+    (1-3) contiguous tensors [M, widths[s]] (sum(widths) == weight rows;
+    every boundary a multiple of 32): the same values as linear's columns.
+    For the GDN layer's in_proj over its four concatenated weights, so that
+    the qkv, z and b | a parts come out as tensors of their own, as the
+    reference's separate projections produce them
+    (nanovllm/models/qwen3_5.py:929-939).  gates: as in linear (gate_col
+    counts the concatenated columns).  Returns the list of parts, and with
+    gates (parts, g, beta)."""
+    dev = _check_cuda(x, weight)
+    _bf16(x, "x")
+    _bf16(weight, "weight")
+    K = x.shape[-1]
+    N = weight.shape[0]
+    assert weight.shape[1] == K and sum(widths) == N and 1 <= len(widths) <= 3
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    w = weight if (weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0) \
+        else weight.contiguous()
+    M = x2.shape[0]
+    parts = [torch.empty(M, wd, dtype=torch.bfloat16, device=x.device) for wd in widths]
+    ends, e = [], 0
+    for wd in widths:
+        e += wd
+        ends.append(e)
+    n = len(widths)
+    c_arr = (ctypes.c_void_p * n)(*[p.data_ptr() for p in parts])
+    ld_arr = (ctypes.c_int64 * n)(*[p.stride(0) for p in parts])
+    end_arr = (ctypes.c_int * n)(*ends)
+    g = beta = None
+    a_log = dt_bias = None
+    gate_col = Hv = 0
+    if gates is not None:
+        a_log, dt_bias = gates["A_log"], gates["dt_bias"]
+        if a_log.dtype != dt_bias.dtype or a_log.dtype not in (torch.bfloat16, torch.float32):
+            a_log, dt_bias = a_log.float(), dt_bias.float()
+        a_log, dt_bias = a_log.contiguous(), dt_bias.contiguous()
+        Hv = a_log.numel()
+        gate_col = int(gates["gate_col"])
+        g = torch.empty(M, Hv, dtype=torch.float32, device=x.device)
+        beta = torch.empty(M, Hv, dtype=torch.bfloat16, device=x.device)
+    _lib.call("gdn_gemm_bf16_cols", _lib.ptr(x2), x2.stride(0), _lib.ptr(w), w.stride(0), M, N, K, n, c_arr,
+              ld_arr, end_arr, _lib.ptr(g), _lib.ptr(beta), _lib.ptr(a_log), _lib.ptr(dt_bias),
+              int(a_log is not None and a_log.dtype == torch.float32), gate_col, Hv, _stream(dev))
+    parts = [p.view(*x.shape[:-1], p.shape[1]) for p in parts]
+    return parts if gates is None else (parts, g, beta)
 
 
 # -------------------------------------------------------------- gated norm --
