@@ -360,16 +360,16 @@ int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb
                   int gate_col, int Hv, void* stream);
 
 /*
- * gdn_gemm_bf16 with C's columns written to up to three separate tensors: part
- * s (of n_parts, 1..3) holds columns [col_end[s - 1], col_end[s]) (from 0) at
- * C[s], row stride ldc[s]; col_end increasing, multiples of 32 except the last,
+ * gdn_gemm_bf16 with C's columns written to up to four separate tensors: part
+ * s (of n_parts, 1..4) holds columns [col_end[s - 1], col_end[s]) (from 0) at
+ * C[s], row stride ldc[s]; col_end increasing, multiples of 16 except the last,
  * which is N.  The same values as one C of N columns.  For the GDN layer's
  * in_proj over the four concatenated weights (the call sites of
  * nanovllm/models/qwen3_5.py:929-939, whose four projections each produce a
- * tensor of their own): qkv, z and the b | a columns come out as separate
- * contiguous tensors, whose rows the prefill and the gated norm read faster
- * than strided columns of one [M, N] buffer.  Gate outputs as in
- * gdn_gemm_bf16 (gate_col counts C's columns).
+ * tensor of their own): qkv, z, b and a come out as separate contiguous
+ * tensors, whose rows the prefill and the gated norm read faster than strided
+ * columns of one [M, N] buffer, and which the gate readers take without a
+ * copy.  Gate outputs as in gdn_gemm_bf16 (gate_col counts C's columns).
  */
 int gdn_gemm_bf16_cols(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, int M, int N, int K,
                        int n_parts, uint16_t* const* C, const int64_t* ldc, const int* col_end, float* g,

@@ -57,15 +57,17 @@ constexpr int kCUs = gdn::kNumCu;
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// The output: C's columns in up to three parts, part s holding columns
+// The output: C's columns in up to four parts, part s holding columns
 // [end[s - 1], end[s]) (end[-1] = 0) at c[s] with row stride ld[s]; vec[s]: its
-// rows take 16-byte stores.  Every part boundary is a multiple of 32, so each
-// 32-column block of a tile lies in one part.
+// rows take 16-byte stores.  Every part boundary is a multiple of 16, so each
+// 16-column half of a 32-column block (one store pair of every lane) lies in
+// one part, and the part is the same for the whole wave.
+constexpr int kMaxParts = 4;
 struct GemmOut {
-  uint16_t* c[3];
-  int64_t ld[3];
-  int end[3];
-  int vec[3];
+  uint16_t* c[kMaxParts];
+  int64_t ld[kMaxParts];
+  int end[kMaxParts];
+  int vec[kMaxParts];
 };
 
 struct GemmGates {
@@ -138,13 +140,28 @@ __device__ __forceinline__ void gemm_store(const f32x16_t (&acc)[BM / 64][BN / 6
     for (int j = 0; j < NJ; ++j) {
       const int cb = n0 + (BN / 2) * wn + 32 * j;  // wave-uniform
       if (cb >= N) continue;
-      // the output part of this 32-column block (wave-uniform)
-      const int s = cb < out.end[0] ? 0 : cb < out.end[1] ? 1 : 2;
-      const int cbeg = s == 0 ? 0 : out.end[s - 1], cend = out.end[s];
-      const bool vec = out.vec[s] != 0;
-      uint16_t* crow = out.c[s] + static_cast<int64_t>(row_ok ? m : 0) * out.ld[s] - cbeg;
+      // the output part of this block's first 16 columns (wave-uniform;
+      // selects with constant indices, so the part table stays in scalar
+      // registers)
+      int s = cb < out.end[0] ? 0 : cb < out.end[1] ? 1 : cb < out.end[2] ? 2 : 3;
+      auto pick = [&s](auto a0, auto a1, auto a2, auto a3) { return s == 0 ? a0 : s == 1 ? a1 : s == 2 ? a2 : a3; };
+      int cbeg = pick(0, out.end[0], out.end[1], out.end[2]);
+      int cend = pick(out.end[0], out.end[1], out.end[2], out.end[3]);
+      bool vec = pick(out.vec[0], out.vec[1], out.vec[2], out.vec[3]) != 0;
+      uint16_t* crow = pick(out.c[0], out.c[1], out.c[2], out.c[3]) +
+                       static_cast<int64_t>(row_ok ? m : 0) * pick(out.ld[0], out.ld[1], out.ld[2], out.ld[3]) - cbeg;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
+        if (p == 1 && cend == cb + 16 && cend < N) {
+          // the second 16 columns open the next part (a boundary inside the
+          // block: rare)
+          ++s;
+          cbeg = cend;
+          cend = pick(out.end[0], out.end[1], out.end[2], out.end[3]);
+          vec = pick(out.vec[0], out.vec[1], out.vec[2], out.vec[3]) != 0;
+          crow = pick(out.c[0], out.c[1], out.c[2], out.c[3]) +
+                 static_cast<int64_t>(row_ok ? m : 0) * pick(out.ld[0], out.ld[1], out.ld[2], out.ld[3]) - cbeg;
+        }
         const int q = 2 * p;
         const auto lo = __builtin_amdgcn_permlane32_swap(gdn::f2bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
                                                          gdn::f2bf2(acc[i][j][4 * q + 4], acc[i][j][4 * q + 5]),
@@ -563,7 +580,7 @@ extern "C" int gdn_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* B, 
   if (st != GDN_OK) return st;
   if (!part_ok(C, ldc, N)) return GDN_ERR_INVALID_ARG;
   const int v = ldc % 8 == 0;
-  const GemmOut out{{C, C, C}, {ldc, ldc, ldc}, {N, N, N}, {v, v, v}};
+  const GemmOut out{{C, C, C, C}, {ldc, ldc, ldc, ldc}, {N, N, N, N}, {v, v, v, v}};
   const GemmGates gt{g, beta, A_log, dt_bias, param_is_fp32 ? 1 : 0, gate_col, Hv};
   return gemm_launch(A, lda, B, ldb, out, M, N, K, gt, stream);
 }
@@ -572,18 +589,19 @@ extern "C" int gdn_gemm_bf16_cols(const uint16_t* A, int64_t lda, const uint16_t
                                   int n_parts, uint16_t* const* C, const int64_t* ldc, const int* col_end, float* g,
                                   uint16_t* beta, const void* A_log, const void* dt_bias, int param_is_fp32,
                                   int gate_col, int Hv, void* stream) {
-  if (M < 0 || N < 0 || K < 0 || n_parts < 1 || n_parts > 3 || !C || !ldc || !col_end) return GDN_ERR_INVALID_ARG;
+  if (M < 0 || N < 0 || K < 0 || n_parts < 1 || n_parts > kMaxParts || !C || !ldc || !col_end)
+    return GDN_ERR_INVALID_ARG;
   if (M == 0 || N == 0) return GDN_OK;
   if (!A || !B) return GDN_ERR_INVALID_ARG;
   const int st = gemm_check(A, lda, B, ldb, M, N, K, g, beta, A_log, dt_bias, gate_col, Hv);
   if (st != GDN_OK) return st;
   GemmOut out{};
   int beg = 0;
-  for (int s = 0; s < 3; ++s) {
+  for (int s = 0; s < kMaxParts; ++s) {
     const int e = s < n_parts ? col_end[s] : N;
     if (s < n_parts) {
-      // increasing boundaries at multiples of 32, the last one at N
-      if (e <= beg || (s + 1 < n_parts ? e % 32 != 0 || e >= N : e != N)) return GDN_ERR_INVALID_ARG;
+      // increasing boundaries at multiples of 16, the last one at N
+      if (e <= beg || (s + 1 < n_parts ? e % 16 != 0 || e >= N : e != N)) return GDN_ERR_INVALID_ARG;
       if (!part_ok(C[s], ldc[s], e - beg)) return GDN_ERR_INVALID_ARG;
       out.c[s] = C[s];
       out.ld[s] = ldc[s];

@@ -497,25 +497,25 @@ class GatedDeltaNetLayer:
 
     def project_in(self, hidden, gates: bool = False):
         """hidden [N, hidden] -> (mixed, z, b, a): one GEMM over the four
-        concatenated weights whose output goes to three tensors, mixed [N, C]
-        and z [N, Hv*D] contiguous and b, a as the halves of one [N, 2 Hv]
-        (rows of contiguous tensors read faster than columns of one wide
-        buffer); with gates, also (g, beta) of the b and a columns from the
-        GEMM's epilogue (bit-equal to the gate kernel on them,
-        qwen3_5.py:933-934), else None."""
+        concatenated weights whose output goes to four contiguous tensors,
+        mixed [N, C], z [N, Hv*D], b and a [N, Hv] (rows of contiguous tensors
+        read faster than columns of one wide buffer, and the gate readers take
+        them without a copy); with gates, also (g, beta) of the b and a
+        columns from the GEMM's epilogue (bit-equal to the gate kernel on
+        them, qwen3_5.py:933-934), else None."""
         c = self.core
         C, V, Hv = c.conv_dim, c.value_dim, c.Hv
-        widths = [C, V, 2 * Hv]
+        widths = [C, V, Hv, Hv]
         with self._timed("in_proj"):
-            if all(w % 32 == 0 for w in widths[:-1]):
+            if all(w % 16 == 0 for w in widths[:-1]):
                 if gates:
-                    (mixed, z, ba), g, beta = ops.linear_cols(hidden, self.w_in, widths,
-                                                              gates={"gate_col": C + V, "A_log": c.A_log,
-                                                                     "dt_bias": c.dt_bias})
+                    (mixed, z, b, a), g, beta = ops.linear_cols(hidden, self.w_in, widths,
+                                                                gates={"gate_col": C + V, "A_log": c.A_log,
+                                                                       "dt_bias": c.dt_bias})
                     gb = (g, beta)
                 else:
-                    (mixed, z, ba), gb = ops.linear_cols(hidden, self.w_in, widths), None
-                return mixed, z, ba[:, :Hv], ba[:, Hv:], gb
+                    (mixed, z, b, a), gb = ops.linear_cols(hidden, self.w_in, widths), None
+                return mixed, z, b, a, gb
             if gates:
                 y, g, beta = ops.linear(hidden, self.w_in, gates={"gate_col": C + V, "A_log": c.A_log,
                                                                   "dt_bias": c.dt_bias})

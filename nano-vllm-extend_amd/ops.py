@@ -840,10 +840,10 @@ def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = Non
 def linear_cols(x: torch.Tensor, weight: torch.Tensor, widths: list[int],
                 gates: dict | None = None):
     """linear(x, weight) with the output's columns split into len(widths)
-    (1-3) contiguous tensors [M, widths[s]] (sum(widths) == weight rows;
-    every boundary a multiple of 32): the same values as linear's columns.
+    (1-4) contiguous tensors [M, widths[s]] (sum(widths) == weight rows;
+    every boundary a multiple of 16): the same values as linear's columns.
     For the GDN layer's in_proj over its four concatenated weights, so that
-    the qkv, z and b | a parts come out as tensors of their own, as the
+    the qkv, z, b and a parts come out as tensors of their own, as the
     reference's separate projections produce them
     (nanovllm/models/qwen3_5.py:929-939).  gates: as in linear (gate_col
     counts the concatenated columns).  Returns the list of parts, and with
@@ -853,7 +853,7 @@ def linear_cols(x: torch.Tensor, weight: torch.Tensor, widths: list[int],
     _bf16(weight, "weight")
     K = x.shape[-1]
     N = weight.shape[0]
-    assert weight.shape[1] == K and sum(widths) == N and 1 <= len(widths) <= 3
+    assert weight.shape[1] == K and sum(widths) == N and 1 <= len(widths) <= 4
     x2 = x.reshape(-1, K)
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = x2.contiguous()

@@ -96,10 +96,17 @@ def test_in_proj_with_gate_epilogue(pkg, dev, M):
     assert torch.equal(g, g2) and torch.equal(beta.view(torch.int16), beta2.view(torch.int16))
 
 
-@pytest.mark.parametrize("M", [64, 100, 777, 1790])
+def _layouts(C, V, Hv):
+    # (the layer's three- and four-part in_proj; boundaries off the 32-column
+    # grid, where one 32-column block's pieces go to two parts)
+    return {"3": [C, V, 2 * Hv], "4": [C, V, Hv, Hv], "16": [48, C - 48, V + 16, 2 * Hv - 16]}
+
+
+@pytest.mark.parametrize("layout", ["3", "4", "16"])
 @pytest.mark.parametrize("with_gates", [False, True])
-def test_in_proj_column_parts_equal_one_output(pkg, dev, M, with_gates):
-    """gdn_gemm_bf16_cols (the layer's in_proj into separate qkv, z and b | a
+@pytest.mark.parametrize("M", [64, 100, 777, 1790])
+def test_in_proj_column_parts_equal_one_output(pkg, dev, M, with_gates, layout):
+    """gdn_gemm_bf16_cols (the layer's in_proj into separate qkv, z, b and a
     tensors): every part bit-equal to the same columns of the one-output GEMM,
     and the gate outputs too, for each tile shape (M = 64: 64 x 64 tiles with
     the deeper pipeline, 100: 64 x 128, 777: 192 x 256, 1790: 256 x 256)."""
@@ -114,39 +121,45 @@ def test_in_proj_column_parts_equal_one_output(pkg, dev, M, with_gates):
     A_log = (torch.rand(Hv, generator=gen) * math.log(16)).to(BF16).to(dev)
     dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(BF16).to(dev)
     gates = {"gate_col": C + V, "A_log": A_log, "dt_bias": dt_bias} if with_gates else None
+    widths = _layouts(C, V, Hv)[layout]
     one = pkg.ops.linear(x, w, gates=gates)
-    parts = pkg.ops.linear_cols(x, w, [C, V, 2 * Hv], gates=gates)
+    parts = pkg.ops.linear_cols(x, w, widths, gates=gates)
     torch.cuda.synchronize()
     if with_gates:
         (y, g, beta), (ps, g2, beta2) = one, parts
         assert torch.equal(g, g2) and torch.equal(beta.view(torch.int16), beta2.view(torch.int16))
     else:
         y, ps = one, parts
-    for p, c0, c1 in zip(ps, (0, C, C + V), (C, C + V, N)):
-        assert p.is_contiguous() and p.shape == (M, c1 - c0)
-        assert torch.equal(p.view(torch.int16), y[:, c0:c1].contiguous().view(torch.int16)), (c0, c1)
+    c0 = 0
+    for p, wd in zip(ps, widths):
+        assert p.is_contiguous() and p.shape == (M, wd)
+        assert torch.equal(p.view(torch.int16), y[:, c0:c0 + wd].contiguous().view(torch.int16)), (c0, wd)
+        c0 += wd
 
 
 def test_column_parts_rejected_shapes(pkg, dev):
-    """Part boundaries off the 32-column grid, out of order, or a last
-    boundary other than N are rejected before any launch.  Real (small)
-    buffers, each part's wide enough for every column, so even a launch that
-    the checks had wrongly let through would stay in bounds."""
+    """Part boundaries off the 16-column grid, out of order, a last boundary
+    other than N, or more than four parts are rejected before any launch.
+    Real (small) buffers, each part's wide enough for every column, so even a
+    launch that the checks had wrongly let through would stay in bounds."""
     import ctypes
     lib = pkg._lib.load()
     _lib = pkg._lib
     M, N, K = 4, 96, 64
     a = torch.zeros(M, K, dtype=BF16, device=dev)
     b = torch.zeros(N, K, dtype=BF16, device=dev)
-    outs = [torch.zeros(M, 128, dtype=BF16, device=dev) for _ in range(2)]
-    c = (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs])
-    ld = (ctypes.c_int64 * 2)(128, 128)
+    outs = [torch.zeros(M, 128, dtype=BF16, device=dev) for _ in range(5)]
+    c = (ctypes.c_void_p * 5)(*[o.data_ptr() for o in outs])
+    ld = (ctypes.c_int64 * 5)(*([128] * 5))
     stream = torch.cuda.current_stream(dev).cuda_stream
-    for ends in ((48, 96), (64, 100), (96, 64), (64, 64)):
-        e = (ctypes.c_int * 2)(*ends)
-        assert lib.gdn_gemm_bf16_cols(a.data_ptr(), K, b.data_ptr(), K, M, N, K, 2, c, ld, e, None, None, None, None,
-                                      0, 0, 0, stream) == _lib.GDN_ERR_INVALID_ARG, ends
-    e = (ctypes.c_int * 2)(64, 96)
-    assert lib.gdn_gemm_bf16_cols(a.data_ptr(), K, b.data_ptr(), K, M, N, K, 2, c, ld, e, None, None, None, None,
-                                  0, 0, 0, stream) == _lib.GDN_OK
+
+    def call(ends):
+        e = (ctypes.c_int * len(ends))(*ends)
+        return lib.gdn_gemm_bf16_cols(a.data_ptr(), K, b.data_ptr(), K, M, N, K, len(ends), c, ld, e, None, None,
+                                      None, None, 0, 0, 0, stream)
+
+    for ends in ((40, 96), (64, 100), (96, 64), (64, 64), (16, 32, 48, 64, 96), (8, 48, 64, 96)):
+        assert call(ends) == _lib.GDN_ERR_INVALID_ARG, ends
+    for ends in ((64, 96), (16, 48, 64, 96)):
+        assert call(ends) == _lib.GDN_OK, ends
     torch.cuda.synchronize()
