@@ -6,7 +6,8 @@ without host offsets.  Each case is held to the three separate calls
 (fused_g_beta -> causal_conv_silu_varlen_parts -> chunk_gated_delta_rule_varlen)
 bit for bit, outputs and both pools, and to the CPU oracle's prefill chain
 (nanovllm/models/qwen3_5.py:922-961) at the suite's output and state bars.
-The fused decode step likewise (test_random_shape_decode)."""
+The fused decode step likewise (test_random_shape_decode), and long sequences
+cut into segments (test_random_shape_segments)."""
 import pytest
 import torch
 
@@ -175,3 +176,65 @@ def test_random_shape_decode(pkg, dev, i):
         assert torch.equal(res[2].cpu().view(torch.int16), rpool.view(torch.int16)), f"{name}: conv pool vs oracle"
         if z is None:
             assert_out(res[0].cpu(), ro.reshape(B, Hv, D).to(BF16), f"case {i} {name} output")
+
+
+def _draw_segments(i):
+    gen = torch.Generator().manual_seed(3000 + i)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=gen))]
+    Hk = pick([1, 2, 4])
+    Hv = Hk * pick([1, 2])
+    D = pick([64, 128])
+    n = int(torch.randint(1, 6, (1,), generator=gen))
+    lens = [int(torch.randint(1, 400, (1,), generator=gen)) for _ in range(n)]
+    lens[int(torch.randint(n, (1,), generator=gen))] = int(torch.randint(600, 3000, (1,), generator=gen))
+    return dict(Hk=Hk, Hv=Hv, D=D, lens=lens, segs=pick([2, 3, 4, 6, 8, 12]),
+                h0=bool(torch.rand(1, generator=gen) < 0.6), fused=bool(torch.rand(1, generator=gen) < 0.5))
+
+
+@pytest.mark.parametrize("i", list(range(12)))
+def test_random_shape_segments(pkg, dev, i):
+    """Long sequences cut into segments (max_segments) at random shapes: the
+    chunk rule alone or the fused prefill, against the CPU oracle at the
+    output and state bars, and against the same call in one pass."""
+    from helpers import STATE_REL, rule_inputs, state_rel
+    c = _draw_segments(i)
+    Hk, Hv, D, lens, segs = c["Hk"], c["Hv"], c["D"], c["lens"], c["segs"]
+    print(f"random segments case {i}: {c}", flush=True)
+    N = sum(lens)
+    cu = cu_of(lens)
+    cu_h = torch.tensor(cu, dtype=torch.int64)
+    n = len(lens)
+    if not c["fused"]:
+        gen = torch.Generator().manual_seed(900 + i)
+        q, k, v, g, beta = rule_inputs(gen, N, Hk, Hv, D)
+        h0 = torch.randn(n, Hv, D, D, generator=gen) * 0.1 if c["h0"] else None
+        ro, rS = gdn_ref.chunk_varlen(q, k, v, g, beta.float(), cu, h0)
+        args = (q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), cu_h.to(dev),
+                None if h0 is None else h0.to(dev))
+        o_s, S_s = pkg.ops.chunk_gated_delta_rule_varlen(*args, cu_seqlens_cpu=cu_h, max_segments=segs)
+        o_1, S_1 = pkg.ops.chunk_gated_delta_rule_varlen(*args, cu_seqlens_cpu=cu_h, max_segments=1)
+        torch.cuda.synchronize()
+        S_s, S_1 = S_s.cpu(), S_1.cpu()
+    else:
+        slots = n + 2
+        C, mixed, conv_w, A_log, dt_bias, a, b, conv_pool, s_pool, ids = _case(950 + i, Hk, Hv, D, lens, slots)
+        if not c["h0"]:
+            s_pool.zero_()
+        g, beta = gdn_ref.g_beta(b, a, A_log, dt_bias, None)
+        y, _ = gdn_ref.conv_varlen(mixed, conv_pool[ids], conv_w, lens)
+        kd = Hk * D
+        q, k, v = y[:, :kd].reshape(N, Hk, D), y[:, kd:2 * kd].reshape(N, Hk, D), y[:, 2 * kd:].reshape(N, Hv, D)
+        ro, rS = gdn_ref.chunk_varlen(q, k, v, g, beta.float(), cu, s_pool[ids])
+        d = [t.to(dev) for t in (mixed, conv_w, A_log, dt_bias, a, b, ids)]
+        res = []
+        for ms in (segs, 1):
+            cp, sp = conv_pool.to(dev), s_pool.to(dev)
+            o = pkg.ops.conv_chunk_prefill_varlen(d[0], cp, d[1], d[5], d[4], d[2], d[3], cu_h.to(dev), sp, d[6], Hk,
+                                                  Hv, D, cu_seqlens_cpu=cu_h, max_segments=ms)
+            torch.cuda.synchronize()
+            res.append((o, sp.cpu()[ids]))
+        (o_s, S_s), (o_1, S_1) = res
+    assert_out(o_s.cpu(), ro.to(BF16), f"case {i} segmented output")
+    assert_state(S_s, rS, f"case {i} segmented state")
+    assert_out(o_s.cpu(), o_1.cpu(), f"case {i} segmented vs one pass")
+    assert state_rel(S_s, S_1) < STATE_REL
