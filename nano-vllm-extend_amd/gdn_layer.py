@@ -390,13 +390,16 @@ class GatedDeltaNetCore:
         would run the gate kernel).  Returns [N, Hv*D] bf16."""
         rows = (lambda i, j: None) if gb is None else (lambda i, j: (gb[0][i:j], gb[1][i:j]))
         N = mixed.shape[0]
-        lens = cu_seqlens_q[1:] - cu_seqlens_q[:-1]
-        bs = lens.shape[0]
         T = int(max_seqlen_q)
         if T == 1:
             return self.decode(mixed, z, b, a, ids, conv_cache, s_cache, gb=gb).view(N, self.value_dim)
+        # per-sequence lengths on the device, formed only where a path reads
+        # them (a decode step or a varlen prefill given lens_q launches nothing
+        # for them)
+        lens_dev = lambda: cu_seqlens_q[1:] - cu_seqlens_q[:-1]
+        bs = cu_seqlens_q.shape[0] - 1
         if lens_q is None:
-            lens_q = lens.tolist()
+            lens_q = lens_dev().tolist()
         n1 = 0
         while n1 < bs and lens_q[n1] == 1:
             n1 += 1
@@ -412,14 +415,15 @@ class GatedDeltaNetCore:
                 parts.append(self.prefill_varlen(mixed[off:], z[off:], b[off:], a[off:], lens_q[off:],
                                                  ids[off:], conv_cache, s_cache,
                                                  gb=rows(off, N)).view(-1, self.value_dim))
-                return torch.cat(parts, dim=0)
-            lens_p = lens[off:]
-            Tp = T if off == 0 else max(lens_q[off:])
-            parts.append(self._padded_varlen(mixed[off:], z[off:], b[off:], a[off:], lens_p, Tp, ids[off:],
-                                             conv_cache, s_cache, gb=rows(off, N)))
-            return torch.cat(parts, dim=0)
+            else:
+                lens_p = lens_dev()[off:]
+                Tp = T if off == 0 else max(lens_q[off:])
+                parts.append(self._padded_varlen(mixed[off:], z[off:], b[off:], a[off:], lens_p, Tp, ids[off:],
+                                                 conv_cache, s_cache, gb=rows(off, N)))
+            # (one part: no concatenation, which would copy the whole output)
+            return parts[0] if len(parts) == 1 else torch.cat(parts, dim=0)
         # len-1 rows that are not a contiguous prefix: one padded pass
-        return self._padded_varlen(mixed, z, b, a, lens, T, ids, conv_cache, s_cache, gb=gb)
+        return self._padded_varlen(mixed, z, b, a, lens_dev(), T, ids, conv_cache, s_cache, gb=gb)
 
     def _padded_varlen(self, mixed, z, b, a, lens, T, ids, conv_cache, s_cache, gb=None):
         n = lens.shape[0]
