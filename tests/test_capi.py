@@ -184,3 +184,32 @@ def test_stride_validation_before_launch(pkg):
     assert fdec(C, slot, 3 * C - 3) == _lib.GDN_ERR_INVALID_ARG          # conv slot stride
     assert fdec(C, slot, 3 * C, z=P, sz=Hv * D) == _lib.GDN_ERR_INVALID_ARG       # fused norm without its weight
     assert fdec(C, slot, 3 * C, z=P, sz=Hv * D - 4, nw=P) == _lib.GDN_ERR_INVALID_ARG  # gate rows too short
+
+
+def test_column_part_gemm_validation_before_launch(pkg):
+    """gdn_gemm_bf16_cols rejects part counts outside 1..4, a missing part
+    table, boundaries off the 16-column grid, out of order or not ending at N,
+    and parts narrower than their row stride allows, before any launch.  NULL
+    operands where the part checks come first; dummy (aligned, never
+    dereferenced) ones only where no GPU is visible."""
+    lib = pkg._lib.load()
+    _lib = pkg._lib
+    M, N, K = 4, 96, 64
+
+    def call(ends, lds=None, A=None, n_parts=None, table=True):
+        n = len(ends) if n_parts is None else n_parts
+        c = (ctypes.c_void_p * 5)(*([1 << 20] * 5))
+        ld = (ctypes.c_int64 * 5)(*(lds or [128] * 5))
+        e = (ctypes.c_int * 5)(*(list(ends) + [0] * (5 - len(ends))))
+        return lib.gdn_gemm_bf16_cols(A, K, A, K, M, N, K, n, c if table else None, ld, e, None, None, None, None,
+                                      0, 0, 0, None)
+
+    assert call((96,), n_parts=0) == _lib.GDN_ERR_INVALID_ARG
+    assert call((16, 32, 48, 64, 96)) == _lib.GDN_ERR_INVALID_ARG                 # five parts
+    assert call((96,), table=False) == _lib.GDN_ERR_INVALID_ARG
+    if torch.cuda.device_count() > 0:
+        pytest.skip("dummy device addresses are passed only where no GPU is visible")
+    P = ctypes.c_void_p(1 << 20)
+    for ends in ((40, 96), (64, 100), (96, 64), (64, 64), (8, 48, 64, 96)):
+        assert call(ends, A=P) == _lib.GDN_ERR_INVALID_ARG, ends
+    assert call((64, 96), lds=[32, 128, 128, 128, 128], A=P) == _lib.GDN_ERR_INVALID_ARG   # ld < part width
