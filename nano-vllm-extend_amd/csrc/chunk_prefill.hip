@@ -14,7 +14,8 @@
 //   chunk_prep_kernel: one workgroup per (chunk, key head), all chunks in
 //     parallel, writing one record per value head.  Everything that needs only the chunk's own q, k, g, beta:
 //     the row norms, K K^T, Q K^T, the triangular inverse T (fp32), and it
-//     writes a 57 KiB record: -T' = -T diag(beta e^G / |k|), T'' = T diag(beta),
+//     writes a 51 KiB record: T'' = T diag(beta) with the column scale cT
+//     that makes it -T' = -T diag(beta e^G / |k|),
 //     A and A's fp16 rounding residual as fp16 tiles, the per-token scales,
 //     and the q rows and K^T as fp16 operand fragments.  The fused variant first computes the gates
 //     and the conv1d + SiLU of the chunk's q and k channels from the raw rows.
@@ -137,26 +138,29 @@ __device__ __forceinline__ void wave_sync() {
 // 64 lanes x 16 bytes (8 fp16), lane = row % 32 + 32 * (8-column half of its
 // 16-column k-step), so a wave moves one fragment as one contiguous KiB.
 // Token columns are in position order (position p holds token qswap(p)).
-//   TW  [6] frags      -T' = -T diag(beta e^G / ||k||), block-lower-triangular
-//                      64x64: fragment j = (row tile 0, k-steps 0..1),
-//                      (row tile 1, k-steps 0..3)
-//   TB  [6] frags      T'' = T diag(beta), same order
+//   TB  [6] frags      T'' = T diag(beta), block-lower-triangular 64x64:
+//                      fragment j = (row tile 0, k-steps 0..1), (row tile 1,
+//                      k-steps 0..3)
 //   AQ  [6] frags      A = lower_incl(scale q^.k^ e^{G_t - G_s}), same order
 //   AL  [6] frags      the rounding residual of A: fp16(A_fp32 - fp32(AQ)), same
 //                      order, so that A_fp32 = AQ + AL to ~22 significant bits
 //   VEC fp32 [256]     cQ[64] = scale e^{G_t} / ||q_t||,
 //                      cK[64] = e^{gamma - G_t} / ||k_t|| (0 past the sequence end),
-//                      e^gamma
+//                      e^gamma, and at 192: cT[64] = -e^{G_t} / ||k_t|| (0 past
+//                      the sequence end), the column scale that turns T'' into
+//                      -T' = -T diag(beta e^G / ||k||) = T'' diag(cT) (the K waves)
 //   QP  [2][D/16]      Q' = diag(cQ) q: [token tile][key step]
 //   KT  [D/32][4]      K^T, rows in position order (row p holds key qswap(p)):
 //                      [key tile][token step]
+// (-T' itself is not stored: the record is the state kernel's main HBM read
+// and the prep kernel's main write, and 6 KiB less of it is ~5 % less time.)
 struct Rec {
-  static constexpr int TW = 0;
-  static constexpr int TB = 6144;
-  static constexpr int AQ = 12288;
-  static constexpr int AL = 18432;
-  static constexpr int VEC = 24576;
-  static constexpr int QP = 25600;
+  static constexpr int TB = 0;
+  static constexpr int AQ = 6144;
+  static constexpr int AL = 12288;
+  static constexpr int VEC = 18432;
+  static constexpr int QP = 19456;
+  static constexpr int CT = 3 * kC;  // float offset of cT in VEC
 };
 __host__ __device__ constexpr int64_t rec_kt(int D) { return Rec::QP + 128LL * D; }
 // bytes of one record (a multiple of 256)
@@ -284,7 +288,7 @@ struct __align__(16) PrepSmem {
   } u;
   float Lp[10][16][kTileLd];      // lower tiles of L
   float Td[4][16][kTileLd];       // diagonal tiles of T = (I + L)^-1
-  float G[kC], bt[kC], rk[kC], rq[kC], ssk[kC], ssq[kC], cw[kC], cq[kC];
+  float G[kC], bt[kC], rk[kC], rq[kC], ssk[kC], ssq[kC], cq[kC];
 };
 
 // 16x16 tile (mt, nt) of T, nt <= mt
@@ -672,12 +676,12 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
     const float Gl = sm.G[kC - 1];
     sm.rk[t] = rk;
     sm.rq[t] = rq;
-    sm.cw[t] = -(sm.bt[t] * rk * expf(Gt));  // -T' is what the record holds
     const float cqv = rq * scale * expf(Gt);
     sm.cq[t] = cqv;
     float* vec = reinterpret_cast<float*>(rec + Rec::VEC);
     vec[t] = cqv;
     vec[kC + t] = rk * expf(Gl - Gt);
+    vec[Rec::CT + t] = -(rk * expf(Gt));
     if (t == 0) vec[2 * kC] = expf(Gl);
   }
   __syncthreads();
@@ -848,21 +852,19 @@ __global__ __launch_bounds__(256, 4) void chunk_prep_kernel(
   }
   __syncthreads();
 
-  // ---- -T' = -T diag(beta e^G / ||k||), T'' = T diag(beta): fp16 granules of 8
-  //      column positions (two token quads each) ----
-  for (int e = tid; e < 2 * kC * 8; e += NT) {
-    const int which = e >> 9;  // 0: -T', 1: T''
+  // ---- T'' = T diag(beta): fp16 granules of 8 column positions (two token
+  //      quads each) ----
+  for (int e = tid; e < kC * 8; e += NT) {
     const int t = (e >> 3) & 63, gp = e & 7;
     if ((gp >> 2) > (t >> 5)) continue;  // above the diagonal blocks: not stored
-    const float* c = which ? sm.bt : sm.cw;
-    const float4 a = t_quad(sm, c, t, quad_of_pos(2 * gp));
-    const float4 b = t_quad(sm, c, t, quad_of_pos(2 * gp + 1));
+    const float4 a = t_quad(sm, sm.bt, t, quad_of_pos(2 * gp));
+    const float4 b = t_quad(sm, sm.bt, t, quad_of_pos(2 * gp + 1));
     uint4 pk;
     pk.x = f2h2(a.x, a.y);
     pk.y = f2h2(a.z, a.w);
     pk.z = f2h2(b.x, b.y);
     pk.w = f2h2(b.z, b.w);
-    *reinterpret_cast<uint4*>(rec + (which ? Rec::TB : Rec::TW) + tri_frag_byte(t, 8 * gp)) = pk;
+    *reinterpret_cast<uint4*>(rec + Rec::TB + tri_frag_byte(t, 8 * gp)) = pk;
   }
   // the T tiles and gates are read before the next value head's K rows and
   // gates overwrite them
@@ -937,8 +939,7 @@ template <int D>
 struct KPrefetch {
   static constexpr int NKT = D / 64;  // key tiles per K wave: pk, pk + 2
   s16x8_t k[NKT][4];                  // K^T fragments: key tile pk + 2u, token step
-  s16x8_t tw[6];                      // -T' fragments
-  s16x8_t tb[3];                      // this wave's three of the six T'' fragments (3 pk .. 3 pk + 2)
+  s16x8_t tw[6];                      // the six T'' fragments (scaled into -T' by k_stage)
   s16x8_t vec;                        // the lane's 16 bytes of the record vec block
 };
 
@@ -997,9 +998,7 @@ template <int D>
 __device__ __forceinline__ void k_prefetch_tw(KPrefetch<D>& p, const uint8_t* rec, int pk, int lane) {
   const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
-  for (int j = 0; j < 6; ++j) p.tw[j] = buf_ld(r, 16 * lane, Rec::TW + 1024 * j);
-#pragma unroll
-  for (int j = 0; j < 3; ++j) p.tb[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * (3 * pk + j));
+  for (int j = 0; j < 6; ++j) p.tw[j] = buf_ld(r, 16 * lane, Rec::TB + 1024 * j);
 }
 
 // V rows past the sequence end re-read its last token: those tokens carry
@@ -1047,8 +1046,36 @@ __device__ __forceinline__ void k_stage(KPrefetch<D>& p, StateStage<D>& S, int p
   constexpr int KS = D / 16;
   constexpr int NKT = KPrefetch<D>::NKT;
   *reinterpret_cast<s16x8_t*>(reinterpret_cast<uint8_t*>(S.vec) + 16 * lane) = p.vec;
+  // this wave's three of the six T'' fragments into the stage, as they are
+  if (pk == 0) {
 #pragma unroll
-  for (int j = 0; j < 3; ++j) S.Tb[3 * pk + j][lane] = as_h8(p.tb[j]);
+    for (int j = 0; j < 3; ++j) S.Tb[j][lane] = as_h8(p.tw[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) S.Tb[3 + j][lane] = as_h8(p.tw[j + 3]);
+  }
+  // -T' = T'' diag(cT): lane group g's element e of k-step ks is token
+  // 16 ks + 4 g + e (e < 4) or 16 ks + 8 + 4 g + e - 4, whose cT this wave
+  // has just written to the stage's vec block (its own LDS writes, in order)
+  {
+    const int g = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const float4 fa = *reinterpret_cast<const float4*>(&S.vec[Rec::CT + 16 * ks + 4 * g]);
+      const float4 fb = *reinterpret_cast<const float4*>(&S.vec[Rec::CT + 16 * ks + 8 + 4 * g]);
+      const float f[8] = {fa.x, fa.y, fa.z, fa.w, fb.x, fb.y, fb.z, fb.w};
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        if (jj == 0 && ks >= 2) continue;     // (row tile 0 has k-steps 0..1 only)
+        const int j = jj == 0 ? ks : ks + 2;
+        const h16x8_t t8 = as_h8(p.tw[j]);
+        h16x8_t w8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w8[e] = static_cast<_Float16>(static_cast<float>(t8[e]) * f[e]);
+        p.tw[j] = __builtin_bit_cast(s16x8_t, w8);
+      }
+    }
+  }
   f32x16_t cw[NKT][2];
 #pragma unroll
   for (int u = 0; u < NKT; ++u) {
