@@ -1025,14 +1025,16 @@ __device__ __forceinline__ void q_prefetch(QPrefetch<D>& p, const uint8_t* rec, 
   for (int s = 0; s < D / 16; ++s) p.q[s] = buf_ld(r, 16 * lane, Rec::QP + 1024 * (nt * (D / 16) + s));
 }
 
-// four fragments for either tile (tile 0 uses the first two), so every path
-// issues the same loads
-__device__ __forceinline__ void a_prefetch(APrefetch& p, const uint8_t* rec, int nt, int lane) {
+// the fragments of token tile NT: key steps 0..1 for tile 0, 0..3 for tile 1
+// (the output role is compiled per tile, so each path's loads are exact)
+template <int NT>
+__device__ __forceinline__ void a_prefetch(APrefetch& p, const uint8_t* rec, int lane) {
+  constexpr int NA = NT ? 4 : 2;
   const __amdgpu_buffer_rsrc_t r = buf_rsrc(rec);
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) p.a[ks] = buf_ld(r, 16 * lane, Rec::AQ + 1024 * (2 * nt + ks));
+  for (int ks = 0; ks < NA; ++ks) p.a[ks] = buf_ld(r, 16 * lane, Rec::AQ + 1024 * (2 * NT + ks));
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) p.al[ks] = buf_ld(r, 16 * lane, Rec::AL + 1024 * (2 * nt + ks));
+  for (int ks = 0; ks < NA; ++ks) p.al[ks] = buf_ld(r, 16 * lane, Rec::AL + 1024 * (2 * NT + ks));
 }
 
 // K waves: K^T and -W of key tiles pk (+ 2) into the stage, as fragments.
@@ -1217,46 +1219,34 @@ __device__ __forceinline__ void o_inter(QPrefetch<D>& p, const uint8_t* next, co
 
 // Output waves, second half (the interval after): acc += Vn^T A^T as
 // Vh A + Vl A + Vh A_lo (o_intra), then the bf16 tile goes out (o_store).
-// The A registers are reloaded after all of the products (a_prefetch): the
-// masked copies of fragments 2 and 3 leave no registers for loads in between.
-template <int NC>
-__device__ __forceinline__ void o_intra(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[NC], int nt,
-                                        int lane) {
-  h16x8_t vh[NC][4], vl[NC][4];
+// The A registers are reloaded after all of the products (a_prefetch).  Token
+// tile 0 has A entries at token steps 0 and 1 only, tile 1 at 0..3; the role
+// is compiled per tile (NT), so neither loads nor multiplies what is zero.
+template <int NC, int NT>
+__device__ __forceinline__ void o_intra(const APrefetch& p, const StateXchgV& X, f32x16_t (&acc)[NC], int lane) {
+  constexpr int NS = NT ? 4 : 2;
+  h16x8_t vh[NC][NS], vl[NC][NS];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NS; ++s) {
       vh[c][s] = X.Vh[c][s][lane];
       vl[c][s] = X.Vl[c][s][lane];
     }
   __builtin_amdgcn_sched_barrier(0);
-  // Tile 0 has no A entries at token steps 2 and 3; the fragments loaded there
-  // (tile 1's, so that both tiles issue the same loads) are masked to zero.
-  // Every product then runs on every path, and no loaded register is left
-  // unread.
-  const uint32_t keep_hi = nt ? 0xffffffffu : 0u;
-  h16x8_t af[4], alf[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const u32x4_t x = __builtin_bit_cast(u32x4_t, p.a[s]);
-    const u32x4_t y = __builtin_bit_cast(u32x4_t, p.al[s]);
-    af[s] = __builtin_bit_cast(h16x8_t, s < 2 ? x : (x & keep_hi));
-    alf[s] = __builtin_bit_cast(h16x8_t, s < 2 ? y : (y & keep_hi));
-  }
   // the residual products, then the rounded one
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < NS; ++s)
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vl[c][s], af[s], acc[c]);
+    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vl[c][s], as_h8(p.a[s]), acc[c]);
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < NS; ++s)
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vh[c][s], alf[s], acc[c]);
+    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vh[c][s], as_h8(p.al[s]), acc[c]);
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < NS; ++s)
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vh[c][s], af[s], acc[c]);
+    for (int c = 0; c < NC; ++c) acc[c] = mfma32(vh[c][s], as_h8(p.a[s]), acc[c]);
 }
 
 // The C tiles give each lane 4 columns of a row per store; rows go out whole
@@ -1688,8 +1678,9 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
     // ------------------------------------------------------------ output --
     // (NC: the workgroup's 32-column tiles, a compile-time count for the
     // accumulators)
-    auto output_role = [&](auto nc_tag) {
+    auto output_role = [&](auto nc_tag, auto nt_tag) {
       constexpr int NC = decltype(nc_tag)::value;
+      constexpr int NT = decltype(nt_tag)::value;  // the wave's token tile
       // In the interval of chunk c (between workgroup barriers c and c + 1)
       // an output wave finishes chunk c - 1 (Vn^T A^T, the store) and runs
       // S^T Q'^T of chunk c.  Chunk c's Q' fragments live in register set
@@ -1699,8 +1690,10 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       // stay exact for that, so no load may look younger than it is: every
       // path issues the same loads (past the last chunk they repeat it), the
       // sets go out oldest first, and the loop has a single exit (two chunks
-      // per trip, the odd one after it).
-      const int nt = wave - 2;
+      // per trip, the odd one after it).  Each tile's role is compiled on its
+      // own, so the A loads (two fragment pairs for tile 0, four for tile 1)
+      // are exact on each path.
+      constexpr int nt = NT;
       uint16_t* oh = o + (bos * Hv + h) * D + col0;
       const int64_t ostride = static_cast<int64_t>(kC) * Hv * D;
       QPrefetch<D> q0, q1;
@@ -1709,11 +1702,11 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       const uint8_t* rec1 = rec0 + min<int64_t>(1, nch - 1) * rec_stride;
       q_prefetch<D>(q0, rec0, nt, lane);
       gdn::keep_loads_here();  // the sets go out oldest first, as in the loop
-      a_prefetch(a0, rec0, nt, lane);
+      a_prefetch<NT>(a0, rec0, lane);
       gdn::keep_loads_here();
       q_prefetch<D>(q1, rec1, nt, lane);
       gdn::keep_loads_here();
-      a_prefetch(a1, rec1, nt, lane);
+      a_prefetch<NT>(a1, rec1, lane);
       gdn::keep_loads_here();
       gdn::lds_barrier();
       // The conv-state roll, in interval 0: the U waves have read the old v
@@ -1726,9 +1719,9 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       gdn::keep_loads_here();
       gdn::lds_barrier();
 #define GDN_OITER(jj, QC, AP)                                                                               \
-  o_intra<NC>(AP, sm.xv[((jj) - 1) & 1], acc, nt, lane);                                                   \
+  o_intra<NC, NT>(AP, sm.xv[((jj) - 1) & 1], acc, lane);                                                   \
   __builtin_amdgcn_sched_barrier(0);                                                                        \
-  a_prefetch(AP, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, nt, lane);                            \
+  a_prefetch<NT>(AP, rec0 + min<int64_t>((jj) + 1, nch - 1) * rec_stride, lane);                            \
   gdn::keep_loads_here();                                                                                   \
   o_store<NC>(acc, sm.ot[nt], oh + ((jj) - 1) * ostride, kC, Hv, D, nt, lane);                              \
   o_inter<D, NC>(QC, rec0 + min<int64_t>((jj) + 2, nch - 1) * rec_stride, sm.xs, &sm.sflag[0][0], jj, nt, lane, \
@@ -1745,16 +1738,20 @@ __global__ __launch_bounds__(64 * kStateWaves) void chunk_state_kernel(
       }
 #undef GDN_OITER
       if ((nch - 1) & 1)
-        o_intra<NC>(a1, sm.xv[1], acc, nt, lane);
+        o_intra<NC, NT>(a1, sm.xv[1], acc, lane);
       else
-        o_intra<NC>(a0, sm.xv[0], acc, nt, lane);
+        o_intra<NC, NT>(a0, sm.xv[0], acc, lane);
       o_store<NC>(acc, sm.ot[nt], oh + (nch - 1) * ostride, GDN_LEN(nch - 1), Hv, D, nt, lane);
     };
     if (wave < 4) {
-      if (!kMix || nc == 2)
-        output_role(NcTag<2>{});
+      if ((!kMix || nc == 2) && wave == 2)
+        output_role(NcTag<2>{}, NcTag<0>{});
+      else if (!kMix || nc == 2)
+        output_role(NcTag<2>{}, NcTag<1>{});
+      else if (wave == 2)
+        output_role(NcTag<1>{}, NcTag<0>{});
       else
-        output_role(NcTag<1>{});
+        output_role(NcTag<1>{}, NcTag<1>{});
 #undef GDN_ROLL
     } else {
       // ------------------------------------------------------------ U and K --
